@@ -1,0 +1,186 @@
+"""The reference tests' case lists for the int8 path, restated as data, plus the data each case runs on.
+
+Every list cites the reference test it restates (tests/RecursiveAI.OneGpu.Kernels.Tests/...); the data comes from the
+oracle's restatement of the same generators, so a case here holds the same bytes as the reference test's case.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+import oracle
+
+# Int8Tests.cs:9-21 (ModelShapes): BERT and MiniLM projections at 128 tokens, batch 1 and 8.
+MODEL_SHAPES = [
+    ("minilm qkv/proj b1x128", 128, 384, 384),
+    ("minilm ffn-up b1x128", 128, 1536, 384),
+    ("minilm ffn-down b1x128", 128, 384, 1536),
+    ("bert proj b1x128", 128, 768, 768),
+    ("bert ffn-up b1x128", 128, 3072, 768),
+    ("bert ffn-down b1x128", 128, 768, 3072),
+    ("minilm ffn-up b8x128", 1024, 1536, 384),
+    ("bert proj b8x128", 1024, 768, 768),
+    ("bert ffn-up b8x128", 1024, 3072, 768),
+    ("bert ffn-down b8x128", 1024, 768, 3072),
+]
+
+# Int8Tests.cs:219 (EdgeShapesAreBitExact shapes).
+EDGE_SHAPES = [(1, 1, 1), (1, 1, 0), (3, 5, 7), (64, 64, 16), (65, 63, 17), (1, 257, 33), (130, 1, 31), (17, 129, 1),
+               (2, 2, 4096), (33, 31, 300), (4, 4, 32), (7, 9, 31), (40, 40, 65), (5, 3, 63), (33, 40, 96)]
+
+
+def problem(m, n, k, batch=1, trans_b=False, off_a=0, off_b=0, off_c=0, lda_extra=0, ldb_extra=0, share_b=False):
+    """Int8Tests.Problem (Int8Tests.cs:196-210)."""
+    p = oracle.Gemm(m, n, k, Batch=batch, TransposeB=trans_b, OffsetA=off_a, OffsetB=off_b, OffsetC=off_c)
+    p.Lda = k + lda_extra
+    p.Ldb = (k if trans_b else n) + ldb_extra
+    p.StrideA = m * p.Lda
+    p.StrideB = 0 if share_b else (n if trans_b else k) * p.Ldb
+    if batch == 1:
+        p.StrideA = 0
+        p.StrideB = 0
+    return p
+
+
+@dataclass
+class Case:
+    """Int8Tests.Case (Int8Tests.cs:99-106): signedness, zero-point modes (0 none, 1 scalar, 2 vector), extreme fill."""
+
+    name: str
+    p: oracle.Gemm
+    a_signed: bool
+    b_signed: bool
+    za_mode: int
+    zb_mode: int
+    fill: int = -1
+    data: dict = field(default_factory=dict)
+
+
+def edge_cases() -> list[Case]:
+    """Every case of EdgeShapesAreBitExact (Int8Tests.cs:214-270), in the reference's order."""
+    cases = []
+    for (m, n, k) in EDGE_SHAPES:
+        for s in range(4):
+            for za in range(3):
+                zb = (za + s) % 3
+                cases.append(Case(f"{m}x{n}x{k}", problem(m, n, k, off_a=za, off_b=1 + zb, off_c=s),
+                                  (s & 1) != 0, (s & 2) != 0, za, zb))
+    cases.append(Case("transposed B", problem(40, 70, 50, trans_b=True, off_a=3, off_b=1), False, True, 1, 2))
+    cases.append(Case("padded rows", problem(21, 22, 23, lda_extra=5, ldb_extra=3, off_a=2, off_b=3), True, True, 2, 1))
+    cases.append(Case("batch 5 shared B", problem(9, 70, 33, batch=5, share_b=True, off_a=1, off_b=2), False, True, 1, 2))
+    cases.append(Case("batch 3", problem(70, 9, 33, batch=3, off_a=3, off_b=1, off_c=3), False, False, 2, 1))
+    for fill in (0x00, 0x7F, 0x80, 0xFF):
+        for s in range(4):
+            cases.append(Case(f"extreme {fill:02X}", problem(37, 41, 77, trans_b=(s & 1) != 0), (s & 1) != 0,
+                              (s & 2) != 0, 1 + (s & 1), 2 - (s & 1), fill))
+    for fill in (0x00, 0x7F, 0x80, 0xFF):
+        for s in range(4):
+            for (m, n, k) in ((33, 35, 4096), (3, 70, 4096), (65, 64, 1024)):
+                cases.append(Case(f"long extreme {fill:02X} {m}x{n}x{k}", problem(m, n, k, trans_b=(s & 1) != 0),
+                                  (s & 1) != 0, (s & 2) != 0, (s + fill) % 3, (s + 1) % 3, fill))
+    return cases
+
+
+def model_case(name, m, n, k) -> Case:
+    """ModelShapesAreBitExact (Int8Tests.cs:285-317): u8 activations with a scalar zero point, int8 weights stored N x K."""
+    return Case(name, problem(m, n, k, trans_b=True), False, True, 1, 0)
+
+
+def case_data(c: Case, seed: int) -> dict:
+    """The buffers of RunInt32 (Int8Tests.cs:118-133): raw bytes of A, B and the zero points, extremes filled."""
+    p = c.p
+    lda = p.Lda if p.Lda else p.K
+    ldb = p.Ldb if p.Ldb else (p.K if p.TransposeB else p.N)
+    len_a = p.OffsetA + (p.Batch - 1) * p.StrideA + p.M * lda + 4
+    len_b = p.OffsetB + (p.Batch - 1) * p.StrideB + (p.N if p.TransposeB else p.K) * ldb + 4
+    a = oracle.bytes_(len_a, seed)
+    b = oracle.bytes_(len_b, seed + 1)
+    za = None if c.za_mode == 0 else oracle.bytes_(1 + (p.M if c.za_mode == 2 else 0), seed + 2)
+    zb = None if c.zb_mode == 0 else oracle.bytes_(1 + (p.N if c.zb_mode == 2 else 0), seed + 3)
+    if c.fill >= 0:
+        a[:] = c.fill
+        b[:] = c.fill ^ 0xFF
+        if za is not None:
+            za[:] = c.fill
+        if zb is not None:
+            zb[:] = c.fill ^ 0x80
+    return {"a": a, "b": b, "za": za, "zb": zb}
+
+
+def reference_sums(c: Case, d: dict) -> np.ndarray:
+    """The oracle's definition-form sums for a case (dense Batch*M*N int32)."""
+    za = None if d["za"] is None else (d["za"], c.za_mode == 2, 0)
+    zb = None if d["zb"] is None else (d["zb"], c.zb_mode == 2, 0)
+    return oracle.int8_gemm(c.p, d["a"], c.a_signed, d["b"], c.b_signed, za, zb)
+
+
+# Int8Tests.cs:626 (DynamicQuantizeIsBitExact counts) and the seven input kinds of 638-646.
+DQ_COUNTS = [1, 2, 3, 255, 256, 257, 1023, 1024, 1025, 4097, 128 * 384, 128 * 768, 1024 * 768, 1024 * 384 + 17,
+             262144 + 3]
+DQ_KINDS = [0, 1, 2, 3, 4, 5, 6]
+
+
+def dq_cases():
+    """(count, kind, seed) in the reference's order: seed counts up from 1 across counts x kinds."""
+    seed = 1
+    for count in DQ_COUNTS:
+        for kind in DQ_KINDS:
+            yield count, kind, seed
+            seed += 1
+
+
+# DequantizeTests.cs:93-97 and 263-267: (shape, axis, perAxis).
+DEQUANT_SHAPES = [
+    ([1], 0, False), ([7], 0, True), ([5, 6], 0, True), ([5, 6], 1, True), ([5, 6], -1, False), ([2, 3, 4, 5], 1, True),
+    ([2, 3, 4, 5], -1, True), ([1031, 3], 0, True), ([3, 257], 1, True), ([4, 1, 9], 2, True), ([100003], 0, False),
+    ([384, 768], 1, True),
+]
+
+# DequantizeTests.cs:270: the scale sets of QuantizeIsExact.
+QUANT_SCALE_SETS = [[0.5], [1.0], [0.0137, 0.25, 3.3], [1.0 / 255.0, 0.09999], [1e-6, 1e3, 0.7]]
+
+
+def axis_split(shape, axis, per_axis):
+    """(count, axisLen, inner) as DequantizeKernels.Encode splits the tensor (DequantizeKernels.cs:93-107)."""
+    count = int(np.prod(shape)) if shape else 1
+    if not per_axis:
+        return count, 1, 1
+    ax = axis + len(shape) if axis < 0 else axis
+    inner = int(np.prod(shape[ax + 1:])) if ax + 1 < len(shape) else 1
+    return count, shape[ax], inner
+
+
+# FloatAndRequantizedFormsAreBitExact (Int8Tests.cs:468-501).
+FLOAT_SHAPES = [(1, 1, 1), (5, 7, 9), (64, 65, 100), (130, 70, 384), (128, 384, 384), (33, 257, 77)]
+REQUANT_OUT = [(True, 128), (False, 0), (True, 0), (False, -5), (True, 255), (False, 127)]
+
+# RequantizationRoundsHalfToEvenAndSaturates (Int8Tests.cs:503-547): (multiplier, zeroY, unsigned).
+REQUANT_TIES = [(0.5, 10, True), (0.5, -10, False), (2.5, 0, True), (1e9, 3, True), (-1e9, 3, False),
+                (float("nan"), 5, True), (float("nan"), 5, False), (float("inf"), 1, False), (0.0, 7, True)]
+
+
+def float_case_data(m, n, k, scale_vec, seed):
+    """FloatCase inputs (Int8Tests.cs:334-373): u8 A with scalar zp, int8 B with per-column zp, scales and biases."""
+    a = oracle.bytes_(m * k + 4, seed)
+    b = oracle.bytes_(k * n + 4, seed + 1)
+    za = oracle.bytes_(1, seed + 2)
+    zb = oracle.bytes_(n, seed + 3)
+    i = np.arange(max(n if scale_vec else 1, 1))
+    scale = (np.float32(0.0007) + ((i * 37 + seed) % 101).astype(np.float32) * np.float32(1.3e-5)).astype(np.float32)
+    cols = np.arange(n)
+    ib = (((cols * 7919) % 20001) - 10000).astype(np.int32)
+    fb = ((((cols * 31) % 201) - 100).astype(np.float32) * np.float32(0.0137)).astype(np.float32)
+    return a, b, za, zb, scale, ib, fb
+
+
+def requant_case_data(m, n, k, mult_vec, seed):
+    """RequantCase inputs (Int8Tests.cs:375-399)."""
+    a = oracle.bytes_(m * k + 4, seed)
+    b = oracle.bytes_(k * n + 4, seed + 1)
+    za = oracle.bytes_(1, seed + 2)
+    i = np.arange(n if mult_vec else 1)
+    mult = (np.float32(0.00011) + ((i * 13 + seed) % 59).astype(np.float32) * np.float32(2.7e-6)).astype(np.float32)
+    cols = np.arange(n)
+    ib = (((cols * 6007) % 4001) - 2000).astype(np.int32)
+    return a, b, za, mult, ib

@@ -1,0 +1,286 @@
+"""Pins the CPU oracle before anything is compared with it (CPU only).
+
+The reference ships no golden vectors for this path (its tests compute their expectations on the fly in C#), so the
+oracle is pinned by: the reference's closed forms, brute force / library routines that compute the same mathematics
+independently (numpy int64 matmul, IEEE float32 arithmetic, numpy's float16 cast, np.rint), the signed-domain identity
+agreeing with the definition form, and the reference kernel's own integer division agreeing with IEEE division.
+tests/test_oracle_mutants.py shows each pin catches a planted mistake.
+"""
+import numpy as np
+import pytest
+
+import cases
+import oracle
+
+
+# ------------------------------------------------------------------ int32 sums
+
+def numpy_sums(p, a, a_signed, b, b_signed, za=None, zb=None):
+    """C[b, m, n] = sum_k (A - za)(B - zb) by numpy int64 matmul, wrapped to int32."""
+    lda = p.Lda or p.K
+    ldb = p.Ldb or (p.K if p.TransposeB else p.N)
+    av = a.view(np.int8).astype(np.int64) if a_signed else a.astype(np.int64)
+    bv = b.view(np.int8).astype(np.int64) if b_signed else b.astype(np.int64)
+    out = np.zeros((p.Batch, p.M, p.N), np.int64)
+    for bt in range(p.Batch):
+        ia = p.OffsetA + bt * p.StrideA + np.arange(p.M)[:, None] * lda + np.arange(p.K)[None, :]
+        A = av[ia] if p.K else np.zeros((p.M, 0), np.int64)
+        if p.TransposeB:
+            ib = p.OffsetB + bt * p.StrideB + np.arange(p.N)[:, None] * ldb + np.arange(p.K)[None, :]
+            B = bv[ib].T if p.K else np.zeros((0, p.N), np.int64)
+        else:
+            ib = p.OffsetB + bt * p.StrideB + np.arange(p.K)[:, None] * ldb + np.arange(p.N)[None, :]
+            B = bv[ib] if p.K else np.zeros((0, p.N), np.int64)
+        if za is not None:
+            zbuf, zvec, zoff = za
+            zv = zbuf.view(np.int8).astype(np.int64) if a_signed else zbuf.astype(np.int64)
+            A = A - (zv[zoff:zoff + p.M][:, None] if zvec else zv[zoff])
+        if zb is not None:
+            zbuf, zvec, zoff = zb
+            zv = zbuf.view(np.int8).astype(np.int64) if b_signed else zbuf.astype(np.int64)
+            B = B - (zv[zoff:zoff + p.N][None, :] if zvec else zv[zoff])
+        out[bt] = A @ B
+    return ((out + 2**31) % 2**32 - 2**31).astype(np.int32).ravel()
+
+
+def test_closed_form_matches_the_reference():
+    # MultiDeviceTests.cs:30-31, 53-55: [[1 2], [3 4]] x [[1 -1 2], [-2 3 -3]] = [[-3 5 -4], [-5 9 -6]]
+    p = oracle.Gemm(2, 3, 2)
+    a = np.array([1, 2, 3, 4], np.uint8)
+    b = np.array([1, -1, 2, -2, 3, -3], np.int8).view(np.uint8)
+    want = [-3, 5, -4, -5, 9, -6]
+    assert oracle.int8_gemm(p, a, False, b, True).tolist() == want
+    assert oracle.int8_gemm_identity(p, a, False, b, True).tolist() == want
+
+
+def test_edge_cases_definition_equals_numpy_and_identity():
+    # Every EdgeShapesAreBitExact case (Int8Tests.cs:214-270), with its own data.
+    for i, c in enumerate(cases.edge_cases()):
+        d = cases.case_data(c, i + 1)
+        za = None if d["za"] is None else (d["za"], c.za_mode == 2, 0)
+        zb = None if d["zb"] is None else (d["zb"], c.zb_mode == 2, 0)
+        got = oracle.int8_gemm(c.p, d["a"], c.a_signed, d["b"], c.b_signed, za, zb)
+        np.testing.assert_array_equal(got, numpy_sums(c.p, d["a"], c.a_signed, d["b"], c.b_signed, za, zb), err_msg=c.name)
+        np.testing.assert_array_equal(got, oracle.int8_gemm_identity(c.p, d["a"], c.a_signed, d["b"], c.b_signed, za, zb),
+                                      err_msg=c.name)
+
+
+def test_sums_wrap_modulo_2_32():
+    # K = 40000 at the extremes: |sum| reaches 2.6e9 > 2^31, so the int32 result must wrap like two's complement.
+    k = 40000
+    p = oracle.Gemm(2, 3, k)
+    a = np.full(2 * k, 0x00, np.uint8)
+    b = np.full(k * 3, 0xFF, np.uint8)
+    za = (np.array([255], np.uint8), False, 0)
+    got = oracle.int8_gemm(p, a, False, b, False, za)
+    want = numpy_sums(p, a, False, b, False, za)
+    assert abs(-255 * 255 * k) > 2**31
+    np.testing.assert_array_equal(got, want)
+    np.testing.assert_array_equal(got, oracle.int8_gemm_identity(p, a, False, b, False, za))
+
+
+def test_sampled_rows_equal_full_product():
+    c = cases.model_case("minilm qkv/proj b1x128", 128, 384, 384)
+    d = cases.case_data(c, 3)
+    full = cases.reference_sums(c, d).reshape(128, 384)
+    rows = np.array([0, 5, 77, 127])
+    got = oracle.int8_gemm_rows(c.p, d["a"], False, d["b"], True, rows, (d["za"], False, 0))
+    np.testing.assert_array_equal(got, full[rows])
+
+
+# ------------------------------------------------------------------ float and requantized forms
+
+def test_float_epilogue_is_two_float32_roundings():
+    rng = np.random.default_rng(0)
+    sums = rng.integers(-2**31, 2**31, 5000, dtype=np.int64).astype(np.int32)
+    n = 50
+    scale = rng.uniform(1e-5, 1e-2, n).astype(np.float32)
+    ib = rng.integers(-10000, 10000, n).astype(np.int32)
+    fb = rng.uniform(-2, 2, n).astype(np.float32)
+    got = oracle.float_epilogue(sums, n, scale, True, ib, fb)
+    cols = np.arange(sums.size) % n
+    acc = ((sums.astype(np.int64) + ib[cols] + 2**31) % 2**32 - 2**31).astype(np.int32)
+    want = (acc.astype(np.float32) * scale[cols]).astype(np.float32) + fb[cols]
+    np.testing.assert_array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
+    # Without biases, scalar scale.
+    got = oracle.float_epilogue(sums, n, scale[:1], False)
+    np.testing.assert_array_equal(got.view(np.uint32), (sums.astype(np.float32) * scale[0]).view(np.uint32))
+
+
+def _requant_numpy(acc, mult, zero, unsigned):
+    lo, hi = (0, 255) if unsigned else (-128, 127)
+    v = np.float32(acc) * np.float32(mult)
+    if np.isnan(v):
+        return lo
+    r = np.rint(v)
+    r = min(max(r, np.float32(lo - zero)), np.float32(hi - zero))
+    return int(r) + zero
+
+
+def test_requant_ties_and_saturation():
+    # RequantizationRoundsHalfToEvenAndSaturates (Int8Tests.cs:503-547), plus explicit tie expectations.
+    for mult, zero, unsigned in cases.REQUANT_TIES:
+        for av in range(-9, 10):
+            with np.errstate(invalid="ignore", over="ignore"):
+                assert oracle.requant(av, mult, zero, unsigned) == _requant_numpy(av, mult, zero, unsigned)
+    assert oracle.requant(5, 0.5, 0, True) == 2      # 2.5 -> 2 (half to even)
+    assert oracle.requant(7, 0.5, 0, True) == 4      # 3.5 -> 4
+    assert oracle.requant(-5, 0.5, 0, False) == -2   # -2.5 -> -2
+    assert oracle.requant(1, 1e9, 3, True) == 255
+    assert oracle.requant(1, float("nan"), 5, False) == -128
+
+
+# ------------------------------------------------------------------ DynamicQuantizeLinear
+
+def dq_numpy(x):
+    """DynamicQuantizeLinear from numpy float32 arithmetic (IEEE division, np.rint half-to-even)."""
+    x = np.asarray(x, np.float32)
+    ok = ~np.isnan(x)
+    mn = x[ok].min() if ok.any() else np.float32(np.inf)
+    mx = x[ok].max() if ok.any() else np.float32(-np.inf)
+    lo = mn if mn <= 0 else np.float32(0)
+    hi = mx if mx > 0 else np.float32(0)
+    with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
+        scale = np.float32(hi - lo) / np.float32(255)
+        zp = 0
+        if scale != 0 and np.isfinite(scale):
+            z = np.rint(np.float32(0) - np.float32(lo / scale))
+            zp = 0 if z < 0 else (255 if z > 255 else int(z))
+        if scale == 0:
+            return np.zeros(x.size, np.uint8), np.float32(1), 0
+        v = np.rint(x / scale).astype(np.float32) + np.float32(zp)
+        y = np.where(np.isnan(v), 0, np.clip(v, 0, 255)).astype(np.uint8)
+    return y, scale, zp
+
+
+def test_dynamic_quantize_matches_numpy_on_reference_cases():
+    # All 105 tensors of DynamicQuantizeIsBitExact (Int8Tests.cs:617-703).
+    for count, kind, seed in cases.dq_cases():
+        x = oracle.dq_input(count, seed, kind)
+        y, s, z = oracle.dynamic_quantize(x)
+        wy, ws, wz = dq_numpy(x)
+        assert np.float32(s).view(np.uint32) == np.float32(ws).view(np.uint32), (count, kind)
+        assert z == wz, (count, kind)
+        np.testing.assert_array_equal(y, wy, err_msg=f"{count} {kind}")
+
+
+def test_dynamic_quantize_special_inputs():
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    for x in ([0.0], [-0.0, 0.0], [nan, nan], [1.0, nan, -1.0], [inf, 1.0], [-inf, 2.0], [1e-42, 3e-42], [-1e-42],
+              [1e30, -1e30], [255.0, 0.0], [-3.0, -2.0]):
+        x = np.array(x, np.float32)
+        y, s, z = oracle.dynamic_quantize(x)
+        wy, ws, wz = dq_numpy(x)
+        assert (np.isnan(s) and np.isnan(ws)) or np.float32(s).view(np.uint32) == np.float32(ws).view(np.uint32), x
+        assert z == wz, x
+        np.testing.assert_array_equal(y, wy, err_msg=str(x))
+    # Closed forms: [0, 255] -> scale 1, zp 0, y = x; all zero -> (1, 0).
+    y, s, z = oracle.dynamic_quantize(np.array([0, 255, 17], np.float32))
+    assert (s, z, y.tolist()) == (1.0, 0, [0, 255, 17])
+    assert oracle.dynamic_quantize(np.zeros(5, np.float32))[1:] == (1.0, 0)
+
+
+def test_div_exact_equals_ieee_division():
+    # The reference kernel's integer long division (DivExact.hlsli) equals IEEE float32 division on the quantizer's
+    # operands: the scale computations and every x / scale of the DQ cases, plus random and edge operands.
+    rng = np.random.default_rng(1)
+    xs = [rng.standard_normal(20000).astype(np.float32) * np.float32(10) ** rng.integers(-40, 38, 20000).astype(np.float32),
+          oracle.quantize_input(5000, 3, True), oracle.dq_input(5000, 7, 3)]
+    ss = [np.float32(1 / 255), np.float32(0.0137), np.float32(3.3), np.float32(1e-6), np.float32(1e3),
+          np.float32(4.7 * 2 / 255), np.float32(1e-44), np.float32(7e37)]
+    count = 0
+    with np.errstate(all="ignore"):
+        for x in np.concatenate(xs):
+            for s in ss:
+                got = oracle.div_exact(float(x), float(s))
+                want = np.float32(x) / s
+                assert (np.isnan(got) and np.isnan(want)) or got.view(np.uint32) == np.float32(want).view(np.uint32), (x, s)
+                count += 1
+    assert count > 200000
+
+
+# ------------------------------------------------------------------ (de)quantize
+
+def test_f2h_equals_numpy_float16_rounding():
+    rng = np.random.default_rng(2)
+    # Every half value and its float32 neighbours (ties in between), random bit patterns, the overflow edge.
+    halves = np.arange(0, 65536, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32)
+    halves = halves[np.isfinite(halves)]
+    bits = halves.view(np.uint32)
+    probes = np.concatenate([bits, bits + 1, bits - 1, bits + 0x1000, bits + 0xFFF, bits + 0x1001,
+                             rng.integers(0, 2**32, 200000, dtype=np.uint64).astype(np.uint32),
+                             np.array([0x477FEFFF, 0x477FF000, 0x7F800000, 0xFF800000, 0x7FC00000, 0x33000000, 0x33000001],
+                                      np.uint32)]).view(np.float32)
+    lib = oracle.lib()
+    got = np.array([lib.ora_f2h(float(f)) for f in probes], np.uint16)
+    want = probes.astype(np.float16).view(np.uint16)
+    nan = np.isnan(probes)
+    np.testing.assert_array_equal(got[~nan], want[~nan])
+    assert np.all((got[nan] & 0x7C00) == 0x7C00) and np.all((got[nan] & 0x3FF) != 0)
+
+
+def test_h2f_equals_numpy_for_every_half():
+    lib = oracle.lib()
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = np.array([lib.ora_h2f(int(v)) for v in h], np.float32)
+    want = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    np.testing.assert_array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    assert np.all(np.isnan(got[nan]))
+
+
+@pytest.mark.parametrize("kind", [np.uint8, np.int8, np.int32])
+def test_dequantize_equals_numpy(kind):
+    seed = 7
+    for shape, axis, per_axis in cases.DEQUANT_SHAPES:
+        count, axis_len, inner = cases.axis_split(shape, axis, per_axis)
+        if kind == np.int32:
+            x = oracle.dequant_input_i32(count, seed)
+            z = oracle.dequant_input_i32(axis_len, seed + 2)
+        else:
+            x = oracle.dequant_input_bytes(count, seed).view(kind)
+            z = oracle.dequant_input_bytes(axis_len, seed + 2).view(kind)
+        scale = oracle.rig_random(axis_len, seed + 1, 0.001, 2.0)
+        for zero in (z, None):
+            got = oracle.dequantize(x, scale, per_axis, axis_len, inner, zero)
+            a = (np.arange(count) // inner) % axis_len if per_axis else np.zeros(count, np.int64)
+            zp = zero[a].astype(np.int64) if zero is not None else 0
+            d = ((x.astype(np.int64) - zp + 2**31) % 2**32 - 2**31).astype(np.int32)
+            want = d.astype(np.float32) * scale[a]
+            np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+            got16 = oracle.dequantize(x, scale, per_axis, axis_len, inner, zero, f16_out=True)
+            np.testing.assert_array_equal(got16, want.astype(np.float16).view(np.uint16))
+        seed += 3
+
+
+def test_quantize_equals_numpy():
+    seed = 1
+    for shape, axis, per_axis in cases.DEQUANT_SHAPES:
+        count, axis_len, inner = cases.axis_split(shape, axis, per_axis)
+        for scales in cases.QUANT_SCALE_SETS:
+            x = oracle.quantize_input(count, seed, True)
+            scale = np.array([scales[i % len(scales)] for i in range(axis_len)], np.float32)
+            for signed in (False, True):
+                zero = oracle.dequant_input_bytes(axis_len, seed + 2)
+                for zp in (zero, None):
+                    got = oracle.quantize(x, scale, signed, per_axis, axis_len, inner, zp)
+                    a = (np.arange(count) // inner) % axis_len if per_axis else np.zeros(count, np.int64)
+                    z = 0 if zp is None else (zp.view(np.int8) if signed else zp).astype(np.float32)[a]
+                    with np.errstate(all="ignore"):
+                        v = np.rint(x / scale[a]).astype(np.float32) + np.float32(z) if zp is None else \
+                            np.rint(x / scale[a]).astype(np.float32) + z
+                    lo, hi = (-128, 127) if signed else (0, 255)
+                    want = np.where(np.isnan(v), lo, np.clip(v, lo, hi)).astype(np.int64).astype(np.uint8)
+                    np.testing.assert_array_equal(got, want, err_msg=f"{shape} {axis} {scales} {signed}")
+            seed += 1
+
+
+def test_generators_are_deterministic_and_in_range():
+    a = oracle.bytes_(1000, 5)
+    assert np.array_equal(a, oracle.bytes_(1000, 5)) and not np.array_equal(a, oracle.bytes_(1000, 6))
+    r = oracle.rig_random(1000, 3, -3.0, 5.0)
+    assert r.min() >= -3.0 and r.max() < 5.0
+    u = oracle.synth_uniform_i32(100000, 4, 1, 100, 156)
+    assert u.min() == 100 and u.max() == 156
+    g = oracle.synth_normal_f32(200000, 1, 0, 0.0, 1.0)
+    assert abs(float(g.mean())) < 0.01 and abs(float(g.std()) - 1.0) < 0.01
