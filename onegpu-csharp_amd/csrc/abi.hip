@@ -1,0 +1,646 @@
+// The C ABI of libonegpu_hip.so (include/onegpu_hip.h): contexts, buffers, timing, and the validated entry points of
+// the int8 path. Validation restates the reference's host-side checks (Int8Gemm.Prepare / CheckRange / CheckVector,
+// Int8Gemm.cs:393-501; Check.Range / RangeBytes, KernelSupport.cs:75-110) in terms of byte sizes, so a caller that
+// skipped them still cannot make a kernel read or write outside its buffers.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "og_internal.hpp"
+
+struct og_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    og::Workspace ws{};
+    std::string error;
+    std::string argument;
+    const char *last_kernel = "";
+    std::string name;
+    uint32_t compute_units = 0;
+    uint32_t lds_bytes = 0;
+    uint64_t max_buffer = 0;
+    // timing
+    bool timing = false;
+    int timing_max = 0;
+    int timing_n = 0;
+    std::vector<hipEvent_t> ev_start, ev_stop;
+    std::vector<const char *> ev_name;
+};
+
+namespace {
+
+thread_local std::string t_error;
+thread_local std::string t_argument;
+
+constexpr uint64_t kInitialPartialBytes = 32ull << 20;
+
+int fail(og_ctx *ctx, int status, const char *argument, const char *fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (ctx) {
+        ctx->error = buf;
+        ctx->argument = argument ? argument : "";
+    }
+    t_error = buf;
+    t_argument = argument ? argument : "";
+    return status;
+}
+
+int ok(og_ctx *ctx)
+{
+    if (ctx) {
+        ctx->error.clear();
+        ctx->argument.clear();
+    }
+    return OG_OK;
+}
+
+int hip_status(og_ctx *ctx, hipError_t e, const char *what)
+{
+    if (e == hipSuccess) return OG_OK;
+    int st = OG_ERR_LAUNCH_FAILED;
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) st = OG_ERR_OUT_OF_MEMORY;
+    else if (e == hipErrorNoDevice || e == hipErrorInvalidDevice) st = OG_ERR_NO_DEVICE;
+    else if (e == hipErrorLaunchFailure || e == hipErrorIllegalAddress || e == hipErrorECCNotCorrectable) st = OG_ERR_DEVICE_LOST;
+    return fail(ctx, st, nullptr, "%s: %s (%s)", what, hipGetErrorString(e), hipGetErrorName(e));
+}
+
+// Brackets one kernel launch with timing events when timing is on.
+template <typename F>
+int launch(og_ctx *ctx, const char *what, F &&f)
+{
+    const char *name = "";
+    bool timed = ctx->timing && ctx->timing_n < ctx->timing_max;
+    if (timed) (void)hipEventRecord(ctx->ev_start[ctx->timing_n], ctx->stream);
+    hipError_t e = f(&name);
+    ctx->last_kernel = name;
+    if (timed) {
+        (void)hipEventRecord(ctx->ev_stop[ctx->timing_n], ctx->stream);
+        ctx->ev_name[ctx->timing_n] = name;
+        ctx->timing_n++;
+    }
+    return hip_status(ctx, e, what);
+}
+
+bool fits(uint64_t offset_bytes, uint64_t extent_bytes, const og_buffer &b)
+{
+    return offset_bytes <= b.bytes && extent_bytes <= b.bytes - offset_bytes;
+}
+
+int ensure_partials(og_ctx *ctx, uint64_t bytes)
+{
+    if (bytes <= ctx->ws.partial_bytes) return OG_OK;
+    // Grow geometrically, outside any launch; the old region may still be in use by recorded work, so wait first.
+    uint64_t size = ctx->ws.partial_bytes * 2 > bytes ? ctx->ws.partial_bytes * 2 : bytes;
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_status(ctx, e, "workspace");
+    if (ctx->ws.partials) (void)hipFree(ctx->ws.partials);
+    ctx->ws.partials = nullptr;
+    ctx->ws.partial_bytes = 0;
+    e = hipMalloc(&ctx->ws.partials, size);
+    if (e != hipSuccess) return hip_status(ctx, e, "workspace");
+    ctx->ws.partial_bytes = size;
+    return OG_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *og_version(void) { return "onegpu-hip 0.1 (gfx950)"; }
+
+const char *og_last_error(og_ctx *ctx) { return ctx ? ctx->error.c_str() : t_error.c_str(); }
+
+const char *og_last_error_argument(og_ctx *ctx) { return ctx ? ctx->argument.c_str() : t_argument.c_str(); }
+
+const char *og_last_kernel(og_ctx *ctx) { return ctx ? ctx->last_kernel : ""; }
+
+int og_device_count(int *count)
+{
+    if (!count) return fail(nullptr, OG_ERR_INVALID_ARG, "count", "null pointer");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    *count = e == hipSuccess ? n : 0;
+    return OG_OK;
+}
+
+int og_init(int device_ordinal, og_ctx **out)
+{
+    if (!out) return fail(nullptr, OG_ERR_INVALID_ARG, "out", "null pointer");
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail(nullptr, OG_ERR_NO_DEVICE, nullptr, "no HIP device");
+    if (device_ordinal < 0 || device_ordinal >= n)
+        return fail(nullptr, OG_ERR_INVALID_ARG, "device_ordinal", "device %d of %d", device_ordinal, n);
+    og_ctx *ctx = new og_ctx();
+    ctx->device = device_ordinal;
+    hipError_t e = hipSetDevice(device_ordinal);
+    hipDeviceProp_t prop{};
+    if (e == hipSuccess) e = hipGetDeviceProperties(&prop, device_ordinal);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipMalloc(&ctx->ws.partials, kInitialPartialBytes);
+    if (e == hipSuccess) {
+        ctx->ws.partial_bytes = kInitialPartialBytes;
+        void *p = nullptr;
+        // ranges (2 * kDqMaxGroups floats), counter, result (2 floats), in one allocation
+        size_t bytes = 2 * og::kDqMaxGroups * sizeof(float) + 256 + 256;
+        e = hipMalloc(&p, bytes);
+        if (e == hipSuccess) e = hipMemset(p, 0, bytes);
+        if (e == hipSuccess) {
+            ctx->ws.dq_ranges = static_cast<float *>(p);
+            ctx->ws.dq_counter = reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(p) + 2 * og::kDqMaxGroups * sizeof(float));
+            ctx->ws.dq_result = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(ctx->ws.dq_counter) + 256);
+        }
+    }
+    if (e != hipSuccess) {
+        int st = hip_status(nullptr, e, "og_init");
+        og_destroy(ctx);
+        return st;
+    }
+    ctx->name = prop.name;
+    if (prop.gcnArchName[0]) ctx->name += std::string(" (") + prop.gcnArchName + ")";
+    ctx->compute_units = (uint32_t)prop.multiProcessorCount;
+    ctx->lds_bytes = (uint32_t)prop.sharedMemPerBlock;
+    ctx->max_buffer = (uint64_t)prop.totalGlobalMem;
+    *out = ctx;
+    return OG_OK;
+}
+
+int og_destroy(og_ctx *ctx)
+{
+    if (!ctx) return OG_OK;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    for (auto e : ctx->ev_start) (void)hipEventDestroy(e);
+    for (auto e : ctx->ev_stop) (void)hipEventDestroy(e);
+    if (ctx->ws.partials) (void)hipFree(ctx->ws.partials);
+    if (ctx->ws.dq_ranges) (void)hipFree(ctx->ws.dq_ranges);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return OG_OK;
+}
+
+int og_device_name(og_ctx *ctx, char *buf, size_t len)
+{
+    if (!ctx || !buf || len == 0) return fail(ctx, OG_ERR_INVALID_ARG, "buf", "null context or buffer");
+    snprintf(buf, len, "%s", ctx->name.c_str());
+    return ok(ctx);
+}
+
+int og_device_limits(og_ctx *ctx, uint64_t *max_buffer_bytes, uint32_t *compute_units, uint32_t *lds_bytes)
+{
+    if (!ctx) return fail(ctx, OG_ERR_INVALID_ARG, "ctx", "null context");
+    if (max_buffer_bytes) *max_buffer_bytes = ctx->max_buffer;
+    if (compute_units) *compute_units = ctx->compute_units;
+    if (lds_bytes) *lds_bytes = ctx->lds_bytes;
+    return ok(ctx);
+}
+
+int og_stream(og_ctx *ctx, void **hip_stream)
+{
+    if (!ctx || !hip_stream) return fail(ctx, OG_ERR_INVALID_ARG, "hip_stream", "null context or pointer");
+    *hip_stream = ctx->stream;
+    return ok(ctx);
+}
+
+int og_sync(og_ctx *ctx)
+{
+    if (!ctx) return fail(ctx, OG_ERR_INVALID_ARG, "ctx", "null context");
+    (void)hipSetDevice(ctx->device);
+    int st = hip_status(ctx, hipStreamSynchronize(ctx->stream), "og_sync");
+    return st == OG_OK ? ok(ctx) : st;
+}
+
+int og_alloc(og_ctx *ctx, uint64_t bytes, void **dptr)
+{
+    if (!ctx || !dptr) return fail(ctx, OG_ERR_INVALID_ARG, "dptr", "null context or pointer");
+    *dptr = nullptr;
+    (void)hipSetDevice(ctx->device);
+    hipError_t e = hipMalloc(dptr, bytes ? bytes : 4);
+    if (e != hipSuccess) return fail(ctx, OG_ERR_OUT_OF_MEMORY, "bytes", "hipMalloc of %llu bytes: %s", (unsigned long long)bytes, hipGetErrorString(e));
+    return ok(ctx);
+}
+
+int og_free(og_ctx *ctx, void *dptr)
+{
+    if (!ctx) return fail(ctx, OG_ERR_INVALID_ARG, "ctx", "null context");
+    if (!dptr) return ok(ctx);
+    (void)hipSetDevice(ctx->device);
+    // The buffer may still be named by recorded work: wait for the stream before releasing it.
+    (void)hipStreamSynchronize(ctx->stream);
+    int st = hip_status(ctx, hipFree(dptr), "og_free");
+    return st == OG_OK ? ok(ctx) : st;
+}
+
+static int copy(og_ctx *ctx, void *dst, const void *src, uint64_t bytes, hipMemcpyKind kind, bool wait)
+{
+    if (!ctx) return fail(ctx, OG_ERR_INVALID_ARG, "ctx", "null context");
+    if (bytes == 0) return ok(ctx);
+    if (!dst || !src) return fail(ctx, OG_ERR_INVALID_ARG, dst ? "src" : "dst", "null pointer");
+    (void)hipSetDevice(ctx->device);
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, kind, ctx->stream);
+    if (e == hipSuccess && wait) e = hipStreamSynchronize(ctx->stream);
+    int st = hip_status(ctx, e, "og_memcpy");
+    return st == OG_OK ? ok(ctx) : st;
+}
+
+int og_memcpy_h2d(og_ctx *ctx, void *dst, const void *src, uint64_t bytes) { return copy(ctx, dst, src, bytes, hipMemcpyHostToDevice, true); }
+int og_memcpy_d2h(og_ctx *ctx, void *dst, const void *src, uint64_t bytes) { return copy(ctx, dst, src, bytes, hipMemcpyDeviceToHost, true); }
+int og_memcpy_d2d(og_ctx *ctx, void *dst, const void *src, uint64_t bytes) { return copy(ctx, dst, src, bytes, hipMemcpyDeviceToDevice, false); }
+
+int og_fill_bytes(og_ctx *ctx, void *dst, uint8_t value, uint64_t bytes)
+{
+    if (!ctx) return fail(ctx, OG_ERR_INVALID_ARG, "ctx", "null context");
+    if (bytes && !dst) return fail(ctx, OG_ERR_INVALID_ARG, "dst", "null pointer");
+    (void)hipSetDevice(ctx->device);
+    int st = launch(ctx, "og_fill_bytes", [&](const char **k) { *k = "fill-bytes"; return og::launch_fill_bytes(dst, value, bytes, ctx->stream); });
+    return st == OG_OK ? ok(ctx) : st;
+}
+
+// ------------------------------------------------------------------ timing
+
+int og_timing_begin(og_ctx *ctx, int max_dispatches)
+{
+    if (!ctx) return fail(ctx, OG_ERR_INVALID_ARG, "ctx", "null context");
+    if (max_dispatches < 1) return fail(ctx, OG_ERR_INVALID_ARG, "max_dispatches", "must be at least 1, got %d", max_dispatches);
+    (void)hipSetDevice(ctx->device);
+    while ((int)ctx->ev_start.size() < max_dispatches) {
+        hipEvent_t a, b;
+        if (hipEventCreate(&a) != hipSuccess) return fail(ctx, OG_ERR_OUT_OF_MEMORY, nullptr, "hipEventCreate");
+        if (hipEventCreate(&b) != hipSuccess) { (void)hipEventDestroy(a); return fail(ctx, OG_ERR_OUT_OF_MEMORY, nullptr, "hipEventCreate"); }
+        ctx->ev_start.push_back(a);
+        ctx->ev_stop.push_back(b);
+        ctx->ev_name.push_back("");
+    }
+    ctx->timing = true;
+    ctx->timing_max = max_dispatches;
+    ctx->timing_n = 0;
+    return ok(ctx);
+}
+
+int og_timing_end(og_ctx *ctx, int *dispatches)
+{
+    if (!ctx) return fail(ctx, OG_ERR_INVALID_ARG, "ctx", "null context");
+    ctx->timing = false;
+    if (dispatches) *dispatches = ctx->timing_n;
+    return ok(ctx);
+}
+
+int og_timing_read(og_ctx *ctx, int index, float *ms, const char **kernel_name)
+{
+    if (!ctx) return fail(ctx, OG_ERR_INVALID_ARG, "ctx", "null context");
+    if (index < 0 || index >= ctx->timing_n) return fail(ctx, OG_ERR_INVALID_ARG, "index", "%d outside the %d timed dispatches", index, ctx->timing_n);
+    (void)hipSetDevice(ctx->device);
+    hipError_t e = hipEventSynchronize(ctx->ev_stop[index]);
+    float t = 0.0f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&t, ctx->ev_start[index], ctx->ev_stop[index]);
+    if (e != hipSuccess) return hip_status(ctx, e, "og_timing_read");
+    if (ms) *ms = t;
+    if (kernel_name) *kernel_name = ctx->ev_name[index];
+    return ok(ctx);
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------ Int8Gemm
+
+namespace og {
+
+GemmKernel choose_gemm_kernel(int32_t M, int32_t N, int32_t K, int32_t batch, uint32_t flags)
+{
+    (void)N;
+    (void)batch;
+    if (flags & OG_GEMM_PORTABLE) return GemmKernel::Portable;
+    const bool trans_b = flags & OG_GEMM_TRANSPOSE_B;
+    // Few rows against weights stored K x N: stream B once (the reference's row kernel regime, Int8Gemm.cs:562-563).
+    if (!trans_b && M <= 16 && K > 0 && !(flags & OG_GEMM_NO_SKINNY)) {
+        if (skinny_slices(M, N, K, batch) <= 1 && !(flags & OG_GEMM_NO_DIRECT)) return GemmKernel::SkinnyDirect;
+        return GemmKernel::Skinny;
+    }
+    return GemmKernel::Tiled;
+}
+
+const char *gemm_kernel_name(GemmKernel k)
+{
+    switch (k) {
+    case GemmKernel::Portable: return "portable-tile64x64x16";
+    case GemmKernel::Skinny: return "mfma-i8-rows16-splitk";
+    case GemmKernel::SkinnyDirect: return "mfma-i8-rows16-direct";
+    default: return "mfma-i8-tile128x128x64";
+    }
+}
+
+}  // namespace og
+
+extern "C" {
+
+static const uint32_t kKnownGemmFlags = 0x7Fu | 0x380u | OG_GEMM_PORTABLE | OG_GEMM_NO_SKINNY | OG_GEMM_NO_DIRECT;
+
+// Checks the parameter block alone; returns OG_OK or the failing status (message and argument set).
+static int check_gemm_params(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch)
+{
+    if (!p) return fail(ctx, OG_ERR_INVALID_ARG, "params", "null parameter block");
+    const uint32_t imax = 0x7FFFFFFFu;
+    if (p->M > imax) return fail(ctx, OG_ERR_INVALID_ARG, "M", "must not be negative, got %d", (int32_t)p->M);
+    if (p->N > imax) return fail(ctx, OG_ERR_INVALID_ARG, "N", "must not be negative, got %d", (int32_t)p->N);
+    if (p->K > imax) return fail(ctx, OG_ERR_INVALID_ARG, "K", "must not be negative, got %d", (int32_t)p->K);
+    if (batch < 1 || batch > imax) return fail(ctx, OG_ERR_INVALID_ARG, "Batch", "must be at least 1, got %d", (int32_t)batch);
+    if (p->Flags & ~kKnownGemmFlags) return fail(ctx, OG_ERR_INVALID_ARG, "Flags", "unknown flag bits 0x%x", p->Flags & ~kKnownGemmFlags);
+    if ((p->Flags & OG_GEMM_ZA_PER_ROW) && !(p->Flags & OG_GEMM_ZA)) return fail(ctx, OG_ERR_INVALID_ARG, "Flags", "per-row zero point without a zero point");
+    if ((p->Flags & OG_GEMM_ZB_PER_COL) && !(p->Flags & OG_GEMM_ZB)) return fail(ctx, OG_ERR_INVALID_ARG, "Flags", "per-column zero point without a zero point");
+    if (p->Epi & ~0xFu) return fail(ctx, OG_ERR_INVALID_ARG, "Epi", "unknown epilogue bits 0x%x", p->Epi & ~0xFu);
+    if ((p->Epi & (OG_EPI_SCALE_PER_COL | OG_EPI_FLOAT_BIAS)) && !(p->Epi & OG_EPI_FLOAT))
+        return fail(ctx, OG_ERR_INVALID_ARG, "Epi", "a scale or float bias needs the float result bit");
+    const bool trans_b = p->Flags & OG_GEMM_TRANSPOSE_B;
+    const uint64_t lda = p->Lda ? p->Lda : (p->K ? p->K : 1);
+    const uint64_t cols_b = trans_b ? p->K : p->N;
+    const uint64_t ldb = p->Ldb ? p->Ldb : (cols_b ? cols_b : 1);
+    if (lda > imax || lda < p->K) return fail(ctx, OG_ERR_INVALID_ARG, "Lda", "%llu is smaller than K = %u", (unsigned long long)lda, p->K);
+    if (ldb > imax || ldb < cols_b) return fail(ctx, OG_ERR_INVALID_ARG, "Ldb", "%llu is smaller than the stored row length %llu", (unsigned long long)ldb, (unsigned long long)cols_b);
+    if ((uint64_t)batch * p->M * p->N > imax) return fail(ctx, OG_ERR_INVALID_ARG, "Batch", "the result holds more elements than the kernels address");
+    if (p->M > 0 && p->N > 0 && p->StrideC < (uint64_t)p->M * p->N && batch > 1)
+        return fail(ctx, OG_ERR_INVALID_ARG, "StrideC", "%u is smaller than M * N", p->StrideC);
+    return OG_OK;
+}
+
+int og_int8_gemm_kernel_name(const og_int8_gemm_params *p, uint32_t batch, char *buf, size_t len)
+{
+    if (!p || !buf || len == 0) return fail(nullptr, OG_ERR_INVALID_ARG, "params", "null pointer");
+    og::GemmKernel k = og::choose_gemm_kernel((int32_t)p->M, (int32_t)p->N, (int32_t)p->K, (int32_t)(batch ? batch : 1), p->Flags);
+    snprintf(buf, len, "%s", og::gemm_kernel_name(k));
+    return OG_OK;
+}
+
+int og_int8_gemm(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_buffer A, og_buffer B, og_buffer C,
+                 og_buffer ZA, og_buffer ZB, og_buffer bias, og_buffer scale, og_buffer fbias)
+{
+    int st = check_gemm_params(ctx, p, batch);
+    if (st != OG_OK) return st;
+    const bool trans_b = p->Flags & OG_GEMM_TRANSPOSE_B;
+    const uint64_t M = p->M, N = p->N, K = p->K;
+    const uint64_t lda = p->Lda ? p->Lda : (K ? K : 1);
+    const uint64_t rows_b = trans_b ? N : K, cols_b = trans_b ? K : N;
+    const uint64_t ldb = p->Ldb ? p->Ldb : (cols_b ? cols_b : 1);
+    const uint64_t stride_c = batch > 1 ? p->StrideC : M * N;
+    // Operand ranges (Int8Gemm.CheckRange: the last byte an operand reaches lies inside its buffer).
+    if (M > 0 && N > 0 && K > 0) {
+        if (!A.ptr) return fail(ctx, OG_ERR_INVALID_ARG, "a", "A is missing");
+        if (!B.ptr) return fail(ctx, OG_ERR_INVALID_ARG, "b", "B is missing");
+        uint64_t last_a = p->OffA + (uint64_t)(batch - 1) * p->StrideA + (M - 1) * lda + (K - 1);
+        if (last_a >= A.bytes) return fail(ctx, OG_ERR_INVALID_ARG, "OffsetA", "operand A reaches byte %llu but its buffer holds %llu", (unsigned long long)last_a, (unsigned long long)A.bytes);
+        uint64_t last_b = p->OffB + (uint64_t)(batch - 1) * p->StrideB + (rows_b - 1) * ldb + (cols_b - 1);
+        if (last_b >= B.bytes) return fail(ctx, OG_ERR_INVALID_ARG, "OffsetB", "operand B reaches byte %llu but its buffer holds %llu", (unsigned long long)last_b, (unsigned long long)B.bytes);
+    }
+    const uint64_t count_c = M * N ? (uint64_t)(batch - 1) * stride_c + M * N : 0;
+    if (M > 0 && N > 0) {
+        if (!C.ptr) return fail(ctx, OG_ERR_INVALID_ARG, "c", "C is missing");
+        if (((uintptr_t)C.ptr & 3) != 0) return fail(ctx, OG_ERR_INVALID_ARG, "c", "C is not 4-byte aligned");
+        if (!fits((uint64_t)p->OffC * 4, count_c * 4, C)) return fail(ctx, OG_ERR_INVALID_ARG, "c", "elements %u..%llu reach past the buffer of %llu", p->OffC, (unsigned long long)(p->OffC + count_c), (unsigned long long)(C.bytes / 4));
+    }
+    const bool has_za = p->Flags & OG_GEMM_ZA, has_zb = p->Flags & OG_GEMM_ZB;
+    if (has_za) {
+        uint64_t n = (p->Flags & OG_GEMM_ZA_PER_ROW) ? M : 1;
+        if (!ZA.ptr) return fail(ctx, OG_ERR_INVALID_ARG, "zpA", "the zero point of A is missing");
+        if (!fits(p->OffZA, n, ZA)) return fail(ctx, OG_ERR_INVALID_ARG, "zpA", "elements %u..%llu reach past the buffer of %llu", p->OffZA, (unsigned long long)(p->OffZA + n), (unsigned long long)ZA.bytes);
+    }
+    if (has_zb) {
+        uint64_t n = (p->Flags & OG_GEMM_ZB_PER_COL) ? N : 1;
+        if (!ZB.ptr) return fail(ctx, OG_ERR_INVALID_ARG, "zpB", "the zero point of B is missing");
+        if (!fits(p->OffZB, n, ZB)) return fail(ctx, OG_ERR_INVALID_ARG, "zpB", "elements %u..%llu reach past the buffer of %llu", p->OffZB, (unsigned long long)(p->OffZB + n), (unsigned long long)ZB.bytes);
+    }
+    if (p->Epi & OG_EPI_INT_BIAS) {
+        if (!bias.ptr || ((uintptr_t)bias.ptr & 3)) return fail(ctx, OG_ERR_INVALID_ARG, "bias", "the int32 bias is missing or misaligned");
+        if (!fits((uint64_t)p->OffBias * 4, N * 4, bias)) return fail(ctx, OG_ERR_INVALID_ARG, "bias", "elements %u..%llu reach past the buffer of %llu", p->OffBias, (unsigned long long)(p->OffBias + N), (unsigned long long)(bias.bytes / 4));
+    }
+    if (p->Epi & OG_EPI_FLOAT) {
+        uint64_t n = (p->Epi & OG_EPI_SCALE_PER_COL) ? N : 1;
+        if (!scale.ptr || ((uintptr_t)scale.ptr & 3)) return fail(ctx, OG_ERR_INVALID_ARG, "scale", "the scale is missing or misaligned");
+        if (!fits((uint64_t)p->OffScale * 4, n * 4, scale)) return fail(ctx, OG_ERR_INVALID_ARG, "scale", "elements %u..%llu reach past the buffer of %llu", p->OffScale, (unsigned long long)(p->OffScale + n), (unsigned long long)(scale.bytes / 4));
+    }
+    if (p->Epi & OG_EPI_FLOAT_BIAS) {
+        if (!fbias.ptr || ((uintptr_t)fbias.ptr & 3)) return fail(ctx, OG_ERR_INVALID_ARG, "floatBias", "the float bias is missing or misaligned");
+        if (!fits((uint64_t)p->OffFBias * 4, N * 4, fbias)) return fail(ctx, OG_ERR_INVALID_ARG, "floatBias", "elements %u..%llu reach past the buffer of %llu", p->OffFBias, (unsigned long long)(p->OffFBias + N), (unsigned long long)(fbias.bytes / 4));
+    }
+    if (!ctx) return fail(ctx, OG_ERR_NO_DEVICE, "ctx", "no context: the arguments are valid but there is no device to run on");
+    if (M == 0 || N == 0) return ok(ctx);
+
+    og::GemmArgs g{};
+    g.A = static_cast<const uint8_t *>(A.ptr) + p->OffA;
+    g.B = static_cast<const uint8_t *>(B.ptr) + p->OffB;
+    g.C = static_cast<uint8_t *>(C.ptr) + (uint64_t)p->OffC * 4;
+    g.ZA = has_za ? static_cast<const uint8_t *>(ZA.ptr) + p->OffZA : nullptr;
+    g.ZB = has_zb ? static_cast<const uint8_t *>(ZB.ptr) + p->OffZB : nullptr;
+    g.bias = (p->Epi & OG_EPI_INT_BIAS) ? static_cast<const int32_t *>(bias.ptr) + p->OffBias : nullptr;
+    g.scale = (p->Epi & OG_EPI_FLOAT) ? static_cast<const float *>(scale.ptr) + p->OffScale : nullptr;
+    g.fbias = (p->Epi & OG_EPI_FLOAT_BIAS) ? static_cast<const float *>(fbias.ptr) + p->OffFBias : nullptr;
+    g.strideA = p->StrideA;
+    g.strideB = p->StrideB;
+    g.strideC = (int64_t)stride_c;
+    g.M = (int32_t)M;
+    g.N = (int32_t)N;
+    g.K = (int32_t)K;
+    g.batch = (int32_t)batch;
+    g.lda = (int32_t)lda;
+    g.ldb = (int32_t)ldb;
+    g.flags = p->Flags;
+    g.epi = p->Epi;
+
+    (void)hipSetDevice(ctx->device);
+    og::GemmKernel k = og::choose_gemm_kernel(g.M, g.N, g.K, g.batch, g.flags);
+    switch (k) {
+    case og::GemmKernel::Portable:
+        st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_portable(g, ctx->stream, n); });
+        break;
+    case og::GemmKernel::Tiled:
+        st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_tiled(g, ctx->stream, n); });
+        break;
+    case og::GemmKernel::SkinnyDirect:
+        st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_skinny(g, ctx->ws, ctx->stream, n, 0); });
+        break;
+    case og::GemmKernel::Skinny:
+        st = ensure_partials(ctx, og::skinny_workspace_bytes(g.M, g.N, g.K, g.batch));
+        if (st != OG_OK) return st;
+        st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_skinny(g, ctx->ws, ctx->stream, n, 0); });
+        if (st == OG_OK)
+            st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_skinny(g, ctx->ws, ctx->stream, n, 1); });
+        break;
+    }
+    return st == OG_OK ? ok(ctx) : st;
+}
+
+int og_int8_epilogue(og_ctx *ctx, const og_int8_epilogue_params *p, og_buffer acc, og_buffer out, og_buffer bias,
+                     og_buffer scale, og_buffer fbias)
+{
+    if (!p) return fail(ctx, OG_ERR_INVALID_ARG, "params", "null parameter block");
+    if (p->Mode > 3) return fail(ctx, OG_ERR_INVALID_ARG, "Mode", "unknown mode %u", p->Mode);
+    if (p->Count > 0x7FFFFFFFu) return fail(ctx, OG_ERR_INVALID_ARG, "Count", "too many elements");
+    if (p->Count > 0 && p->N == 0) return fail(ctx, OG_ERR_INVALID_ARG, "N", "must be at least 1");
+    const uint64_t cnt = p->Count, n = p->N;
+    const bool byte_out = p->Mode == 2;
+    if (p->Mode != 3) {
+        if (cnt && (!acc.ptr || ((uintptr_t)acc.ptr & 3))) return fail(ctx, OG_ERR_INVALID_ARG, "scratch", "the int32 sums are missing or misaligned");
+        if (cnt && !fits((uint64_t)p->OffAcc * 4, cnt * 4, acc)) return fail(ctx, OG_ERR_INVALID_ARG, "scratch", "elements %u..%llu reach past the buffer", p->OffAcc, (unsigned long long)(p->OffAcc + cnt));
+    }
+    if (cnt && (!out.ptr || (!byte_out && ((uintptr_t)out.ptr & 3)))) return fail(ctx, OG_ERR_INVALID_ARG, "y", "the output is missing or misaligned");
+    if (cnt && !fits((uint64_t)p->OffOut * (byte_out ? 1 : 4), cnt * (byte_out ? 1 : 4), out)) return fail(ctx, OG_ERR_INVALID_ARG, "y", "elements %u..%llu reach past the buffer", p->OffOut, (unsigned long long)(p->OffOut + cnt));
+    if ((p->Flags & 1u) && p->Mode != 3 && cnt && !fits((uint64_t)p->OffBias * 4, n * 4, bias)) return fail(ctx, OG_ERR_INVALID_ARG, "intBias", "the bias does not cover N values");
+    if ((p->Mode == 1 || p->Mode == 2) && cnt && (!scale.ptr || !fits((uint64_t)p->OffScale * 4, ((p->Flags & 2u) ? n : 1) * 4, scale))) return fail(ctx, OG_ERR_INVALID_ARG, "multiplier", "the scale does not cover its values");
+    if (p->Mode == 3 && cnt && (!fbias.ptr || !fits((uint64_t)p->OffFBias * 4, n * 4, fbias))) return fail(ctx, OG_ERR_INVALID_ARG, "floatBias", "the float bias does not cover N values");
+    if (p->Mode == 2) {
+        const bool u8 = p->Flags & 8u;
+        if (p->ZeroPoint < (u8 ? 0 : -128) || p->ZeroPoint > (u8 ? 255 : 127)) return fail(ctx, OG_ERR_INVALID_ARG, "zeroPointY", "%d is outside the output type's range", p->ZeroPoint);
+    }
+    if (!ctx) return fail(ctx, OG_ERR_NO_DEVICE, "ctx", "no context: the arguments are valid but there is no device to run on");
+    og::EpilogueArgs e{};
+    e.acc = acc.ptr ? static_cast<const int32_t *>(acc.ptr) + p->OffAcc : nullptr;
+    e.out = static_cast<uint8_t *>(out.ptr) + (uint64_t)p->OffOut * (byte_out ? 1 : 4);
+    e.bias = (p->Flags & 1u) ? static_cast<const int32_t *>(bias.ptr) + p->OffBias : nullptr;
+    e.scale = scale.ptr ? static_cast<const float *>(scale.ptr) + p->OffScale : nullptr;
+    e.fbias = fbias.ptr ? static_cast<const float *>(fbias.ptr) + p->OffFBias : nullptr;
+    e.count = p->Count;
+    e.n = p->N;
+    e.mode = p->Mode;
+    e.flags = p->Flags;
+    e.zero_point = p->ZeroPoint;
+    e.out_byte_offset = byte_out ? p->OffOut : 0;
+    (void)hipSetDevice(ctx->device);
+    int st = launch(ctx, "og_int8_epilogue", [&](const char **k) { return og::launch_int8_epilogue(e, ctx->stream, k); });
+    return st == OG_OK ? ok(ctx) : st;
+}
+
+// ------------------------------------------------------------------ DynamicQuantizeLinear
+
+int og_dynamic_quantize(og_ctx *ctx, const og_dq_params *p, og_buffer X, og_buffer Y, og_buffer scale, og_buffer zero)
+{
+    if (!p) return fail(ctx, OG_ERR_INVALID_ARG, "params", "null parameter block");
+    if (p->Count < 1 || p->Count > 0x7FFFFFFFu) return fail(ctx, OG_ERR_INVALID_ARG, "count", "count %d must be at least 1", (int32_t)p->Count);
+    if (!X.ptr || ((uintptr_t)X.ptr & 3) || !fits((uint64_t)p->OffX * 4, (uint64_t)p->Count * 4, X)) return fail(ctx, OG_ERR_INVALID_ARG, "x", "elements %u..%llu reach past the buffer", p->OffX, (unsigned long long)p->OffX + p->Count);
+    if (!Y.ptr || !fits(p->OffY, p->Count, Y)) return fail(ctx, OG_ERR_INVALID_ARG, "y", "elements %u..%llu reach past the buffer", p->OffY, (unsigned long long)p->OffY + p->Count);
+    if (!scale.ptr || ((uintptr_t)scale.ptr & 3) || !fits((uint64_t)p->OffScale * 4, 4, scale)) return fail(ctx, OG_ERR_INVALID_ARG, "scale", "element %u reaches past the buffer", p->OffScale);
+    if (!zero.ptr || !fits(p->OffZero, 1, zero)) return fail(ctx, OG_ERR_INVALID_ARG, "zeroPoint", "element %u reaches past the buffer", p->OffZero);
+    if (!ctx) return fail(ctx, OG_ERR_NO_DEVICE, "ctx", "no context: the arguments are valid but there is no device to run on");
+    og::DqArgs d{};
+    d.x = static_cast<const float *>(X.ptr) + p->OffX;
+    d.y = static_cast<uint8_t *>(Y.ptr) + p->OffY;
+    d.scale = static_cast<float *>(scale.ptr) + p->OffScale;
+    d.zero = static_cast<uint8_t *>(zero.ptr) + p->OffZero;
+    d.count = p->Count;
+    (void)hipSetDevice(ctx->device);
+    int st = launch(ctx, "og_dynamic_quantize", [&](const char **k) { return og::launch_dynamic_quantize(d, ctx->ws, ctx->stream, k, 0); });
+    if (st == OG_OK) st = launch(ctx, "og_dynamic_quantize", [&](const char **k) { return og::launch_dynamic_quantize(d, ctx->ws, ctx->stream, k, 1); });
+    return st == OG_OK ? ok(ctx) : st;
+}
+
+// ------------------------------------------------------------------ DequantizeLinear / QuantizeLinear
+
+static int check_axis(og_ctx *ctx, const og_dequant_params *p)
+{
+    if (p->Count > 0x7FFFFFFFu) return fail(ctx, OG_ERR_INVALID_ARG, "shape", "the tensor holds more than 2147483647 elements");
+    if (p->Flags & ~3u) return fail(ctx, OG_ERR_INVALID_ARG, "Flags", "unknown flag bits 0x%x", p->Flags & ~3u);
+    if ((p->Flags & 1u) && (p->AxisLen == 0 || p->Inner == 0) && p->Count) return fail(ctx, OG_ERR_INVALID_ARG, "axis", "per-axis parameters need AxisLen and Inner of at least 1");
+    return OG_OK;
+}
+
+int og_dequantize(og_ctx *ctx, int kind, int f16_out, const og_dequant_params *p, og_buffer X, og_buffer scale,
+                  og_buffer zero, og_buffer out)
+{
+    if (!p) return fail(ctx, OG_ERR_INVALID_ARG, "params", "null parameter block");
+    if (kind < OG_KIND_U8 || kind > OG_KIND_I32) return fail(ctx, OG_ERR_INVALID_ARG, "TIn", "unknown input kind %d", kind);
+    int st = check_axis(ctx, p);
+    if (st != OG_OK) return st;
+    const uint64_t cnt = p->Count, params = (p->Flags & 1u) ? p->AxisLen : 1, esz = kind == OG_KIND_I32 ? 4 : 1;
+    const uint64_t osz = f16_out ? 2 : 4;
+    if (cnt) {
+        if (!X.ptr || (esz == 4 && ((uintptr_t)X.ptr & 3)) || !fits(p->OffX * esz, cnt * esz, X)) return fail(ctx, OG_ERR_INVALID_ARG, "x", "elements %u..%llu reach past the buffer", p->OffX, (unsigned long long)(p->OffX + cnt));
+        if (!scale.ptr || ((uintptr_t)scale.ptr & 3) || !fits((uint64_t)p->OffS * 4, params * 4, scale)) return fail(ctx, OG_ERR_INVALID_ARG, "scale", "elements %u..%llu reach past the buffer", p->OffS, (unsigned long long)(p->OffS + params));
+        if ((p->Flags & 2u) && (!zero.ptr || (esz == 4 && ((uintptr_t)zero.ptr & 3)) || !fits(p->OffZ * esz, params * esz, zero))) return fail(ctx, OG_ERR_INVALID_ARG, "zeroPoint", "elements %u..%llu reach past the buffer", p->OffZ, (unsigned long long)(p->OffZ + params));
+        if (!out.ptr || ((uintptr_t)out.ptr & (osz - 1)) || !fits(p->OffO * osz, cnt * osz, out)) return fail(ctx, OG_ERR_INVALID_ARG, "output", "elements %u..%llu reach past the buffer", p->OffO, (unsigned long long)(p->OffO + cnt));
+    }
+    if (!ctx) return fail(ctx, OG_ERR_NO_DEVICE, "ctx", "no context: the arguments are valid but there is no device to run on");
+    og::DequantArgs d{};
+    d.x = static_cast<const uint8_t *>(X.ptr) + p->OffX * esz;
+    d.scale = static_cast<const float *>(scale.ptr) + p->OffS;
+    d.zero = (p->Flags & 2u) ? static_cast<const uint8_t *>(zero.ptr) + p->OffZ * esz : nullptr;
+    d.out = static_cast<uint8_t *>(out.ptr) + p->OffO * osz;
+    d.count = p->Count;
+    d.axis_len = p->AxisLen ? p->AxisLen : 1;
+    d.inner = p->Inner ? p->Inner : 1;
+    d.per_axis = p->Flags & 1u;
+    d.has_zero = p->Flags & 2u;
+    (void)hipSetDevice(ctx->device);
+    st = launch(ctx, "og_dequantize", [&](const char **k) { return og::launch_dequantize(d, kind, f16_out != 0, ctx->stream, k); });
+    return st == OG_OK ? ok(ctx) : st;
+}
+
+int og_quantize(og_ctx *ctx, int is_signed, int f16_in, const og_dequant_params *p, og_buffer X, og_buffer scale,
+                og_buffer zero, og_buffer out)
+{
+    if (!p) return fail(ctx, OG_ERR_INVALID_ARG, "params", "null parameter block");
+    int st = check_axis(ctx, p);
+    if (st != OG_OK) return st;
+    const uint64_t cnt = p->Count, params = (p->Flags & 1u) ? p->AxisLen : 1, isz = f16_in ? 2 : 4;
+    if (cnt) {
+        if (!X.ptr || ((uintptr_t)X.ptr & (isz - 1)) || !fits(p->OffX * isz, cnt * isz, X)) return fail(ctx, OG_ERR_INVALID_ARG, "x", "elements %u..%llu reach past the buffer", p->OffX, (unsigned long long)(p->OffX + cnt));
+        if (!scale.ptr || ((uintptr_t)scale.ptr & 3) || !fits((uint64_t)p->OffS * 4, params * 4, scale)) return fail(ctx, OG_ERR_INVALID_ARG, "scale", "elements %u..%llu reach past the buffer", p->OffS, (unsigned long long)(p->OffS + params));
+        if ((p->Flags & 2u) && (!zero.ptr || !fits(p->OffZ, params, zero))) return fail(ctx, OG_ERR_INVALID_ARG, "zeroPoint", "elements %u..%llu reach past the buffer", p->OffZ, (unsigned long long)(p->OffZ + params));
+        if (!out.ptr || !fits(p->OffO, cnt, out)) return fail(ctx, OG_ERR_INVALID_ARG, "output", "elements %u..%llu reach past the buffer", p->OffO, (unsigned long long)(p->OffO + cnt));
+    }
+    if (!ctx) return fail(ctx, OG_ERR_NO_DEVICE, "ctx", "no context: the arguments are valid but there is no device to run on");
+    og::DequantArgs d{};
+    d.x = static_cast<const uint8_t *>(X.ptr) + p->OffX * isz;
+    d.scale = static_cast<const float *>(scale.ptr) + p->OffS;
+    d.zero = (p->Flags & 2u) ? static_cast<const uint8_t *>(zero.ptr) + p->OffZ : nullptr;
+    d.out = static_cast<uint8_t *>(out.ptr) + p->OffO;
+    d.count = p->Count;
+    d.axis_len = p->AxisLen ? p->AxisLen : 1;
+    d.inner = p->Inner ? p->Inner : 1;
+    d.per_axis = p->Flags & 1u;
+    d.has_zero = p->Flags & 2u;
+    (void)hipSetDevice(ctx->device);
+    st = launch(ctx, "og_quantize", [&](const char **k) { return og::launch_quantize(d, is_signed != 0, f16_in != 0, ctx->stream, k); });
+    return st == OG_OK ? ok(ctx) : st;
+}
+
+// ------------------------------------------------------------------ utilities
+
+int og_util_synth(og_ctx *ctx, int kind, uint64_t seed, uint32_t tensor, og_buffer out, uint64_t offset, uint64_t count,
+                  double lo, double hi)
+{
+    if (kind < 0 || kind > 2) return fail(ctx, OG_ERR_INVALID_ARG, "kind", "unknown kind %d", kind);
+    const uint64_t esz = kind == 0 ? 1 : 4;
+    if (count && (!out.ptr || ((uintptr_t)out.ptr & (esz - 1)) || !fits(offset * esz, count * esz, out))) return fail(ctx, OG_ERR_INVALID_ARG, "out", "elements reach past the buffer");
+    if (kind != 2 && (lo > hi || lo < -2147483648.0 || hi > 2147483647.0)) return fail(ctx, OG_ERR_INVALID_ARG, "lo", "bad integer range");
+    if (!ctx) return fail(ctx, OG_ERR_NO_DEVICE, "ctx", "no context");
+    (void)hipSetDevice(ctx->device);
+    int st = launch(ctx, "og_util_synth", [&](const char **k) { *k = "synth"; return og::launch_synth(kind, seed, tensor, static_cast<uint8_t *>(out.ptr) + offset * esz, count, lo, hi, ctx->stream); });
+    return st == OG_OK ? ok(ctx) : st;
+}
+
+int og_util_col_absmax_scale(og_ctx *ctx, og_buffer W, uint32_t rows, uint32_t cols, float divisor, og_buffer scale)
+{
+    if ((uint64_t)rows * cols && (!W.ptr || !fits(0, (uint64_t)rows * cols * 4, W))) return fail(ctx, OG_ERR_INVALID_ARG, "W", "the tensor reaches past the buffer");
+    if (cols && (!scale.ptr || !fits(0, (uint64_t)cols * 4, scale))) return fail(ctx, OG_ERR_INVALID_ARG, "scale", "the scales reach past the buffer");
+    if (!ctx) return fail(ctx, OG_ERR_NO_DEVICE, "ctx", "no context");
+    (void)hipSetDevice(ctx->device);
+    int st = launch(ctx, "og_util_col_absmax_scale", [&](const char **k) { *k = "col-absmax-scale"; return og::launch_col_absmax_scale(static_cast<const float *>(W.ptr), rows, cols, divisor, static_cast<float *>(scale.ptr), ctx->stream); });
+    return st == OG_OK ? ok(ctx) : st;
+}
+
+int og_util_scale_product(og_ctx *ctx, og_buffer a, og_buffer b, uint32_t n, og_buffer out)
+{
+    if (n && (!a.ptr || !fits(0, 4, a) || !b.ptr || !fits(0, (uint64_t)n * 4, b) || !out.ptr || !fits(0, (uint64_t)n * 4, out))) return fail(ctx, OG_ERR_INVALID_ARG, "out", "operands do not cover n values");
+    if (!ctx) return fail(ctx, OG_ERR_NO_DEVICE, "ctx", "no context");
+    (void)hipSetDevice(ctx->device);
+    int st = launch(ctx, "og_util_scale_product", [&](const char **k) { *k = "scale-product"; return og::launch_scale_product(static_cast<const float *>(a.ptr), static_cast<const float *>(b.ptr), n, static_cast<float *>(out.ptr), ctx->stream); });
+    return st == OG_OK ? ok(ctx) : st;
+}
+
+}  // extern "C"

@@ -1,0 +1,152 @@
+// Internal declarations shared by the HIP translation units of libonegpu_hip.so: the resolved argument blocks the
+// kernels take, their launchers, and the device helpers common to them. Everything here is gfx950 (CDNA4) code.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "onegpu_hip.h"
+
+namespace og {
+
+// One int8 product after validation: base pointers with the caller's offsets already applied, strides in bytes (A, B)
+// and elements (C), zero points as pointers to their first element (nullptr when absent).
+struct GemmArgs {
+    const uint8_t *A;
+    const uint8_t *B;
+    void *C;
+    const uint8_t *ZA;
+    const uint8_t *ZB;
+    const int32_t *bias;
+    const float *scale;
+    const float *fbias;
+    int64_t strideA, strideB, strideC;
+    int32_t M, N, K, batch;
+    int32_t lda, ldb;
+    uint32_t flags;  // OG_GEMM_*
+    uint32_t epi;    // OG_EPI_*
+};
+
+// Device workspace owned by a context: the split-k partial sums of the few-rows kernel and the dynamic quantizer's
+// per-workgroup ranges, done-counter and result slot. Sized once at og_init; grown (outside any launch) when a larger
+// few-rows product arrives.
+struct Workspace {
+    int32_t *partials;       // split-k partial sums (int32)
+    uint64_t partial_bytes;
+    float *dq_ranges;        // 2 * kDqMaxGroups floats
+    uint32_t *dq_counter;    // one done-counter, reset by the last workgroup
+    float *dq_result;        // scale, zero point (as float) of the last dynamic quantization
+};
+
+constexpr int kDqMaxGroups = 1024;
+
+// Kernel choice for a product, as og_int8_gemm_kernel_name reports it.
+enum class GemmKernel { Portable, Tiled, Skinny, SkinnyDirect };
+GemmKernel choose_gemm_kernel(int32_t M, int32_t N, int32_t K, int32_t batch, uint32_t flags);
+const char *gemm_kernel_name(GemmKernel k);
+
+// Launchers (one per kernel family); each returns the launch status. `kernel` receives the name of the kernel run.
+hipError_t launch_gemm_portable(const GemmArgs &g, hipStream_t s, const char **kernel);
+hipError_t launch_gemm_tiled(const GemmArgs &g, hipStream_t s, const char **kernel);
+// Few rows (M <= 16), B stored K x N: split-k partial sums into ws.partials, then a pass that adds them up, corrects for
+// the zero points and applies the epilogue. `slices` is the split chosen by skinny_slices().
+hipError_t launch_gemm_skinny(const GemmArgs &g, const Workspace &ws, hipStream_t s, const char **kernel, int step);
+int skinny_slices(int32_t M, int32_t N, int32_t K, int32_t batch);
+uint64_t skinny_workspace_bytes(int32_t M, int32_t N, int32_t K, int32_t batch);
+
+struct EpilogueArgs {
+    const int32_t *acc;
+    void *out;
+    const int32_t *bias;
+    const float *scale;
+    const float *fbias;
+    uint32_t count, n, mode, flags;
+    int32_t zero_point;
+    uint32_t out_byte_offset;  // mode 2: byte offset of out within its allocation, for vector stores
+};
+hipError_t launch_int8_epilogue(const EpilogueArgs &e, hipStream_t s, const char **kernel);
+
+struct DqArgs {
+    const float *x;
+    uint8_t *y;
+    float *scale;
+    uint8_t *zero;
+    uint32_t count;
+};
+hipError_t launch_dynamic_quantize(const DqArgs &d, const Workspace &ws, hipStream_t s, const char **kernel, int step);
+
+struct DequantArgs {
+    const void *x;
+    const float *scale;
+    const void *zero;
+    void *out;
+    uint32_t count, axis_len, inner;
+    bool per_axis, has_zero;
+};
+hipError_t launch_dequantize(const DequantArgs &d, int kind, bool f16_out, hipStream_t s, const char **kernel);
+hipError_t launch_quantize(const DequantArgs &d, bool is_signed, bool f16_in, hipStream_t s, const char **kernel);
+
+hipError_t launch_fill_bytes(void *dst, uint8_t value, uint64_t bytes, hipStream_t s);
+hipError_t launch_synth(int kind, uint64_t seed, uint32_t tensor, void *out, uint64_t count, double lo, double hi,
+                        hipStream_t s);
+hipError_t launch_col_absmax_scale(const float *w, uint32_t rows, uint32_t cols, float divisor, float *scale,
+                                   hipStream_t s);
+hipError_t launch_scale_product(const float *a, const float *b, uint32_t n, float *out, hipStream_t s);
+
+// ------------------------------------------------------------------ device helpers
+
+#if defined(__HIPCC__)
+// Four signed bytes times four signed bytes, summed, plus c (v_dot4_i32_i8); no clamping, so the sum wraps.
+__device__ __forceinline__ int32_t dot4(uint32_t a, uint32_t b, int32_t c)
+{
+    return __builtin_amdgcn_sdot4((int32_t)a, (int32_t)b, c, false);
+}
+
+// v_perm_b32: byte i of the result is byte sel[i] of the 8-byte value {hi, lo} (selectors 0-3 pick lo, 4-7 hi).
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
+{
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// 4 x 4 byte transpose: r[i] holds row i (byte j = column j); afterwards c[j] holds column j (byte i = row i).
+__device__ __forceinline__ void transpose4x4(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3, uint32_t &c0,
+                                             uint32_t &c1, uint32_t &c2, uint32_t &c3)
+{
+    uint32_t lo01 = perm(r1, r0, 0x05010400u);  // r0.b0 r1.b0 r0.b1 r1.b1
+    uint32_t hi01 = perm(r1, r0, 0x07030602u);  // r0.b2 r1.b2 r0.b3 r1.b3
+    uint32_t lo23 = perm(r3, r2, 0x05010400u);
+    uint32_t hi23 = perm(r3, r2, 0x07030602u);
+    c0 = perm(lo23, lo01, 0x05040100u);
+    c1 = perm(lo23, lo01, 0x07060302u);
+    c2 = perm(hi23, hi01, 0x05040100u);
+    c3 = perm(hi23, hi01, 0x07060302u);
+}
+
+__device__ __forceinline__ int32_t sext8(uint32_t b) { return (int32_t)(int8_t)(uint8_t)b; }
+
+// The int32 sum as the reference's StoreValue leaves it (Int8GemmEpilogue.hlsli:17-42): the raw sum; + int bias;
+// or fl(fl(float(sum + bias)) * scale), then + float bias as a separate rounding.
+__device__ __forceinline__ void store_value(const GemmArgs &g, int64_t ci, int32_t col, uint32_t sum)
+{
+    uint32_t epi = g.epi;
+    if (epi & OG_EPI_INT_BIAS) sum += (uint32_t)g.bias[col];
+    if (!(epi & OG_EPI_FLOAT)) {
+        static_cast<int32_t *>(g.C)[ci] = (int32_t)sum;
+        return;
+    }
+    float s = g.scale[(epi & OG_EPI_SCALE_PER_COL) ? col : 0];
+    float f = __fmul_rn((float)(int32_t)sum, s);
+    if (epi & OG_EPI_FLOAT_BIAS) f = __fadd_rn(f, g.fbias[col]);
+    static_cast<float *>(g.C)[ci] = f;
+}
+
+// Zero point in the signed domain: an unsigned operand's bytes move by -128 (s = u ^ 0x80), and so does its zero point.
+__device__ __forceinline__ int32_t signed_zero(const uint8_t *z, int32_t idx, bool per, bool is_signed)
+{
+    int32_t v = z ? (is_signed ? sext8(z[per ? idx : 0]) : (int32_t)z[per ? idx : 0]) : 0;
+    return is_signed ? v : v - 128;
+}
+#endif
+
+}  // namespace og

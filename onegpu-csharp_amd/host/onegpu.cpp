@@ -1,0 +1,768 @@
+// Host layer over the C ABI: validation and parameter blocks as the reference's C# families build them.
+#include "onegpu.hpp"
+
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+#include <sstream>
+
+namespace onegpu {
+
+namespace {
+
+std::string fmt_long(int64_t v) { return std::to_string(v); }
+
+}  // namespace
+
+size_t ElementSize(ElementType t)
+{
+    switch (t) {
+    case ElementType::UInt8:
+    case ElementType::Int8: return 1;
+    case ElementType::Float16:
+    case ElementType::UInt16:
+    case ElementType::Int16: return 2;
+    case ElementType::Int64: return 8;
+    default: return 4;
+    }
+}
+
+const char *ElementName(ElementType t)
+{
+    switch (t) {
+    case ElementType::UInt8: return "Byte";
+    case ElementType::Int8: return "SByte";
+    case ElementType::Int32: return "Int32";
+    case ElementType::Float32: return "Single";
+    case ElementType::Float16: return "Half";
+    case ElementType::UInt32: return "UInt32";
+    case ElementType::UInt16: return "UInt16";
+    case ElementType::Int16: return "Int16";
+    default: return "Int64";
+    }
+}
+
+// ------------------------------------------------------------------ status mapping
+
+void ThrowIfFailed(og_ctx *ctx, int status, const std::string &operation)
+{
+    if (status == OG_OK) return;
+    std::string msg = og_last_error(ctx);
+    std::string arg = og_last_error_argument(ctx);
+    switch (status) {
+    case OG_ERR_INVALID_ARG: throw GpuKernelShapeException(operation, arg.empty() ? "arguments" : arg, msg);
+    case OG_ERR_UNSUPPORTED: throw GpuUnsupportedException(operation + ": " + msg);
+    case OG_ERR_OUT_OF_MEMORY: throw GpuOutOfMemoryException(operation + ": " + msg);
+    case OG_ERR_DEVICE_LOST: throw GpuDeviceLostException(operation + ": " + msg);
+    case OG_ERR_NO_DEVICE: throw GpuUnsupportedException(operation + ": " + msg, "Device", "a HIP device", "none");
+    default: throw GpuCommandFailedException(operation + ": " + msg);
+    }
+}
+
+// ------------------------------------------------------------------ buffers
+
+struct GpuBuffer::Impl {
+    std::shared_ptr<GpuDevice> device;  // a buffer keeps its device (and so the context it frees into) alive
+    og_ctx *ctx = nullptr;  // null: host-only buffer
+    void *ptr = nullptr;
+    int length = 0;
+    ElementType type = ElementType::UInt8;
+    uint64_t bytes = 0;  // allocated bytes
+    ~Impl()
+    {
+        if (!ptr) return;
+        if (ctx) og_free(ctx, ptr);
+        else std::free(ptr);
+    }
+};
+
+int GpuBuffer::Length() const { return impl_ ? impl_->length : 0; }
+ElementType GpuBuffer::Type() const { return impl_ ? impl_->type : ElementType::UInt8; }
+uint64_t GpuBuffer::Size() const { return impl_ ? impl_->bytes : 0; }
+void *GpuBuffer::DevicePointer() const { return impl_ ? impl_->ptr : nullptr; }
+og_buffer GpuBuffer::Binding() const { return og_buffer{impl_ ? impl_->ptr : nullptr, impl_ ? impl_->bytes : 0}; }
+
+void GpuBuffer::Write(const void *src, uint64_t bytes, uint64_t byte_offset) const
+{
+    if (!impl_ || !impl_->ptr) throw GpuException("GpuBuffer: disposed");
+    if (byte_offset > impl_->bytes || bytes > impl_->bytes - byte_offset)
+        throw std::out_of_range("GpuBuffer.Write: range past the buffer");
+    if (!bytes) return;
+    if (impl_->ctx) ThrowIfFailed(impl_->ctx, og_memcpy_h2d(impl_->ctx, static_cast<uint8_t *>(impl_->ptr) + byte_offset, src, bytes), "GpuBuffer.Write");
+    else std::memcpy(static_cast<uint8_t *>(impl_->ptr) + byte_offset, src, bytes);
+}
+
+void GpuBuffer::Read(void *dst, uint64_t bytes, uint64_t byte_offset) const
+{
+    if (!impl_ || !impl_->ptr) throw GpuException("GpuBuffer: disposed");
+    if (byte_offset > impl_->bytes || bytes > impl_->bytes - byte_offset)
+        throw std::out_of_range("GpuBuffer.Read: range past the buffer");
+    if (!bytes) return;
+    if (impl_->ctx) ThrowIfFailed(impl_->ctx, og_memcpy_d2h(impl_->ctx, dst, static_cast<uint8_t *>(impl_->ptr) + byte_offset, bytes), "GpuBuffer.Read");
+    else std::memcpy(dst, static_cast<uint8_t *>(impl_->ptr) + byte_offset, bytes);
+}
+
+void GpuBuffer::Dispose() { impl_.reset(); }
+
+// ------------------------------------------------------------------ encoder and device
+
+void GpuCommandEncoder::Record(Command c, std::vector<std::shared_ptr<GpuBuffer::Impl>> keep)
+{
+    if (submitted_) throw GpuException("GpuCommandEncoder: already submitted");
+    commands_.push_back(Entry{std::move(c), std::move(keep)});
+}
+
+void GpuCommandEncoder::BeginPassTiming(int max_passes)
+{
+    if (max_passes < 1) throw std::invalid_argument("BeginPassTiming: max_passes must be at least 1");
+    timing_start_ = (int)commands_.size();
+    timing_stop_ = -1;
+    timing_slots_ = max_passes;
+}
+
+int GpuCommandEncoder::EndPassTiming()
+{
+    if (timing_start_ < 0) return 0;
+    timing_stop_ = (int)commands_.size() - 1;
+    return timing_stop_ - timing_start_ + 1;
+}
+
+std::shared_ptr<GpuDevice> GpuDevice::Create(int ordinal, GpuDeviceOptions options)
+{
+    std::shared_ptr<GpuDevice> d(new GpuDevice());
+    og_ctx *ctx = nullptr;
+    int st = og_init(ordinal, &ctx);
+    if (st != OG_OK) {
+        std::string msg = og_last_error(nullptr);
+        if (st == OG_ERR_NO_DEVICE) throw GpuUnsupportedException("GpuDevice: " + msg, "Device", "a HIP device", "none");
+        ThrowIfFailed(nullptr, st, "GpuDevice");
+    }
+    d->ctx_ = ctx;
+    char name[256];
+    og_device_name(ctx, name, sizeof name);
+    d->name_ = name;
+    uint64_t maxbuf = 0;
+    uint32_t cus = 0, lds = 0;
+    og_device_limits(ctx, &maxbuf, &cus, &lds);
+    d->caps_.ComputeUnits = cus;
+    d->caps_.MaxStorageBufferBindingBytes = options.MaxStorageBufferBindingBytes;
+    return d;
+}
+
+std::shared_ptr<GpuDevice> GpuDevice::CreateHostOnly(GpuDeviceOptions options)
+{
+    std::shared_ptr<GpuDevice> d(new GpuDevice());
+    d->name_ = "host only (no GPU)";
+    d->caps_.MaxStorageBufferBindingBytes = options.MaxStorageBufferBindingBytes;
+    return d;
+}
+
+GpuDevice::~GpuDevice()
+{
+    if (ctx_) og_destroy(ctx_);
+}
+
+GpuBuffer GpuDevice::CreateBuffer(ElementType type, int length)
+{
+    if (length < 0) throw std::invalid_argument("CreateBuffer: length must not be negative");
+    auto impl = std::make_shared<GpuBuffer::Impl>();
+    impl->device = shared_from_this();
+    impl->length = length;
+    impl->type = type;
+    uint64_t bytes = (uint64_t)length * ElementSize(type);
+    bytes = (bytes + 3) / 4 * 4;  // a whole 32-bit word, as the reference pads
+    if (bytes == 0) bytes = 4;
+    impl->bytes = bytes;
+    if (ctx_) {
+        impl->ctx = ctx_;
+        ThrowIfFailed(ctx_, og_alloc(ctx_, bytes, &impl->ptr), "CreateBuffer");
+        ThrowIfFailed(ctx_, og_fill_bytes(ctx_, impl->ptr, 0, bytes), "CreateBuffer");
+    } else {
+        impl->ptr = std::calloc(1, bytes);
+        if (!impl->ptr) throw GpuOutOfMemoryException("CreateBuffer: host allocation failed");
+    }
+    return GpuBuffer(impl);
+}
+
+void GpuDevice::Submit(GpuCommandEncoder &encoder)
+{
+    if (encoder.submitted_) throw GpuException("GpuDevice.Submit: encoder already submitted");
+    encoder.submitted_ = true;
+    if (encoder.commands_.empty()) return;
+    if (!ctx_) throw GpuUnsupportedException("GpuDevice.Submit: a host-only device cannot run work", "Device", "a HIP device", "none");
+    timed_ = 0;
+    const int start = encoder.timing_start_, stop = encoder.timing_stop_;
+    for (int i = 0; i < (int)encoder.commands_.size(); i++) {
+        // A command may launch more than one kernel (a split product, the two passes of a quantizer): 4 slots each.
+        if (i == start && stop >= start) ThrowIfFailed(ctx_, og_timing_begin(ctx_, std::max(encoder.timing_slots_, stop - start + 1) * 4), "BeginPassTiming");
+        encoder.commands_[i].run(ctx_);
+        if (i == stop && stop >= start) ThrowIfFailed(ctx_, og_timing_end(ctx_, &timed_), "EndPassTiming");
+    }
+}
+
+void GpuDevice::WaitIdle()
+{
+    if (ctx_) ThrowIfFailed(ctx_, og_sync(ctx_), "GpuDevice.WaitIdle");
+}
+
+std::vector<std::pair<double, std::string>> GpuDevice::ReadPassTimes()
+{
+    std::vector<std::pair<double, std::string>> out;
+    for (int i = 0; i < timed_; i++) {
+        float ms = 0;
+        const char *name = "";
+        ThrowIfFailed(ctx_, og_timing_read(ctx_, i, &ms, &name), "ReadPassTimes");
+        out.emplace_back((double)ms, name);
+    }
+    return out;
+}
+
+// ------------------------------------------------------------------ Check (KernelSupport.cs:68-131)
+
+namespace Check {
+
+void Range(const std::string &operation, const std::string &name, int64_t bufferLength, int64_t offset, int64_t extent,
+           bool half)
+{
+    if (offset < 0) throw GpuKernelShapeException(operation, name + "Offset", "offset " + fmt_long(offset) + " is negative");
+    if (extent < 0 || offset + extent > bufferLength)
+        throw GpuKernelShapeException(operation, name, "elements " + fmt_long(offset) + ".." + fmt_long(offset + extent) +
+                                                           " reach past the buffer of " + fmt_long(bufferLength));
+    if (half && extent > 0 && (((offset + extent + 1) >> 1) << 1) > bufferLength)
+        throw GpuKernelShapeException(operation, name, "the buffer of " + fmt_long(bufferLength) +
+                                                           " halves ends inside a 32-bit word; allocate GpuKernelBuffers.PaddedHalfLength(n) elements");
+}
+
+void RangeBytes(const std::string &operation, const std::string &name, int64_t bufferLength, int64_t offset, int64_t extent)
+{
+    if (offset < 0) throw GpuKernelShapeException(operation, name + "Offset", "offset " + fmt_long(offset) + " is negative");
+    if (extent < 0 || offset + extent > bufferLength)
+        throw GpuKernelShapeException(operation, name, "elements " + fmt_long(offset) + ".." + fmt_long(offset + extent) +
+                                                           " reach past the buffer of " + fmt_long(bufferLength));
+    if (extent > 0 && (((offset + extent + 3) >> 2) << 2) > bufferLength)
+        throw GpuKernelShapeException(operation, name, "the buffer of " + fmt_long(bufferLength) +
+                                                           " bytes ends inside a 32-bit word; allocate GpuKernelBuffers.PaddedBoolLength(n) elements");
+}
+
+int64_t Product(const std::string &operation, const std::string &name, const std::vector<int> &shape)
+{
+    int64_t n = 1;
+    for (size_t i = 0; i < shape.size(); i++) {
+        std::string dim = name + "[" + std::to_string(i) + "]";
+        if (shape[i] < 0) throw GpuKernelShapeException(operation, dim, "dimension " + std::to_string(shape[i]) + " is negative");
+        n *= shape[i];
+        if (n > MaxElements) throw GpuKernelShapeException(operation, dim, "the tensor holds more than 2147483647 elements");
+    }
+    return n;
+}
+
+}  // namespace Check
+
+namespace {
+
+std::vector<std::shared_ptr<GpuBuffer::Impl>> keep_of(std::initializer_list<const GpuBuffer *> bs)
+{
+    std::vector<std::shared_ptr<GpuBuffer::Impl>> k;
+    for (auto *b : bs)
+        if (b && b->Valid()) k.push_back(b->impl());
+    return k;
+}
+
+og_buffer bind(const GpuBuffer &b) { return b.Binding(); }
+
+int axis_of(const std::string &operation, int axis, int rank)
+{
+    if (axis < -rank || axis >= rank)
+        throw GpuKernelShapeException(operation, "axis", "axis " + std::to_string(axis) + " is outside [" +
+                                                             std::to_string(-rank) + ", " + std::to_string(rank) + ")");
+    return axis < 0 ? axis + rank : axis;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ Int8Gemm
+
+static const char *kGemm = "Int8Gemm";
+
+static bool is_int8(ElementType t) { return t == ElementType::UInt8 || t == ElementType::Int8; }
+
+// Int8Gemm.cs:393-400.
+static void RequireInt8(const GpuBuffer &b, const std::string &argument)
+{
+    if (!is_int8(b.Type()))
+        throw GpuKernelShapeException(kGemm, argument, std::string("element type ") + ElementName(b.Type()) +
+                                                           " is not supported; use byte (uint8) or sbyte (int8)");
+}
+
+// The C# signature types an operand by its generic parameter; here the buffer carries it.
+static void RequireType(const std::string &op, const GpuBuffer &b, ElementType t, const std::string &argument)
+{
+    if (b.Type() != t)
+        throw GpuKernelShapeException(op, argument, std::string("element type ") + ElementName(b.Type()) + " is not " + ElementName(t));
+}
+
+static void NonNegative(const std::string &argument, int value)
+{
+    if (value < 0) throw GpuKernelShapeException(kGemm, argument, "must not be negative, got " + std::to_string(value));
+}
+
+// Int8Gemm.cs:411-416.
+static void CheckVector(const std::string &name, const GpuBuffer &buffer, int offset, bool isVector, int n)
+{
+    if (!buffer.Valid()) throw GpuKernelShapeException(kGemm, name, "buffer is null");
+    Check::Range(kGemm, name, buffer.Length(), offset, isVector ? n : 1);
+}
+
+// Int8Gemm.cs:494-501.
+static void CheckRange(const std::string &operand, int offset, int stride, int rows, int cols, int ld, int batch, int length)
+{
+    int64_t last = offset + ((int64_t)(batch - 1) * stride) + ((int64_t)(rows - 1) * ld) + (cols - 1);
+    if (last >= length)
+        throw GpuKernelShapeException(kGemm, "Offset" + operand, "operand " + operand + " reaches byte " + fmt_long(last) +
+                                                                     " but its buffer holds " + std::to_string(length));
+}
+
+Int8Gemm::Int8Gemm(std::shared_ptr<GpuDevice> device, Int8GemmOptions options, int maxCachedBindGroups)
+    : device_(std::move(device)), options_(options)
+{
+    if (!device_) throw std::invalid_argument("device");
+    if (maxCachedBindGroups < 1) throw std::out_of_range("maxCachedBindGroups");
+    variant_ = options_.AllowPackedDot ? "mfma-i8-gfx950" : "portable-tile64x64x16";
+}
+
+Int8Gemm::~Int8Gemm() = default;
+
+void Int8Gemm::Dispose() { scratch_.clear(); }
+
+void Int8Gemm::CheckBindable(const std::string &operand, const GpuBuffer &buffer) const
+{
+    uint64_t maxBinding = device_->Capabilities().MaxStorageBufferBindingBytes;
+    if (maxBinding != 0 && buffer.Size() > maxBinding)
+        throw GpuUnsupportedException(std::string(kGemm) + ": operand " + operand + " is " + std::to_string(buffer.Size()) +
+                                          " bytes, more than one storage binding can cover on " + device_->AdapterName(),
+                                      "MaxStorageBufferBindingBytes", "at most " + std::to_string(maxBinding) + " bytes",
+                                      std::to_string(buffer.Size()) + " bytes");
+}
+
+// Int8Gemm.cs:418-484.
+Int8Gemm::Prepared Int8Gemm::Prepare(const Int8GemmProblem &p, const GpuBuffer &a, const GpuBuffer &b,
+                                     const std::optional<Int8Operand> &zpA, const std::optional<Int8Operand> &zpB)
+{
+    if (!a.Valid()) throw GpuKernelShapeException(kGemm, "a", "buffer is null");
+    if (!b.Valid()) throw GpuKernelShapeException(kGemm, "b", "buffer is null");
+    RequireInt8(a, "a");
+    RequireInt8(b, "b");
+    NonNegative("M", p.M);
+    NonNegative("N", p.N);
+    NonNegative("K", p.K);
+    NonNegative("OffsetA", p.OffsetA);
+    NonNegative("OffsetB", p.OffsetB);
+    NonNegative("OffsetC", p.OffsetC);
+    NonNegative("StrideA", p.StrideA);
+    NonNegative("StrideB", p.StrideB);
+    NonNegative("Lda", p.Lda);
+    NonNegative("Ldb", p.Ldb);
+    if (p.Batch < 1) throw GpuKernelShapeException(kGemm, "Batch", "must be at least 1, got " + std::to_string(p.Batch));
+    int lda = p.Lda == 0 ? std::max(p.K, 1) : p.Lda;
+    int colsB = p.TransposeB ? p.K : p.N;
+    int rowsB = p.TransposeB ? p.N : p.K;
+    int ldb = p.Ldb == 0 ? std::max(colsB, 1) : p.Ldb;
+    if (lda < p.K) throw GpuKernelShapeException(kGemm, "Lda", std::to_string(lda) + " is smaller than K = " + std::to_string(p.K));
+    if (ldb < colsB) throw GpuKernelShapeException(kGemm, "Ldb", std::to_string(ldb) + " is smaller than the stored row length " + std::to_string(colsB));
+    if ((int64_t)p.Batch * p.M * p.N > Check::MaxElements)
+        throw GpuKernelShapeException(kGemm, "Batch", "the result holds more elements than the kernels address");
+    if (p.M > 0 && p.N > 0 && p.K > 0) {
+        CheckRange("A", p.OffsetA, p.StrideA, p.M, p.K, lda, p.Batch, a.Length());
+        CheckRange("B", p.OffsetB, p.StrideB, rowsB, colsB, ldb, p.Batch, b.Length());
+    }
+    if (zpA) {
+        if (zpA->Buffer.Valid()) RequireType(kGemm, zpA->Buffer, a.Type(), "zpA");
+        CheckVector("zpA", zpA->Buffer, zpA->Offset, zpA->IsVector, p.M);
+        CheckBindable("zero point A", zpA->Buffer);
+    }
+    if (zpB) {
+        if (zpB->Buffer.Valid()) RequireType(kGemm, zpB->Buffer, b.Type(), "zpB");
+        CheckVector("zpB", zpB->Buffer, zpB->Offset, zpB->IsVector, p.N);
+        CheckBindable("zero point B", zpB->Buffer);
+    }
+    CheckBindable("A", a);
+    CheckBindable("B", b);
+    return Prepared{lda, ldb, p.M > 0 && p.N > 0};
+}
+
+void Int8Gemm::EncodeInt32(GpuCommandEncoder &encoder, const Int8GemmProblem &problem, const GpuBuffer &a,
+                           const GpuBuffer &b, const GpuBuffer &c, const std::optional<Int8Operand> &zeroPointA,
+                           const std::optional<Int8Operand> &zeroPointB, const std::optional<Int8Operand> &bias)
+{
+    if (!c.Valid()) throw GpuKernelShapeException(kGemm, "c", "buffer is null");
+    auto prep = Prepare(problem, a, b, zeroPointA, zeroPointB);
+    RequireType(kGemm, c, ElementType::Int32, "c");
+    int64_t count = (int64_t)problem.Batch * problem.M * problem.N;
+    Check::Range(kGemm, "c", c.Length(), problem.OffsetC, count);
+    CheckBindable("C", c);
+    Epilogue epi;
+    if (bias) {
+        if (bias->Buffer.Valid()) RequireType(kGemm, bias->Buffer, ElementType::Int32, "bias");
+        CheckVector("bias", bias->Buffer, bias->Offset, true, problem.N);
+        CheckBindable("bias", bias->Buffer);
+        epi.Flags = OG_EPI_INT_BIAS;
+        epi.IntBias = bias->Buffer;
+        epi.OffIntBias = (uint32_t)bias->Offset;
+    }
+    if (!prep.Ok) return;
+    Multiply(encoder, problem, a, a.Type() == ElementType::Int8, b, b.Type() == ElementType::Int8, c, problem.OffsetC,
+             zeroPointA, zeroPointB, epi);
+}
+
+void Int8Gemm::EncodeFloat(GpuCommandEncoder &encoder, const Int8GemmProblem &problem, const GpuBuffer &a,
+                           const GpuBuffer &b, const GpuBuffer &c, const Int8Operand &scale,
+                           const std::optional<Int8Operand> &zeroPointA, const std::optional<Int8Operand> &zeroPointB,
+                           const std::optional<Int8Operand> &floatBias, const std::optional<Int8Operand> &intBias)
+{
+    if (!c.Valid()) throw GpuKernelShapeException(kGemm, "c", "buffer is null");
+    auto prep = Prepare(problem, a, b, zeroPointA, zeroPointB);
+    RequireType(kGemm, c, ElementType::Float32, "c");
+    int64_t count = (int64_t)problem.Batch * problem.M * problem.N;
+    Check::Range(kGemm, "c", c.Length(), problem.OffsetC, count);
+    CheckBindable("C", c);
+    if (scale.Buffer.Valid()) RequireType(kGemm, scale.Buffer, ElementType::Float32, "scale");
+    CheckVector("scale", scale.Buffer, scale.Offset, scale.IsVector, problem.N);
+    if (floatBias) {
+        if (floatBias->Buffer.Valid()) RequireType(kGemm, floatBias->Buffer, ElementType::Float32, "floatBias");
+        CheckVector("floatBias", floatBias->Buffer, floatBias->Offset, true, problem.N);
+    }
+    if (!prep.Ok) return;
+    Epilogue epi;
+    epi.Flags = OG_EPI_FLOAT | (scale.IsVector ? OG_EPI_SCALE_PER_COL : 0u);
+    if (intBias) {
+        if (intBias->Buffer.Valid()) RequireType(kGemm, intBias->Buffer, ElementType::Int32, "intBias");
+        CheckVector("intBias", intBias->Buffer, intBias->Offset, true, problem.N);
+        CheckBindable("bias", intBias->Buffer);
+        epi.Flags |= OG_EPI_INT_BIAS;
+        epi.IntBias = intBias->Buffer;
+        epi.OffIntBias = (uint32_t)intBias->Offset;
+    }
+    if (floatBias) {
+        CheckBindable("float bias", floatBias->Buffer);
+        epi.Flags |= OG_EPI_FLOAT_BIAS;
+        epi.FloatBias = floatBias->Buffer;
+        epi.OffFloatBias = (uint32_t)floatBias->Offset;
+    }
+    CheckBindable("scale", scale.Buffer);
+    epi.Scale = scale.Buffer;
+    epi.OffScale = (uint32_t)scale.Offset;
+    Multiply(encoder, problem, a, a.Type() == ElementType::Int8, b, b.Type() == ElementType::Int8, c, problem.OffsetC,
+             zeroPointA, zeroPointB, epi);
+}
+
+void Int8Gemm::EncodeRequantized(GpuCommandEncoder &encoder, const Int8GemmProblem &problem, const GpuBuffer &a,
+                                 const GpuBuffer &b, const GpuBuffer &y, const Int8Operand &multiplier, int zeroPointY,
+                                 const std::optional<Int8Operand> &zeroPointA, const std::optional<Int8Operand> &zeroPointB,
+                                 const std::optional<Int8Operand> &intBias, const std::optional<Int8Scratch> &scratch)
+{
+    if (!y.Valid()) throw GpuKernelShapeException(kGemm, "y", "buffer is null");
+    auto prep = Prepare(problem, a, b, zeroPointA, zeroPointB);
+    RequireInt8(y, "y");
+    bool outSigned = y.Type() == ElementType::Int8;
+    if (zeroPointY < (outSigned ? -128 : 0) || zeroPointY > (outSigned ? 127 : 255))
+        throw GpuKernelShapeException(kGemm, "zeroPointY", std::to_string(zeroPointY) + " is outside the output type's range");
+    int64_t count = (int64_t)problem.Batch * problem.M * problem.N;
+    Check::Range(kGemm, "y", y.Length(), problem.OffsetC, count);
+    CheckBindable("Y", y);
+    if (multiplier.Buffer.Valid()) RequireType(kGemm, multiplier.Buffer, ElementType::Float32, "multiplier");
+    CheckVector("multiplier", multiplier.Buffer, multiplier.Offset, multiplier.IsVector, problem.N);
+    if (!prep.Ok) return;
+    auto [sums, at] = Scratch(count, scratch);
+    Epilogue none;
+    Multiply(encoder, problem, a, a.Type() == ElementType::Int8, b, b.Type() == ElementType::Int8, sums, at, zeroPointA,
+             zeroPointB, none);
+    // Int8Gemm.Finish (Int8Gemm.cs:649-682), mode 2.
+    uint32_t flags = (multiplier.IsVector ? 2u : 0u) | (outSigned ? 0u : 8u);
+    uint32_t offBias = 0;
+    GpuBuffer biasBuf;
+    if (intBias) {
+        if (intBias->Buffer.Valid()) RequireType(kGemm, intBias->Buffer, ElementType::Int32, "intBias");
+        CheckVector("intBias", intBias->Buffer, intBias->Offset, true, problem.N);
+        flags |= 1u;
+        offBias = (uint32_t)intBias->Offset;
+        biasBuf = intBias->Buffer;
+    }
+    og_int8_epilogue_params w{};
+    w.Count = (uint32_t)count;
+    w.OffAcc = (uint32_t)at;
+    w.OffOut = (uint32_t)problem.OffsetC;
+    w.N = (uint32_t)problem.N;
+    w.Mode = 2;
+    w.Flags = flags;
+    w.OffBias = offBias;
+    w.OffScale = (uint32_t)multiplier.Offset;
+    w.ZeroPoint = zeroPointY;
+    GpuBuffer mult = multiplier.Buffer;
+    encoder.Record(
+        [w, sums, y, biasBuf, mult](og_ctx *ctx) {
+            ThrowIfFailed(ctx, og_int8_epilogue(ctx, &w, bind(sums), bind(y), bind(biasBuf), bind(mult), og_buffer{nullptr, 0}), kGemm);
+        },
+        keep_of({&sums, &y, &biasBuf, &mult}));
+}
+
+int64_t Int8Gemm::ScratchElements(const Int8GemmProblem &problem)
+{
+    return problem.M <= 0 || problem.N <= 0 || problem.Batch <= 0 ? 0 : (int64_t)problem.Batch * problem.M * problem.N;
+}
+
+void Int8Gemm::ReserveScratch(int64_t elements)
+{
+    if (elements < 0 || elements > Check::MaxElements) throw std::out_of_range("elements");
+    if (elements == 0 || (!scratch_.empty() && scratch_.back().Length() >= elements)) return;
+    scratch_.push_back(device_->CreateBuffer(ElementType::Int32, (int)std::max<int64_t>(elements, 4096)));
+}
+
+// Int8Gemm.cs:503-523.
+std::pair<GpuBuffer, int> Int8Gemm::Scratch(int64_t count, const std::optional<Int8Scratch> &given)
+{
+    if (given) {
+        if (!given->Buffer.Valid()) throw GpuKernelShapeException(kGemm, "given", "buffer is null");
+        RequireType(kGemm, given->Buffer, ElementType::Int32, "scratch");
+        Check::Range(kGemm, "scratch", given->Buffer.Length(), given->Offset, count);
+        CheckBindable("scratch", given->Buffer);
+        return {given->Buffer, given->Offset};
+    }
+    if (!scratch_.empty() && scratch_.back().Length() >= count) return {scratch_.back(), 0};
+    int64_t length = std::min<int64_t>(Check::MaxElements, std::max<int64_t>(count, !scratch_.empty() ? (int64_t)scratch_.back().Length() * 2 : 4096));
+    scratch_.push_back(device_->CreateBuffer(ElementType::Int32, (int)length));
+    return {scratch_.back(), 0};
+}
+
+// Int8Gemm.cs:554-639: the 19 parameter words, then one og_int8_gemm call when the encoder is submitted.
+void Int8Gemm::Multiply(GpuCommandEncoder &encoder, const Int8GemmProblem &p, const GpuBuffer &a, bool aSigned,
+                        const GpuBuffer &b, bool bSigned, const GpuBuffer &c, int offsetC,
+                        const std::optional<Int8Operand> &za, const std::optional<Int8Operand> &zb, const Epilogue &epi)
+{
+    int lda = p.Lda == 0 ? std::max(p.K, 1) : p.Lda;
+    int ldb = p.Ldb == 0 ? std::max(p.TransposeB ? p.K : p.N, 1) : p.Ldb;
+    uint32_t flags = (aSigned ? OG_GEMM_A_INT8 : 0u) | (bSigned ? OG_GEMM_B_INT8 : 0u) | (p.TransposeB ? OG_GEMM_TRANSPOSE_B : 0u);
+    uint32_t offZa = 0, offZb = 0;
+    GpuBuffer zaBuf, zbBuf;
+    if (za) {
+        flags |= OG_GEMM_ZA | (za->IsVector ? OG_GEMM_ZA_PER_ROW : 0u);
+        offZa = (uint32_t)za->Offset;
+        zaBuf = za->Buffer;
+    }
+    if (zb) {
+        flags |= OG_GEMM_ZB | (zb->IsVector ? OG_GEMM_ZB_PER_COL : 0u);
+        offZb = (uint32_t)zb->Offset;
+        zbBuf = zb->Buffer;
+    }
+    // The reference's word-alignment bits (informational here: the library checks the addresses itself).
+    if (((p.OffsetA | p.StrideA | lda) & 3) == 0) flags |= 128u;
+    if (((p.OffsetB | p.StrideB | ldb) & 3) == 0) flags |= 256u;
+    if (!options_.AllowPackedDot) flags |= OG_GEMM_PORTABLE;
+    if (options_.Tile == 64) flags |= OG_GEMM_NO_SKINNY;
+    if (options_.Tile == 32) flags |= OG_GEMM_NO_DIRECT;
+
+    og_int8_gemm_params w{};
+    w.M = (uint32_t)p.M;
+    w.N = (uint32_t)p.N;
+    w.K = (uint32_t)p.K;
+    w.OffA = (uint32_t)p.OffsetA;
+    w.OffB = (uint32_t)p.OffsetB;
+    w.OffC = (uint32_t)offsetC;
+    w.StrideA = (uint32_t)p.StrideA;
+    w.StrideB = (uint32_t)p.StrideB;
+    w.StrideC = (uint32_t)((int64_t)p.M * p.N);
+    w.Lda = (uint32_t)lda;
+    w.Ldb = (uint32_t)ldb;
+    w.Flags = flags;
+    w.OffZA = offZa;
+    w.OffZB = offZb;
+    w.Epi = epi.Flags;
+    w.OffBias = epi.OffIntBias;
+    w.OffScale = epi.OffScale;
+    w.OffFBias = epi.OffFloatBias;
+    w.GridX = 0;
+    uint32_t batch = (uint32_t)p.Batch;
+    GpuBuffer A = a, B = b, C = c, ib = epi.IntBias, sc = epi.Scale, fb = epi.FloatBias;
+    encoder.Record(
+        [w, batch, A, B, C, zaBuf, zbBuf, ib, sc, fb](og_ctx *ctx) {
+            ThrowIfFailed(ctx, og_int8_gemm(ctx, &w, batch, bind(A), bind(B), bind(C), bind(zaBuf), bind(zbBuf), bind(ib), bind(sc), bind(fb)), kGemm);
+        },
+        keep_of({&A, &B, &C, &zaBuf, &zbBuf, &ib, &sc, &fb}));
+}
+
+// ------------------------------------------------------------------ DynamicQuantizeKernels
+
+DynamicQuantizeKernels::DynamicQuantizeKernels(std::shared_ptr<GpuDevice> device, int maxCachedBindGroups)
+    : device_(std::move(device))
+{
+    if (!device_) throw std::invalid_argument("device");
+    if (maxCachedBindGroups < 1) throw std::out_of_range("maxCachedBindGroups");
+}
+
+void DynamicQuantizeKernels::Encode(GpuCommandEncoder &encoder, const GpuBuffer &x, int offsetX, int count,
+                                    const GpuBuffer &y, int offsetY, const GpuBuffer &scale, int offsetScale,
+                                    const GpuBuffer &zeroPoint, int offsetZeroPoint)
+{
+    const std::string Name = "DynamicQuantizeLinear";
+    if (!x.Valid()) throw GpuKernelShapeException(Name, "x", "buffer is null");
+    if (!y.Valid()) throw GpuKernelShapeException(Name, "y", "buffer is null");
+    if (!scale.Valid()) throw GpuKernelShapeException(Name, "scale", "buffer is null");
+    if (!zeroPoint.Valid()) throw GpuKernelShapeException(Name, "zeroPoint", "buffer is null");
+    RequireType(Name, x, ElementType::Float32, "x");
+    RequireType(Name, y, ElementType::UInt8, "y");
+    RequireType(Name, scale, ElementType::Float32, "scale");
+    RequireType(Name, zeroPoint, ElementType::UInt8, "zeroPoint");
+    if (count < 1) throw GpuKernelShapeException(Name, "count", "count " + std::to_string(count) + " must be at least 1");
+    Check::Range(Name, "x", x.Length(), offsetX, count);
+    Check::Range(Name, "y", y.Length(), offsetY, count);
+    Check::Range(Name, "scale", scale.Length(), offsetScale, 1);
+    Check::Range(Name, "zeroPoint", zeroPoint.Length(), offsetZeroPoint, 1);
+    og_dq_params w{};
+    w.Count = (uint32_t)count;
+    w.OffX = (uint32_t)offsetX;
+    w.OffY = (uint32_t)offsetY;
+    w.OffScale = (uint32_t)offsetScale;
+    w.OffZero = (uint32_t)offsetZeroPoint;
+    GpuBuffer X = x, Y = y, S = scale, Z = zeroPoint;
+    encoder.Record(
+        [w, X, Y, S, Z](og_ctx *ctx) {
+            ThrowIfFailed(ctx, og_dynamic_quantize(ctx, &w, bind(X), bind(Y), bind(S), bind(Z)), "DynamicQuantizeLinear");
+        },
+        keep_of({&X, &Y, &S, &Z}));
+}
+
+// ------------------------------------------------------------------ DequantizeKernels
+
+DequantizeKernels::DequantizeKernels(std::shared_ptr<GpuDevice> device, int maxCachedBindGroups) : device_(std::move(device))
+{
+    if (!device_) throw std::invalid_argument("device");
+    if (maxCachedBindGroups < 1) throw std::out_of_range("maxCachedBindGroups");
+}
+
+// KernelTypes.IsHalf<T> (KernelSupport.cs:49-65): float or Half, anything else named as T.
+static bool IsHalf(const std::string &operation, ElementType t)
+{
+    switch (t) {
+    case ElementType::Float32: return false;
+    case ElementType::Float16: return true;
+    case ElementType::Int32:
+    case ElementType::Int64:
+    case ElementType::UInt32:
+        throw GpuKernelShapeException(operation, "T", std::string("element type ") + ElementName(t) + " is not supported; use float or Half");
+    default:
+        throw GpuKernelShapeException(operation, "T", std::string("element type ") + ElementName(t) +
+                                                          " is not supported; use float, Half, int, long or uint as the operation allows");
+    }
+}
+
+static void split_axis(const std::string &op, const std::vector<int> &shape, int axis, bool perAxis, int64_t &axisLen,
+                       int64_t &inner)
+{
+    axisLen = 1;
+    inner = 1;
+    if (!perAxis) return;
+    int rank = (int)shape.size();
+    int ax = axis_of(op, axis, rank);
+    axisLen = shape[ax];
+    for (int i = ax + 1; i < rank; i++) inner *= shape[i];
+}
+
+void DequantizeKernels::Encode(GpuCommandEncoder &encoder, const GpuBuffer &x, int offsetX, const std::vector<int> &shape,
+                               int axis, bool perAxis, const GpuBuffer &scale, int offsetScale,
+                               const std::optional<GpuBuffer> &zeroPoint, int offsetZeroPoint, const GpuBuffer &output,
+                               int offsetOutput)
+{
+    const std::string Name = "DequantizeLinear";
+    if (!x.Valid()) throw GpuKernelShapeException(Name, "x", "buffer is null");
+    if (!scale.Valid()) throw GpuKernelShapeException(Name, "scale", "buffer is null");
+    if (!output.Valid()) throw GpuKernelShapeException(Name, "output", "buffer is null");
+    int kind;
+    switch (x.Type()) {
+    case ElementType::UInt8: kind = OG_KIND_U8; break;
+    case ElementType::Int8: kind = OG_KIND_I8; break;
+    case ElementType::Int32: kind = OG_KIND_I32; break;
+    default:
+        throw GpuKernelShapeException(Name, "TIn", std::string("element type ") + ElementName(x.Type()) +
+                                                       " is not supported; use byte (uint8), sbyte (int8) or int");
+    }
+    bool half = IsHalf(Name, output.Type());
+    int64_t count = Check::Product(Name, "shape", shape);
+    int64_t axisLen, inner;
+    split_axis(Name, shape, axis, perAxis, axisLen, inner);
+    int64_t parameters = perAxis ? axisLen : 1;
+    RequireType(Name, scale, ElementType::Float32, "scale");
+    Check::Range(Name, "scale", scale.Length(), offsetScale, parameters);
+    if (kind == OG_KIND_I32) Check::Range(Name, "x", x.Length(), offsetX, count);
+    else Check::RangeBytes(Name, "x", x.Length(), offsetX, count);
+    if (zeroPoint) {
+        RequireType(Name, *zeroPoint, x.Type(), "zeroPoint");
+        if (kind == OG_KIND_I32) Check::Range(Name, "zeroPoint", zeroPoint->Length(), offsetZeroPoint, parameters);
+        else Check::RangeBytes(Name, "zeroPoint", zeroPoint->Length(), offsetZeroPoint, parameters);
+    }
+    Check::Range(Name, "output", output.Length(), offsetOutput, count, half);
+    if (count == 0) return;
+    og_dequant_params w{};
+    w.Count = (uint32_t)count;
+    w.OffX = (uint32_t)offsetX;
+    w.OffO = (uint32_t)offsetOutput;
+    w.OffS = (uint32_t)offsetScale;
+    w.OffZ = (uint32_t)offsetZeroPoint;
+    w.Flags = (perAxis ? 1u : 0u) | (zeroPoint ? 2u : 0u);
+    w.AxisLen = (uint32_t)axisLen;
+    w.Inner = (uint32_t)std::max<int64_t>(inner, 1);
+    GpuBuffer X = x, S = scale, Z = zeroPoint ? *zeroPoint : GpuBuffer(), O = output;
+    encoder.Record(
+        [w, kind, half, X, S, Z, O](og_ctx *ctx) {
+            ThrowIfFailed(ctx, og_dequantize(ctx, kind, half ? 1 : 0, &w, bind(X), bind(S), bind(Z), bind(O)), "DequantizeLinear");
+        },
+        keep_of({&X, &S, &Z, &O}));
+}
+
+void DequantizeKernels::EncodeQuantize(GpuCommandEncoder &encoder, const GpuBuffer &x, int offsetX,
+                                       const std::vector<int> &shape, int axis, bool perAxis, const GpuBuffer &scale,
+                                       int offsetScale, const std::optional<GpuBuffer> &zeroPoint, int offsetZeroPoint,
+                                       const GpuBuffer &output, int offsetOutput)
+{
+    const std::string QName = "QuantizeLinear";
+    if (!x.Valid()) throw GpuKernelShapeException(QName, "x", "buffer is null");
+    if (!scale.Valid()) throw GpuKernelShapeException(QName, "scale", "buffer is null");
+    if (!output.Valid()) throw GpuKernelShapeException(QName, "output", "buffer is null");
+    bool isSigned;
+    switch (output.Type()) {
+    case ElementType::UInt8: isSigned = false; break;
+    case ElementType::Int8: isSigned = true; break;
+    default:
+        throw GpuKernelShapeException(QName, "TOut", std::string("element type ") + ElementName(output.Type()) +
+                                                         " is not supported; use byte (uint8) or sbyte (int8)");
+    }
+    bool half = IsHalf(QName, x.Type());
+    int64_t count = Check::Product(QName, "shape", shape);
+    int64_t axisLen, inner;
+    split_axis(QName, shape, axis, perAxis, axisLen, inner);
+    int64_t parameters = perAxis ? axisLen : 1;
+    Check::Range(QName, "x", x.Length(), offsetX, count, half);
+    RequireType(QName, scale, ElementType::Float32, "scale");
+    Check::Range(QName, "scale", scale.Length(), offsetScale, parameters);
+    if (zeroPoint) {
+        RequireType(QName, *zeroPoint, output.Type(), "zeroPoint");
+        Check::RangeBytes(QName, "zeroPoint", zeroPoint->Length(), offsetZeroPoint, parameters);
+    }
+    Check::RangeBytes(QName, "output", output.Length(), offsetOutput, count);
+    if (count == 0) return;
+    og_dequant_params w{};
+    w.Count = (uint32_t)count;
+    w.OffX = (uint32_t)offsetX;
+    w.OffO = (uint32_t)offsetOutput;
+    w.OffS = (uint32_t)offsetScale;
+    w.OffZ = (uint32_t)offsetZeroPoint;
+    w.Flags = (perAxis ? 1u : 0u) | (zeroPoint ? 2u : 0u);
+    w.AxisLen = (uint32_t)axisLen;
+    w.Inner = (uint32_t)std::max<int64_t>(inner, 1);
+    GpuBuffer X = x, S = scale, Z = zeroPoint ? *zeroPoint : GpuBuffer(), O = output;
+    encoder.Record(
+        [w, isSigned, half, X, S, Z, O](og_ctx *ctx) {
+            ThrowIfFailed(ctx, og_quantize(ctx, isSigned ? 1 : 0, half ? 1 : 0, &w, bind(X), bind(S), bind(Z), bind(O)), "QuantizeLinear");
+        },
+        keep_of({&X, &S, &Z, &O}));
+}
+
+}  // namespace onegpu

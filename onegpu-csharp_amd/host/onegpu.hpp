@@ -1,0 +1,303 @@
+// The host side of the MI355X int8 path: the reference's kernel-family API (RecursiveAI.OneGpu.Kernels — Int8Gemm,
+// DynamicQuantizeKernels, DequantizeKernels) and the slice of its device layer they need (GpuDevice, GpuBuffer,
+// GpuCommandEncoder, the exceptions), in C++ over the C ABI of libonegpu_hip.so (include/onegpu_hip.h).
+//
+// Names, argument meaning, validation order and the exception raised for each bad argument follow the C# sources cited
+// at each member, so code written against the reference API reads the same here. What differs is only what HIP makes
+// moot: there are no bind groups (BindGroupsCreated stays 0), and buffers carry their element type at run time where
+// the C# API has a generic parameter, so the type checks the C# compiler or RequireInt8 makes happen at the call.
+#pragma once
+
+#include <cstdint>
+#include <functional>
+#include <memory>
+#include <optional>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "onegpu_hip.h"
+
+namespace onegpu {
+
+// ------------------------------------------------------------------ exceptions (src/RecursiveAI.OneGpu/GpuDevice.cs:266-396;
+// src/RecursiveAI.OneGpu.Kernels/GpuKernelShapeException.cs:7-25)
+
+class GpuException : public std::runtime_error {
+public:
+    explicit GpuException(const std::string &m) : std::runtime_error(m) {}
+};
+
+// A shape, stride, offset or size is invalid for the operation; raised before any work is recorded.
+class GpuKernelShapeException : public GpuException {
+public:
+    GpuKernelShapeException(std::string operation, std::string argument, const std::string &message)
+        : GpuException(operation + ": " + argument + ": " + message), Operation(std::move(operation)),
+          Argument(std::move(argument)), Detail(message) {}
+    std::string Operation, Argument, Detail;
+};
+
+class GpuUnsupportedException : public GpuException {
+public:
+    GpuUnsupportedException(const std::string &message, std::string capability = "", std::string expected = "",
+                            std::string actual = "")
+        : GpuException(message), Capability(std::move(capability)), Expected(std::move(expected)), Actual(std::move(actual)) {}
+    std::string Capability, Expected, Actual;
+};
+
+class GpuOutOfMemoryException : public GpuException {
+public:
+    using GpuException::GpuException;
+};
+
+class GpuDeviceLostException : public GpuException {
+public:
+    using GpuException::GpuException;
+};
+
+class GpuCommandFailedException : public GpuException {
+public:
+    using GpuException::GpuException;
+};
+
+// ------------------------------------------------------------------ device layer
+
+// The element types the path uses; the C# names are what its messages print (typeof(T).Name).
+enum class ElementType { UInt8, Int8, Int32, Float32, Float16, UInt32, UInt16, Int16, Int64 };
+size_t ElementSize(ElementType t);
+const char *ElementName(ElementType t);
+
+// The limits the families consult (src/RecursiveAI.OneGpu/ComputeCapabilities.cs:86-203).
+struct GpuComputeCapabilities {
+    uint64_t MaxStorageBufferBindingBytes = 0;  // 0: no limit per binding (HIP binds plain device addresses)
+    uint32_t MaxWorkgroupCount = 0;             // 0: no per-axis grid limit the families must fold around
+    bool Int8DotProduct = true;                 // int8 MFMA and v_dot4_i32_i8
+    uint32_t ComputeUnits = 0;
+};
+
+struct GpuDeviceOptions {
+    // Lower than the hardware's, to run a product the way a device with small bindings (llvmpipe: 128 MB) refuses it.
+    uint64_t MaxStorageBufferBindingBytes = 0;
+};
+
+class GpuDevice;
+
+// A typed device buffer (src/RecursiveAI.OneGpu/GpuBufferOfT.cs:11-89). Length counts elements; byte buffers are
+// allocated to a whole 32-bit word as CreateBuffer<T> does (src/RecursiveAI.OneGpu/ComputeKernel.cs:93-95).
+class GpuBuffer {
+public:
+    struct Impl;
+    GpuBuffer() = default;
+    explicit GpuBuffer(std::shared_ptr<Impl> impl) : impl_(std::move(impl)) {}
+    int Length() const;
+    ElementType Type() const;
+    uint64_t Size() const;        // bytes
+    void *DevicePointer() const;  // device address (host address on a host-only device)
+    void Write(const void *src, uint64_t bytes, uint64_t byte_offset = 0) const;
+    void Read(void *dst, uint64_t bytes, uint64_t byte_offset = 0) const;
+    void Dispose();
+    bool Valid() const { return impl_ != nullptr; }
+    og_buffer Binding() const;
+    const std::shared_ptr<Impl> &impl() const { return impl_; }
+
+private:
+    std::shared_ptr<Impl> impl_;
+};
+
+// Records work; nothing runs until GpuDevice::Submit (src/RecursiveAI.OneGpu/GpuDevice.cs:155-161; Resources.cs:148-316).
+class GpuCommandEncoder {
+public:
+    using Command = std::function<void(og_ctx *)>;
+    void Record(Command c, std::vector<std::shared_ptr<GpuBuffer::Impl>> keep);
+    int DispatchCount() const { return (int)commands_.size(); }
+    // Per-dispatch timing of the commands recorded between the two calls (Resources.cs:216-222).
+    void BeginPassTiming(int max_passes);
+    int EndPassTiming();
+
+private:
+    friend class GpuDevice;
+    struct Entry {
+        Command run;
+        std::vector<std::shared_ptr<GpuBuffer::Impl>> keep;
+    };
+    std::vector<Entry> commands_;
+    int timing_start_ = -1;  // first timed command
+    int timing_stop_ = -1;   // last timed command
+    int timing_slots_ = 0;
+    bool submitted_ = false;
+};
+
+class GpuDevice : public std::enable_shared_from_this<GpuDevice> {
+public:
+    // A HIP device (og_init). Throws GpuUnsupportedException when there is none.
+    static std::shared_ptr<GpuDevice> Create(int ordinal = 0, GpuDeviceOptions options = {});
+    // No GPU: buffers live in host memory and every family validates and records as usual, but Submit of a non-empty
+    // encoder throws. Lets argument checks run where no GPU exists.
+    static std::shared_ptr<GpuDevice> CreateHostOnly(GpuDeviceOptions options = {});
+    ~GpuDevice();
+
+    GpuBuffer CreateBuffer(ElementType type, int length);
+    GpuCommandEncoder BeginCommands() { return GpuCommandEncoder(); }
+    void Submit(GpuCommandEncoder &encoder);
+    void WaitIdle();
+    // GPU milliseconds and kernel name of each dispatch timed by the last submitted encoder (TryReadTimestamps).
+    std::vector<std::pair<double, std::string>> ReadPassTimes();
+
+    const GpuComputeCapabilities &Capabilities() const { return caps_; }
+    const std::string &AdapterName() const { return name_; }
+    std::string Backend() const { return ctx_ ? "Hip" : "HostOnly"; }
+    og_ctx *Context() const { return ctx_; }
+    bool HasGpu() const { return ctx_ != nullptr; }
+
+private:
+    GpuDevice() = default;
+    og_ctx *ctx_ = nullptr;
+    GpuComputeCapabilities caps_;
+    std::string name_;
+    int timed_ = 0;
+};
+
+// Maps a C-ABI status to the reference's exception (operation names the family).
+void ThrowIfFailed(og_ctx *ctx, int status, const std::string &operation);
+
+// ------------------------------------------------------------------ Int8Gemm (src/RecursiveAI.OneGpu.Kernels/Int8Gemm.cs)
+
+struct Int8GemmOptions {
+    bool AllowPackedDot = true;  // false forces the portable kernel (Int8Gemm.cs:9-13)
+    // Test hook (Int8Gemm.cs:15-16): 0 chooses by size; any other value keeps the few-rows kernel off so every shape
+    // runs on the tiled MFMA kernel (64), or keeps the few-rows kernel but always splits k (32).
+    int Tile = 0;
+};
+
+// A zero point, scale, multiplier or bias operand (Int8Gemm.cs:23-29).
+struct Int8Operand {
+    GpuBuffer Buffer;
+    int Offset = 0;
+    bool IsVector = false;
+};
+
+// Caller-placed int32 scratch for EncodeRequantized (Int8Gemm.cs:31-37).
+struct Int8Scratch {
+    GpuBuffer Buffer;
+    int Offset = 0;
+};
+
+// Int8Gemm.cs:39-95.
+struct Int8GemmProblem {
+    Int8GemmProblem() = default;
+    Int8GemmProblem(int m, int n, int k) : M(m), N(n), K(k), Batch(1) {}
+    int M = 0, N = 0, K = 0, Batch = 1;
+    bool TransposeB = false;
+    int Lda = 0, Ldb = 0, OffsetA = 0, OffsetB = 0, OffsetC = 0, StrideA = 0, StrideB = 0;
+    double Ops() const { return 2.0 * Batch * M * N * K; }
+};
+
+class Int8Gemm {
+public:
+    explicit Int8Gemm(std::shared_ptr<GpuDevice> device, Int8GemmOptions options = {}, int maxCachedBindGroups = 1024);
+    ~Int8Gemm();
+
+    // Int8Gemm.cs:217-253: C = (A - zeroA)(B - zeroB) (+ bias per column), int32.
+    void EncodeInt32(GpuCommandEncoder &encoder, const Int8GemmProblem &problem, const GpuBuffer &a, const GpuBuffer &b,
+                     const GpuBuffer &c, const std::optional<Int8Operand> &zeroPointA = std::nullopt,
+                     const std::optional<Int8Operand> &zeroPointB = std::nullopt,
+                     const std::optional<Int8Operand> &bias = std::nullopt);
+    // Int8Gemm.cs:255-314: float(sum + intBias) * scale + floatBias, one dispatch.
+    void EncodeFloat(GpuCommandEncoder &encoder, const Int8GemmProblem &problem, const GpuBuffer &a, const GpuBuffer &b,
+                     const GpuBuffer &c, const Int8Operand &scale, const std::optional<Int8Operand> &zeroPointA = std::nullopt,
+                     const std::optional<Int8Operand> &zeroPointB = std::nullopt,
+                     const std::optional<Int8Operand> &floatBias = std::nullopt,
+                     const std::optional<Int8Operand> &intBias = std::nullopt);
+    // Int8Gemm.cs:316-363: QLinearMatMul, the sums in scratch, then the requantizing pass.
+    void EncodeRequantized(GpuCommandEncoder &encoder, const Int8GemmProblem &problem, const GpuBuffer &a,
+                           const GpuBuffer &b, const GpuBuffer &y, const Int8Operand &multiplier, int zeroPointY,
+                           const std::optional<Int8Operand> &zeroPointA = std::nullopt,
+                           const std::optional<Int8Operand> &zeroPointB = std::nullopt,
+                           const std::optional<Int8Operand> &intBias = std::nullopt,
+                           const std::optional<Int8Scratch> &scratch = std::nullopt);
+
+    static int64_t ScratchElements(const Int8GemmProblem &problem);   // Int8Gemm.cs:525-531
+    void ReserveScratch(int64_t elements);                            // Int8Gemm.cs:533-549
+    const std::string &Variant() const { return variant_; }           // Int8Gemm.cs:214-215
+    int BindGroupsCreated() const { return 0; }                       // nothing is bound on HIP
+    void ReleaseBindings() {}
+    void Dispose();
+
+private:
+    struct Prepared {
+        int Lda, Ldb;
+        bool Ok;
+    };
+    struct Epilogue {
+        uint32_t Flags = 0;
+        GpuBuffer IntBias;
+        uint32_t OffIntBias = 0;
+        GpuBuffer Scale;
+        uint32_t OffScale = 0;
+        GpuBuffer FloatBias;
+        uint32_t OffFloatBias = 0;
+    };
+    Prepared Prepare(const Int8GemmProblem &p, const GpuBuffer &a, const GpuBuffer &b,
+                     const std::optional<Int8Operand> &zpA, const std::optional<Int8Operand> &zpB);
+    void CheckBindable(const std::string &operand, const GpuBuffer &buffer) const;
+    void Multiply(GpuCommandEncoder &encoder, const Int8GemmProblem &p, const GpuBuffer &a, bool aSigned,
+                  const GpuBuffer &b, bool bSigned, const GpuBuffer &c, int offsetC,
+                  const std::optional<Int8Operand> &za, const std::optional<Int8Operand> &zb, const Epilogue &epi);
+    std::pair<GpuBuffer, int> Scratch(int64_t count, const std::optional<Int8Scratch> &given);
+
+    std::shared_ptr<GpuDevice> device_;
+    Int8GemmOptions options_;
+    std::string variant_;
+    std::vector<GpuBuffer> scratch_;
+};
+
+// ------------------------------------------------------------------ DynamicQuantizeKernels (DynamicQuantizeKernels.cs)
+
+class DynamicQuantizeKernels {
+public:
+    explicit DynamicQuantizeKernels(std::shared_ptr<GpuDevice> device, int maxCachedBindGroups = 1024);
+    // DynamicQuantizeKernels.cs:47-90.
+    void Encode(GpuCommandEncoder &encoder, const GpuBuffer &x, int offsetX, int count, const GpuBuffer &y, int offsetY,
+                const GpuBuffer &scale, int offsetScale, const GpuBuffer &zeroPoint, int offsetZeroPoint);
+    int BindGroupsCreated() const { return 0; }
+    void ReleaseBindings() {}
+    void Dispose() {}
+
+private:
+    std::shared_ptr<GpuDevice> device_;
+};
+
+// ------------------------------------------------------------------ DequantizeKernels (DequantizeKernels.cs)
+
+class DequantizeKernels {
+public:
+    explicit DequantizeKernels(std::shared_ptr<GpuDevice> device, int maxCachedBindGroups = 1024);
+    // DequantizeKernels.cs:158-260 (DequantizeLinear).
+    void Encode(GpuCommandEncoder &encoder, const GpuBuffer &x, int offsetX, const std::vector<int> &shape, int axis,
+                bool perAxis, const GpuBuffer &scale, int offsetScale, const std::optional<GpuBuffer> &zeroPoint,
+                int offsetZeroPoint, const GpuBuffer &output, int offsetOutput);
+    // DequantizeKernels.cs:298-382 (QuantizeLinear).
+    void EncodeQuantize(GpuCommandEncoder &encoder, const GpuBuffer &x, int offsetX, const std::vector<int> &shape,
+                        int axis, bool perAxis, const GpuBuffer &scale, int offsetScale,
+                        const std::optional<GpuBuffer> &zeroPoint, int offsetZeroPoint, const GpuBuffer &output,
+                        int offsetOutput);
+    int BindGroupsCreated() const { return 0; }
+    void ReleaseBindings() {}
+    void Dispose() {}
+
+private:
+    std::shared_ptr<GpuDevice> device_;
+};
+
+// ------------------------------------------------------------------ shared checks (KernelSupport.cs:68-131)
+
+namespace Check {
+constexpr int64_t MaxElements = 2147483647;
+void Range(const std::string &operation, const std::string &name, int64_t bufferLength, int64_t offset, int64_t extent,
+           bool half = false);
+void RangeBytes(const std::string &operation, const std::string &name, int64_t bufferLength, int64_t offset,
+                int64_t extent);
+int64_t Product(const std::string &operation, const std::string &name, const std::vector<int> &shape);
+}  // namespace Check
+
+}  // namespace onegpu

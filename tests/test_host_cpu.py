@@ -1,0 +1,224 @@
+"""CPU tests of the boundary: the host layer rejects what the reference rejects (with the same exception and argument),
+and the C-ABI library loads, exports every entry point include/onegpu_hip.h declares, and re-validates arguments
+itself. No kernel runs here: the host-only device records work but cannot submit it."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import onegpu_hip as og
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.fixture
+def d():
+    return og.GpuDevice.CreateHostOnly()
+
+
+def buf(d, t, n):
+    return d.CreateBufferOf(t, n)
+
+
+def shape_error(fn, argument=None):
+    with pytest.raises(og.GpuKernelShapeException) as ex:
+        fn()
+    if argument is not None:
+        assert ex.value.Argument == argument, str(ex.value)
+    return ex.value
+
+
+def test_int8_gemm_bad_arguments_are_rejected(d):
+    # BadArgumentsAreRejected (Int8Tests.cs:549-574), with the argument each rejection names.
+    gemm = og.Int8Gemm(d)
+    a, b = buf(d, og.ElementType.UInt8, 64), buf(d, og.ElementType.Int8, 64)
+    c, f, fl = buf(d, og.ElementType.Int32, 64), buf(d, og.ElementType.Float32, 64), buf(d, og.ElementType.Float32, 1)
+    enc = d.BeginCommands()
+    P = og.Int8GemmProblem
+
+    def prob(m, n, k, **kw):
+        p = P(m, n, k)
+        for key, v in kw.items():
+            setattr(p, key, v)
+        return p
+
+    shape_error(lambda: gemm.EncodeInt32(enc, P(9, 9, 9), a, b, c), "OffsetA")
+    shape_error(lambda: gemm.EncodeInt32(enc, P(-1, 2, 2), a, b, c), "M")
+    shape_error(lambda: gemm.EncodeInt32(enc, prob(2, 2, 2, Batch=0), a, b, c), "Batch")
+    shape_error(lambda: gemm.EncodeInt32(enc, prob(2, 2, 2, Lda=1), a, b, c), "Lda")
+    shape_error(lambda: gemm.EncodeInt32(enc, prob(2, 2, 2, OffsetC=62), a, b, c), "c")
+    shape_error(lambda: gemm.EncodeInt32(enc, prob(8, 8, 8, OffsetA=1), a, b, c), "OffsetA")
+    shape_error(lambda: gemm.EncodeInt32(enc, P(2, 2, 2), a, b, c, og.Int8Operand(a, 63, True)), "zpA")
+    shape_error(lambda: gemm.EncodeInt32(enc, P(2, 2, 2), f, b, c), "a")
+    shape_error(lambda: gemm.EncodeFloat(enc, P(2, 8, 2), a, b, f, og.Int8Operand(fl, 0, True)), "scale")
+    shape_error(lambda: gemm.EncodeRequantized(enc, P(2, 2, 2), a, b, a, og.Int8Operand(fl, 0), 300), "zeroPointY")
+    shape_error(lambda: gemm.EncodeRequantized(enc, P(2, 2, 2), a, b, b, og.Int8Operand(fl, 0), 128), "zeroPointY")
+    # Further checks of Prepare (Int8Gemm.cs:419-484).
+    shape_error(lambda: gemm.EncodeInt32(enc, prob(2, 2, 2, Ldb=1), a, b, c), "Ldb")
+    shape_error(lambda: gemm.EncodeInt32(enc, prob(2, 2, 2, StrideA=-1), a, b, c), "StrideA")
+    shape_error(lambda: gemm.EncodeInt32(enc, P(2, 2, 2), a, c, c), "b")
+    shape_error(lambda: gemm.EncodeInt32(enc, P(2, 2, 2), a, b, f), "c")
+    shape_error(lambda: gemm.EncodeInt32(enc, prob(70000, 70000, 1), a, b, c), "Batch")
+    assert enc.DispatchCount == 0
+    # A valid call records one dispatch; M = 0 records nothing (Int8Gemm.cs:247-250).
+    gemm.EncodeInt32(enc, P(2, 2, 2), a, b, c)
+    gemm.EncodeInt32(enc, P(0, 2, 2), a, b, c)
+    assert enc.DispatchCount == 1
+    with pytest.raises(og.GpuUnsupportedException):
+        d.Submit(enc)
+
+
+def test_scratch_that_is_too_small_is_refused(d):
+    # Int8ScratchTests.cs:68-89
+    gemm = og.Int8Gemm(d)
+    a = d.CreateBuffer(np.zeros(64 * 8 + 4, np.uint8))
+    b = d.CreateBuffer(np.zeros(64 * 8 + 4, np.int8))
+    y = buf(d, og.ElementType.UInt8, 64 * 64 + 4)
+    mult = d.CreateBuffer(np.array([0.001], np.float32))
+    small = buf(d, og.ElementType.Int32, 100)
+    e = shape_error(lambda: gemm.EncodeRequantized(d.BeginCommands(), og.Int8GemmProblem(64, 64, 8), a, b, y,
+                                                   og.Int8Operand(mult, 0), 0, scratch=og.Int8Scratch(small)), "scratch")
+    assert e.Operation == "Int8Gemm"
+    assert og.Int8Gemm.ScratchElements(og.Int8GemmProblem(160, 96, 64)) == 160 * 96
+    assert og.Int8Gemm.ScratchElements(og.Int8GemmProblem(0, 96, 64)) == 0
+
+
+def test_operands_beyond_one_binding_are_unsupported():
+    # CheckBindable (Int8Gemm.cs:402-409), with a device that caps a binding as llvmpipe does (128 MB here 1 KB).
+    d = og.GpuDevice.CreateHostOnly(max_binding_bytes=1024)
+    gemm = og.Int8Gemm(d)
+    a, b = buf(d, og.ElementType.UInt8, 4096), buf(d, og.ElementType.Int8, 64)
+    c = buf(d, og.ElementType.Int32, 64)
+    with pytest.raises(og.GpuUnsupportedException) as ex:
+        gemm.EncodeInt32(d.BeginCommands(), og.Int8GemmProblem(2, 2, 2), a, b, c)
+    assert ex.value.Capability == "MaxStorageBufferBindingBytes"
+
+
+def test_variants(d):
+    assert og.Int8Gemm(d, og.Int8GemmOptions(AllowPackedDot=False)).Variant == "portable-tile64x64x16"
+    assert og.Int8Gemm(d).Variant == "mfma-i8-gfx950"
+    assert og.Int8Gemm(d).BindGroupsCreated == 0
+
+
+def test_dynamic_quantize_bad_arguments(d):
+    k = og.DynamicQuantizeKernels(d)
+    x, y = buf(d, og.ElementType.Float32, 16), buf(d, og.ElementType.UInt8, 16)
+    s, z = buf(d, og.ElementType.Float32, 1), buf(d, og.ElementType.UInt8, 4)
+    enc = d.BeginCommands()
+    shape_error(lambda: k.Encode(enc, x, 0, 0, y, 0, s, 0, z, 0), "count")
+    shape_error(lambda: k.Encode(enc, x, 1, 16, y, 0, s, 0, z, 0), "x")
+    shape_error(lambda: k.Encode(enc, x, 0, 16, y, 1, s, 0, z, 0), "y")
+    shape_error(lambda: k.Encode(enc, x, 0, 16, y, 0, s, 1, z, 0), "scale")
+    shape_error(lambda: k.Encode(enc, x, 0, 16, y, 0, s, 0, z, 4), "zeroPoint")
+    shape_error(lambda: k.Encode(enc, x, -1, 4, y, 0, s, 0, z, 0), "xOffset")
+    k.Encode(enc, x, 0, 16, y, 0, s, 0, z, 3)
+    assert enc.DispatchCount == 1
+
+
+def test_dequantize_bad_arguments(d):
+    # DequantizeTests.BadArgumentsAreRejected (DequantizeTests.cs:126-145)
+    k = og.DequantizeKernels(d)
+    x, s = buf(d, og.ElementType.UInt8, 16), buf(d, og.ElementType.Float32, 4)
+    o, big = buf(d, og.ElementType.Float32, 16), buf(d, og.ElementType.UInt32, 16)
+    ox = buf(d, og.ElementType.UInt16, 16)
+    enc = d.BeginCommands()
+    shape_error(lambda: k.Encode(enc, x, 0, [4, 4], 1, True, s, 1, None, 0, o, 0), "scale")
+    shape_error(lambda: k.Encode(enc, x, 0, [4, 4], 5, True, s, 0, None, 0, o, 0), "axis")
+    shape_error(lambda: k.Encode(enc, x, 8, [4, 4], 0, False, s, 0, None, 0, o, 0), "x")
+    shape_error(lambda: k.Encode(enc, big, 0, [4], 0, False, s, 0, None, 0, o, 0), "TIn")
+    shape_error(lambda: k.Encode(enc, x, 0, [4], 0, False, s, 0, None, 0, ox, 0), "T")
+    shape_error(lambda: k.Encode(enc, x, 0, [-1, 4], 0, False, s, 0, None, 0, o, 0), "shape[0]")
+
+
+def test_quantize_bad_arguments(d):
+    # DequantizeTests.QuantizeRejectsBadArguments (DequantizeTests.cs:291-311)
+    k = og.DequantizeKernels(d)
+    x, s = buf(d, og.ElementType.Float32, 16), buf(d, og.ElementType.Float32, 4)
+    o, o16 = buf(d, og.ElementType.UInt8, 16), buf(d, og.ElementType.Int16, 16)
+    xi = buf(d, og.ElementType.Int32, 16)
+    enc = d.BeginCommands()
+    shape_error(lambda: k.EncodeQuantize(enc, x, 0, [4, 4], 1, True, s, 1, None, 0, o, 0), "scale")
+    shape_error(lambda: k.EncodeQuantize(enc, x, 0, [4, 4], 5, True, s, 0, None, 0, o, 0), "axis")
+    shape_error(lambda: k.EncodeQuantize(enc, x, 8, [4, 4], 0, False, s, 0, None, 0, o, 0), "x")
+    shape_error(lambda: k.EncodeQuantize(enc, x, 0, [4, 4], 0, False, s, 0, None, 0, o, 3), "output")
+    shape_error(lambda: k.EncodeQuantize(enc, x, 0, [4], 0, False, s, 0, None, 0, o16, 0), "TOut")
+    shape_error(lambda: k.EncodeQuantize(enc, xi, 0, [4], 0, False, s, 0, None, 0, o, 0), "T")
+
+
+# ------------------------------------------------------------------ the C ABI
+
+
+def declared_symbols():
+    text = open(os.path.join(ROOT, "include", "onegpu_hip.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char \*)\s*(og_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(og.LIB_PATH)
+    names = declared_symbols()
+    assert len(names) >= 25, names
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+class Buf(ctypes.Structure):
+    _fields_ = [("ptr", ctypes.c_void_p), ("bytes", ctypes.c_uint64)]
+
+
+class GemmParams(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in ("M", "N", "K", "OffA", "OffB", "OffC", "StrideA", "StrideB", "StrideC",
+                                               "Lda", "Ldb", "Flags", "OffZA", "OffZB", "Epi", "OffBias", "OffScale",
+                                               "OffFBias", "GridX")]
+
+
+def test_abi_validates_before_touching_a_device():
+    # The C ABI re-checks ranges itself: with no context it reports the bad argument, or, when every argument is
+    # valid, that there is no device. Host addresses stand in for device ones: nothing is dereferenced.
+    lib = ctypes.CDLL(og.LIB_PATH)
+    lib.og_int8_gemm.argtypes = [ctypes.c_void_p, ctypes.POINTER(GemmParams), ctypes.c_uint32] + [Buf] * 8
+    lib.og_last_error_argument.restype = ctypes.c_char_p
+    lib.og_last_error_argument.argtypes = [ctypes.c_void_p]
+    lib.og_last_error.restype = ctypes.c_char_p
+    lib.og_last_error.argtypes = [ctypes.c_void_p]
+    host = (ctypes.c_uint8 * 4096)()
+    addr = ctypes.addressof(host)
+    none = Buf(None, 0)
+
+    def call(p, a=64, b=64, c=256, batch=1, **kw):
+        bufs = dict(A=Buf(addr, a), B=Buf(addr, b), C=Buf(addr, c), ZA=none, ZB=none, bias=none, scale=none, fbias=none)
+        bufs.update(kw)
+        st = lib.og_int8_gemm(None, ctypes.byref(p), batch, *bufs.values())
+        return st, lib.og_last_error_argument(None).decode()
+
+    p = GemmParams(M=4, N=4, K=4, Lda=4, Ldb=4, StrideC=16)
+    assert call(p) == (6, "ctx")                                  # valid: no device
+    assert call(p, a=15) == (1, "OffsetA")                        # A one byte short
+    assert call(p, b=15) == (1, "OffsetB")
+    assert call(p, c=63) == (1, "c")
+    assert call(GemmParams(M=4, N=4, K=4, Lda=3, Ldb=4))[1] == "Lda"
+    assert call(GemmParams(M=4, N=4, K=4, Flags=0x08))[1] == "zpA"  # zero point flagged but absent
+    assert call(GemmParams(M=4, N=4, K=4, Epi=0x1))[1] == "scale"
+    assert call(GemmParams(M=4, N=4, K=4, Epi=0x4))[1] == "Epi"
+    assert call(GemmParams(M=4, N=4, K=4, Flags=0x10000))[1] == "Flags"
+    assert call(p, batch=0)[1] == "Batch"
+    assert call(GemmParams(M=0x80000000, N=1, K=1))[1] == "M"
+    st, _ = call(GemmParams(M=4, N=4, K=4, Flags=0x08 | 0x10), ZA=Buf(addr, 3))
+    assert lib.og_last_error_argument(None).decode() == "zpA"
+
+
+def test_kernel_choice_is_reported():
+    lib = ctypes.CDLL(og.LIB_PATH)
+    lib.og_int8_gemm_kernel_name.argtypes = [ctypes.POINTER(GemmParams), ctypes.c_uint32, ctypes.c_char_p, ctypes.c_size_t]
+    out = ctypes.create_string_buffer(64)
+
+    def name(**kw):
+        lib.og_int8_gemm_kernel_name(ctypes.byref(GemmParams(**kw)), 1, out, 64)
+        return out.value.decode()
+
+    assert name(M=4096, N=4096, K=4096).startswith("mfma-i8-tile")
+    assert name(M=1, N=11008, K=4096) == "mfma-i8-rows16-splitk"
+    assert name(M=16, N=11008, K=4096).startswith("mfma-i8-rows16")
+    assert name(M=1, N=11008, K=4096, Flags=0x4).startswith("mfma-i8-tile")     # transposed B: tiled
+    assert name(M=1, N=11008, K=4096, Flags=0x400) == "portable-tile64x64x16"

@@ -1,0 +1,272 @@
+"""GPU parity of the int8 path against the CPU oracle, through the host layer and the C ABI: the reference's
+Int8Tests (tests/RecursiveAI.OneGpu.Kernels.Tests/Int8Tests.cs), case for case, bit-exact."""
+import numpy as np
+import pytest
+
+import cases
+import oracle
+import onegpu_hip as og
+from gpu_rig import as_i8, as_u8, configs, device, run, run_int32, say, to_problem, binding, abi, check
+
+pytestmark = pytest.mark.gpu
+
+
+def test_closed_form():
+    # MultiDeviceTests.cs:30-31, 40, 53-55
+    d = device()
+    with og.Int8Gemm(d) as gemm:
+        a = d.CreateBuffer(np.array([1, 2, 3, 4, 5, 6], np.uint8))
+        b = d.CreateBuffer(np.array([1, -1, 2, -2, 3, -3], np.int8))
+        c = d.CreateBufferOf(og.ElementType.Int32, 6)
+        for _ in range(3):
+            run(d, lambda e: gemm.EncodeInt32(e, og.Int8GemmProblem(2, 3, 2), a, b, c))
+        assert c.Read().tolist() == [-3, 5, -4, -5, 9, -6]
+
+
+@pytest.mark.parametrize("config", ["default", "portable", "tiled only", "split k"])
+def test_edge_shapes_are_bit_exact(config):
+    # EdgeShapesAreBitExact (Int8Tests.cs:214-283): every case, each kernel forced in turn.
+    d = device()
+    gemm = dict(configs(d, True))[config]
+    bad_total = 0
+    kernels = set()
+    for i, c in enumerate(cases.edge_cases()):
+        say(f"edge [{config}] case {i} {c.name} signed {c.a_signed}/{c.b_signed} zp {c.za_mode}/{c.zb_mode}")
+        bad, k = run_int32(d, gemm, c, i + 1)
+        kernels.add(k)
+        if bad:
+            say(f"MISMATCH [{config}] {c.name}: {bad} elements")
+        bad_total += bad
+    say(f"ROW int8 gemm | {config} | kernels {sorted(kernels)} | mismatching int32 sums {bad_total}")
+    assert bad_total == 0
+
+
+def test_model_shapes_are_bit_exact():
+    # ModelShapesAreBitExact (Int8Tests.cs:285-317): u8 activations with a zero point, int8 weights stored N x K,
+    # plus the same shapes with the weights stored K x N (the layout of the benchmark configurations).
+    d = device()
+    bad_total = 0
+    for name, m, n, k in cases.MODEL_SHAPES:
+        for trans in (True, False):
+            c = cases.model_case(name, m, n, k)
+            if not trans:
+                c.p = cases.problem(m, n, k)
+            data = cases.case_data(c, m + n + k)
+            want = cases.reference_sums(c, data)
+            for config, gemm in configs(d, m <= 128):
+                say(f"model {name} trans {trans} [{config}]")
+                bad, kernel = run_int32(d, gemm, c, m + n + k, want)
+                say(f"ROW int8 gemm | u8 x i8 | {name} trans {trans}, {config} | {kernel} | mismatches {bad}")
+                bad_total += bad
+    assert bad_total == 0
+
+
+def test_forcing_the_dot_variant_off_changes_nothing():
+    # Int8Tests.cs:319-332
+    d = device()
+    chosen = og.Int8Gemm(d)
+    forced = og.Int8Gemm(d, og.Int8GemmOptions(AllowPackedDot=False))
+    c = cases.Case("forced", cases.problem(70, 90, 100), False, True, 1, 2)
+    b1, _ = run_int32(d, chosen, c, 5)
+    b2, _ = run_int32(d, forced, c, 5)
+    assert b1 + b2 == 0
+    assert forced.Variant == "portable-tile64x64x16"
+    assert chosen.Variant != forced.Variant
+
+
+def _float_case(d, gemm, m, n, k, scale_vec, with_ib, with_fb, seed):
+    """FloatCase (Int8Tests.cs:334-373)."""
+    a, b, za, zb, scale, ib, fb = cases.float_case_data(m, n, k, scale_vec, seed)
+    p = cases.problem(m, n, k)
+    want = oracle.int8_gemm(p, a, False, b, True, (za, False, 0), (zb, True, 0))
+    expected = oracle.float_epilogue(want, n, scale, scale_vec, ib if with_ib else None, fb if with_fb else None)
+    ba, bb = d.CreateBuffer(as_u8(a)), d.CreateBuffer(as_i8(b))
+    bza, bzb = d.CreateBuffer(as_u8(za)), d.CreateBuffer(as_i8(zb))
+    bs, bib, bfb = d.CreateBuffer(scale), d.CreateBuffer(ib), d.CreateBuffer(fb)
+    bc = d.CreateBufferOf(og.ElementType.Float32, m * n)
+    run(d, lambda e: gemm.EncodeFloat(e, to_problem(p), ba, bb, bc, og.Int8Operand(bs, 0, scale_vec),
+                                      og.Int8Operand(bza, 0), og.Int8Operand(bzb, 0, True),
+                                      og.Int8Operand(bfb, 0, True) if with_fb else None,
+                                      og.Int8Operand(bib, 0, True) if with_ib else None))
+    got = bc.Read()
+    same = np.where(np.isnan(expected), np.isnan(got), got.view(np.uint32) == expected.view(np.uint32))
+    return int(np.count_nonzero(~same))
+
+
+def _requant_case(d, gemm, m, n, k, mult_vec, unsigned, zero_y, with_bias, seed, a_signed, b_signed):
+    """RequantCase (Int8Tests.cs:375-466)."""
+    a, b, za, mult, ib = cases.requant_case_data(m, n, k, mult_vec, seed)
+    p = cases.problem(m, n, k, off_c=3)
+    want = oracle.int8_gemm(p, a, a_signed, b, b_signed, (za, False, 0))
+    expected = oracle.requant_array(want, n, mult, mult_vec, zero_y, unsigned, ib if with_bias else None)
+    out = np.full(og.padded_bool_length(3 + m * n + 3) + 4, 0xA7, np.uint8)
+    ba = d.CreateBuffer(as_i8(a) if a_signed else as_u8(a))
+    bb = d.CreateBuffer(as_i8(b) if b_signed else as_u8(b))
+    bz = d.CreateBuffer(as_i8(za) if a_signed else as_u8(za))
+    bm, bib = d.CreateBuffer(mult), d.CreateBuffer(ib)
+    y = d.CreateBuffer(out if unsigned else out.view(np.int8))
+    run(d, lambda e: gemm.EncodeRequantized(e, to_problem(p), ba, bb, y, og.Int8Operand(bm, 0, mult_vec), zero_y,
+                                            og.Int8Operand(bz, 0), None,
+                                            og.Int8Operand(bib, 0, True) if with_bias else None))
+    got = y.Read().view(np.uint8)
+    bad = int(np.count_nonzero(got[3:3 + m * n] != expected))
+    bad += int(np.count_nonzero(got[:3] != 0xA7)) + int(np.count_nonzero(got[3 + m * n:] != 0xA7))
+    return bad
+
+
+def test_float_and_requantized_forms_are_bit_exact():
+    # FloatAndRequantizedFormsAreBitExact (Int8Tests.cs:468-501)
+    d = device()
+    gemm = og.Int8Gemm(d)
+    bad_f = bad_q = 0
+    seed = 10
+    for (m, n, k) in cases.FLOAT_SHAPES:
+        for vec in (False, True):
+            for ib, fb in ((False, False), (True, False), (False, True), (True, True)):
+                say(f"float {m}x{n}x{k} vec {vec} ib {ib} fb {fb}")
+                bad_f += _float_case(d, gemm, m, n, k, vec, ib, fb, seed)
+                seed += 1
+        for vec in (False, True):
+            for unsigned, zero in cases.REQUANT_OUT:
+                say(f"requant {m}x{n}x{k} vec {vec} u8 {unsigned} zero {zero}")
+                bad_q += _requant_case(d, gemm, m, n, k, vec, unsigned, zero, (seed & 1) == 0, seed, (seed & 2) != 0,
+                                       (seed & 4) != 0)
+                seed += 1
+    say(f"ROW float bits {bad_f} requant bytes {bad_q}")
+    assert bad_f + bad_q == 0
+
+
+def test_requantization_rounds_half_to_even_and_saturates():
+    # Int8Tests.cs:503-547
+    d = device()
+    gemm = og.Int8Gemm(d)
+    bad = 0
+    for mult, zero_y, unsigned in cases.REQUANT_TIES:
+        for av in range(-9, 10):
+            a = np.zeros(4, np.int8)
+            a[0] = av
+            b = np.zeros(4, np.int8)
+            b[0] = 1
+            with np.errstate(all="ignore"):
+                want = oracle.requant(av, mult, zero_y, unsigned) & 0xFF
+            ba, bb = d.CreateBuffer(a), d.CreateBuffer(b)
+            bm = d.CreateBuffer(np.array([mult], np.float32))
+            y = d.CreateBufferOf(og.ElementType.UInt8 if unsigned else og.ElementType.Int8, 4)
+            run(d, lambda e: gemm.EncodeRequantized(e, og.Int8GemmProblem(1, 1, 1), ba, bb, y, og.Int8Operand(bm, 0), zero_y))
+            bad += int(y.Read().view(np.uint8)[0] != want)
+    assert bad == 0
+
+
+def test_dynamic_quantize_is_bit_exact():
+    # DynamicQuantizeIsBitExact (Int8Tests.cs:617-703)
+    d = device()
+    k = og.DynamicQuantizeKernels(d)
+    bad = 0
+    OffX, OffY, OffS, OffZ = 1, 3, 2, 5
+    for count, kind, seed in cases.dq_cases():
+        say(f"dq count {count} kind {kind}")
+        x = oracle.dq_input(count, seed, kind)
+        wy, ws, wz = oracle.dynamic_quantize(x)
+        xs = np.zeros(count + OffX, np.float32)
+        xs[OffX:] = x
+        bx = d.CreateBuffer(xs)
+        y_init = np.full(((OffY + count + 3) & ~3) + 4, 0x3C, np.uint8)
+        by = d.CreateBuffer(y_init)
+        bs = d.CreateBufferOf(og.ElementType.Float32, 4)
+        bz = d.CreateBuffer(np.full(8, 0xEE, np.uint8))
+        run(d, lambda e: k.Encode(e, bx, OffX, count, by, OffY, bs, OffS, bz, OffZ))
+        y, sc, zp = by.Read(), bs.Read(), bz.Read()
+        here = int(np.count_nonzero(y[OffY:OffY + count] != wy))
+        here += int(sc[OffS].view(np.uint32) != np.float32(ws).view(np.uint32)) + int(zp[OffZ] != wz)
+        here += int(np.count_nonzero(y[:OffY] != 0x3C)) + int(np.count_nonzero(y[OffY + count:] != 0x3C))
+        here += int(np.count_nonzero(np.delete(zp, OffZ) != 0xEE))
+        if here:
+            say(f"MISMATCH dq count {count} kind {kind}: {here} (scale {sc[OffS]!r} want {ws!r}, zero {zp[OffZ]} want {wz})")
+        bad += here
+    assert bad == 0
+
+
+def test_dynamic_quantize_special_values():
+    d = device()
+    k = og.DynamicQuantizeKernels(d)
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    for x in ([0.0], [-0.0, 0.0], [nan, nan], [1.0, nan, -1.0], [inf, 1.0], [-inf, 2.0], [1e-42, 3e-42], [-1e-42],
+              [1e30, -1e30], [255.0, 0.0], [-3.0, -2.0], [3e38, -3e38]):
+        x = np.array(x, np.float32)
+        wy, ws, wz = oracle.dynamic_quantize(x)
+        bx, by = d.CreateBuffer(x), d.CreateBufferOf(og.ElementType.UInt8, 4)
+        bs, bz = d.CreateBufferOf(og.ElementType.Float32, 1), d.CreateBufferOf(og.ElementType.UInt8, 4)
+        run(d, lambda e: k.Encode(e, bx, 0, x.size, by, 0, bs, 0, bz, 0))
+        assert by.Read()[:x.size].tolist() == wy.tolist(), x
+        s = bs.Read()[0]
+        assert (np.isnan(s) and np.isnan(ws)) or s.view(np.uint32) == np.float32(ws).view(np.uint32), x
+        assert bz.Read()[0] == wz, x
+
+
+def test_dynamic_quantize_feeds_the_product_without_leaving_the_device():
+    # Int8Tests.cs:705-751: DQ, the on-device scale product, MatMulIntegerToFloat, in stream order.
+    d = device()
+    dq, gemm = og.DynamicQuantizeKernels(d), og.Int8Gemm(d)
+    M, N, K = 128, 384, 384
+    x = oracle.rig_random(M * K, 3, -3.0, 5.0)
+    wy, wscale, wzero = oracle.dynamic_quantize(x)
+    w = oracle.bytes_(N * K, 4)
+    wscales = (np.float32(0.002) + (np.arange(N) % 17).astype(np.float32) * np.float32(1e-4)).astype(np.float32)
+    p = cases.problem(M, N, K, trans_b=True)
+    sums = oracle.int8_gemm(p, wy, False, w, True, (np.array([wzero], np.uint8), False, 0))
+    bx, by = d.CreateBuffer(x), d.CreateBufferOf(og.ElementType.UInt8, M * K)
+    bs, bz = d.CreateBufferOf(og.ElementType.Float32, 1), d.CreateBufferOf(og.ElementType.UInt8, 1)
+    bw, bws = d.CreateBuffer(as_i8(w)), d.CreateBuffer(wscales)
+    bscale, bc = d.CreateBufferOf(og.ElementType.Float32, N), d.CreateBufferOf(og.ElementType.Float32, M * N)
+    run(d, lambda e: dq.Encode(e, bx, 0, M * K, by, 0, bs, 0, bz, 0))
+    check(abi().og_util_scale_product(d.Context, binding(bs), binding(bws), N, binding(bscale)), d)
+    run(d, lambda e: gemm.EncodeFloat(e, to_problem(p), by, bw, bc, og.Int8Operand(bscale, 0, True), og.Int8Operand(bz, 0)))
+    got = bc.Read()
+    want = sums.astype(np.float32) * (np.float32(wscale) * wscales[np.arange(M * N) % N])
+    assert np.count_nonzero(got.view(np.uint32) != want.astype(np.float32).view(np.uint32)) == 0
+
+
+def test_products_wider_than_one_grid_axis_are_bit_exact():
+    # ConvIntegerTests.cs:343-390: more than 65535 tiles along one axis.
+    d = device()
+    for (m, n) in ((3, 4_300_001), (4_300_001, 3), (2, 4_194_241)):
+        k = 5
+        a, b = oracle.bytes_(m * k, 11), oracle.bytes_(k * n, 12)
+        za, zb = oracle.bytes_(1, 13), oracle.bytes_(n, 14)
+        p = oracle.Gemm(m, n, k)
+        want = oracle.int8_gemm(p, a, False, b, True, (za, False, 0), (zb, True, 0))
+        ba, bb = d.CreateBuffer(as_u8(a)), d.CreateBuffer(as_i8(b))
+        bza, bzb = d.CreateBuffer(as_u8(za)), d.CreateBuffer(as_i8(zb))
+        for opts in (og.Int8GemmOptions(), og.Int8GemmOptions(AllowPackedDot=False), og.Int8GemmOptions(Tile=64)):
+            say(f"wide {m}x{n} allow {opts.AllowPackedDot} tile {opts.Tile}")
+            gemm = og.Int8Gemm(d, opts)
+            bc = d.CreateBufferOf(og.ElementType.Int32, m * n)
+            run(d, lambda e: gemm.EncodeInt32(e, og.Int8GemmProblem(m, n, k), ba, bb, bc, og.Int8Operand(bza, 0),
+                                              og.Int8Operand(bzb, 0, True)))
+            got = bc.Read()
+            assert np.count_nonzero(got != want) == 0, (m, n, d.LastKernel)
+            bc.Dispose()
+
+
+def test_scratch_semantics():
+    # Int8ScratchTests.cs:27-89
+    d = device()
+    N, K, Small, Large = 96, 64, 32, 160
+    a = d.CreateBuffer(oracle.bytes_(Large * K + 4, 1))
+    b = d.CreateBuffer(np.zeros(N * K + 4, np.int8))
+    y = d.CreateBufferOf(og.ElementType.UInt8, Large * N + 4)
+    mult = og.Int8Operand(d.CreateBuffer(np.array([0.001], np.float32)), 0)
+    need = og.Int8Gemm.ScratchElements(og.Int8GemmProblem(Large, N, K))
+    assert need == Large * N
+    scratch = d.CreateBufferOf(og.ElementType.Int32, need)
+    gemm = og.Int8Gemm(d)
+    for m in (Small, Large):
+        run(d, lambda e: gemm.EncodeRequantized(e, og.Int8GemmProblem(m, N, K), a, b, y, mult, 3, scratch=og.Int8Scratch(scratch)))
+    assert gemm.BindGroupsCreated == 0
+    gemm.ReserveScratch(need)
+    run(d, lambda e: gemm.EncodeRequantized(e, og.Int8GemmProblem(Large, N, K), a, b, y, mult, 3))
+    assert y.Read()[:Large * N].tolist() == [3] * (Large * N)   # B = 0: every sum is 0, so y = zeroPointY
+    small = d.CreateBufferOf(og.ElementType.Int32, 100)
+    with pytest.raises(og.GpuKernelShapeException) as ex:
+        gemm.EncodeRequantized(d.BeginCommands(), og.Int8GemmProblem(64, 64, 8), a, b, y, mult, 0, scratch=og.Int8Scratch(small))
+    assert ex.value.Argument == "scratch"
