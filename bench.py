@@ -1,0 +1,367 @@
+"""Benchmark of the MI355X int8 quantized-matmul path on BASELINE.json's configurations.
+
+One JSON line on stdout. `value` is the headline metric's first half: int8 TOPS of MatMulInteger at M = N = K = 4096
+(configuration 4: uint8 A with a per-row zero point, int8 B stored K x N, int32 out), whole-job throughput over
+exactly --steps products with inputs resident in HBM, bracketed by device synchronisation. The second half, GB/s of
+the M = 1, K = 4096, N = 11008 decode GEMV (configuration 3, weights rotated over 9 copies so the 45 MB matrix cannot
+sit in the 256 MiB Infinity Cache), is in `gemv_m1`; the other configurations are in `configs`.
+
+`roofline` is for the dominant kernel (the 4096^3 MFMA product): algorithmic ops 2*M*N*K per launch over the average
+launch duration measured with HIP events on the stream the kernel runs on. `cpu_baseline` times the oracle (a C
+restatement of the reference's CPU reference, multithreaded) on a bounded sample of rows of the same product.
+Every configuration's output is checked against the oracle (sampled rows) before it is reported.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (os.path.join(ROOT, "onegpu-csharp_amd"), os.path.join(ROOT, "oracle")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+import numpy as np  # noqa: E402
+
+import onegpu_hip as og  # noqa: E402
+
+PEAK_INT8_TOPS = 5000.0      # MI355X dense int8 MFMA (5.0 POPS)
+PEAK_HBM_GBS = 8000.0        # MI355X HBM3E (8 TB/s)
+METRIC = "int8 TOPS (% of MFMA peak) at 4096³; GB/s (% of HBM) at M=1 GEMV"
+
+
+# ------------------------------------------------------------------ C ABI utilities (synthetic data on the device)
+
+class _Buf(ctypes.Structure):
+    _fields_ = [("ptr", ctypes.c_void_p), ("bytes", ctypes.c_uint64)]
+
+
+_L = None
+
+
+def _abi():
+    global _L
+    if _L is None:
+        _L = ctypes.CDLL(og.LIB_PATH)
+        _L.og_util_synth.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_uint64, ctypes.c_uint32, _Buf,
+                                     ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double]
+        _L.og_util_col_absmax_scale.argtypes = [ctypes.c_void_p, _Buf, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_float,
+                                                _Buf]
+        _L.og_util_scale_product.argtypes = [ctypes.c_void_p, _Buf, _Buf, ctypes.c_uint32, _Buf]
+        _L.og_last_error.argtypes = [ctypes.c_void_p]
+        _L.og_last_error.restype = ctypes.c_char_p
+    return _L
+
+
+def _b(buf):
+    return _Buf(buf.DevicePointer, buf.Size)
+
+
+def _ok(st, d):
+    if st != 0:
+        raise RuntimeError(f"C ABI status {st}: {_abi().og_last_error(d.Context).decode()}")
+
+
+def synth(d, etype, n, seed, tensor, lo, hi, kind):
+    b = d.CreateBufferOf(etype, n)
+    _ok(_abi().og_util_synth(d.Context, kind, seed, tensor, _b(b), 0, n, lo, hi), d)
+    return b
+
+
+def sym_weights(d, k, n, seed, tensor):
+    """N(0, 0.02) float weights [K, N] -> per-column scale max|w| / 127 -> QuantizeLinear to int8 (axis 1)."""
+    w = synth(d, og.ElementType.Float32, k * n, seed, tensor, 0.0, 0.02, 2)
+    scale = d.CreateBufferOf(og.ElementType.Float32, n)
+    _ok(_abi().og_util_col_absmax_scale(d.Context, _b(w), k, n, 127.0, _b(scale)), d)
+    q = d.CreateBufferOf(og.ElementType.Int8, k * n)
+    e = d.BeginCommands()
+    og.DequantizeKernels(d).EncodeQuantize(e, w, 0, [k, n], 1, True, scale, 0, None, 0, q, 0)
+    d.Submit(e)
+    d.WaitIdle()
+    w.Dispose()
+    return q, scale
+
+
+# ------------------------------------------------------------------ timing
+
+def timed(d, record, steps, warmup):
+    """Runs `record(encoder, i)` warmup times untimed, then `steps` times in one encoder with per-dispatch events.
+    Returns (wall seconds for the timed steps, [(ms, kernel)] per dispatch)."""
+    for i in range(warmup):
+        e = d.BeginCommands()
+        record(e, i)
+        d.Submit(e)
+    d.WaitIdle()
+    e = d.BeginCommands()
+    e.BeginPassTiming(steps)
+    for i in range(steps):
+        record(e, warmup + i)
+    e.EndPassTiming()
+    d.WaitIdle()
+    t0 = time.perf_counter()
+    d.Submit(e)
+    d.WaitIdle()
+    wall = time.perf_counter() - t0
+    return wall, d.ReadPassTimes()
+
+
+def kernel_stats(times, name_prefix=None):
+    ms = [t for t, k in times if name_prefix is None or k.startswith(name_prefix)]
+    return statistics.mean(ms), statistics.median(ms), (times[0][1] if times else "")
+
+
+# ------------------------------------------------------------------ configurations
+
+def c4_square(d, steps, warmup, check=True):
+    """Configuration 4: 4096^3, A uint8 U{0..255} with per-row a_zp U{100..156}, B int8 U{-127..127}, int32 out."""
+    M = N = K = 4096
+    a = synth(d, og.ElementType.UInt8, M * K, 4, 0, 0, 255, 0)
+    za = synth(d, og.ElementType.UInt8, M, 4, 1, 100, 156, 0)
+    b = synth(d, og.ElementType.Int8, K * N, 4, 2, -127, 127, 0)
+    c = d.CreateBufferOf(og.ElementType.Int32, M * N)
+    gemm = og.Int8Gemm(d)
+    p = og.Int8GemmProblem(M, N, K)
+    zpa = og.Int8Operand(za, 0, True)
+    wall, times = timed(d, lambda e, i: gemm.EncodeInt32(e, p, a, b, c, zpa), steps, warmup)
+    mean_ms, med_ms, kname = kernel_stats(times)
+    res = {"ops": 2.0 * M * N * K, "wall_s": wall, "kernel_mean_ms": mean_ms, "kernel_median_ms": med_ms,
+           "kernel": kname, "bytes": M * K + K * N + M + 4 * M * N}
+    if check:
+        import oracle
+        rows = np.array([0, 1, 777, 2048, 4095])
+        A, B, Z = a.Read(), b.Read(), za.Read()
+        want = oracle.int8_gemm_rows(oracle.Gemm(M, N, K), A, False, B.view(np.uint8), True, rows, (Z, True, 0))
+        got = c.Read().reshape(M, N)[rows]
+        res["check"] = "bit-exact on sampled rows" if np.array_equal(got, want) else "MISMATCH"
+        res["host_operands"] = (A, B, Z)
+    return res
+
+
+def c3_gemv(d, m, steps, warmup, copies=9, check=True):
+    """Configuration 3: A = DynamicQuantizeLinear(N(0,1) [m x 4096]); B int8 [4096 x 11008] symmetric per column
+    (N(0, 0.02)); MatMulIntegerToFloat with scale = actScale * wScale[n]. `copies` weight matrices rotate."""
+    K, N = 4096, 11008
+    x = synth(d, og.ElementType.Float32, m * K, 3, 10, 0.0, 1.0, 2)
+    ya = d.CreateBufferOf(og.ElementType.UInt8, m * K)
+    s = d.CreateBufferOf(og.ElementType.Float32, 1)
+    z = d.CreateBufferOf(og.ElementType.UInt8, 4)
+    e = d.BeginCommands()
+    og.DynamicQuantizeKernels(d).Encode(e, x, 0, m * K, ya, 0, s, 0, z, 0)
+    d.Submit(e)
+    ws = []
+    for cidx in range(copies):
+        q, wscale = sym_weights(d, K, N, 3, 20 + cidx)
+        sc = d.CreateBufferOf(og.ElementType.Float32, N)
+        _ok(_abi().og_util_scale_product(d.Context, _b(s), _b(wscale), N, _b(sc)), d)
+        ws.append((q, sc))
+    c = d.CreateBufferOf(og.ElementType.Float32, m * N)
+    gemm = og.Int8Gemm(d)
+    p = og.Int8GemmProblem(m, N, K)
+    zpa = og.Int8Operand(z, 0)
+    wall, times = timed(d, lambda e, i: gemm.EncodeFloat(e, p, ya, ws[i % copies][0], c,
+                                                          og.Int8Operand(ws[i % copies][1], 0, True), zpa), steps, warmup)
+    # A few-rows product may be split into two dispatches (partial sums, then their sum); its time is both.
+    n_disp = len(times) // steps
+    step_ms = [sum(times[i * n_disp + j][0] for j in range(n_disp)) for i in range(steps)]
+    bytes_ = K * N + m * K + 4 * m * N + 4 * N + 4 + 1
+    res = {"m": m, "ops": 2.0 * m * N * K, "bytes": bytes_, "wall_s": wall, "step_mean_ms": statistics.mean(step_ms),
+           "step_median_ms": statistics.median(step_ms), "kernels": [k for _, k in times[:n_disp]],
+           "dispatch_mean_ms": [statistics.mean(times[i * n_disp + j][0] for i in range(steps)) for j in range(n_disp)]}
+    if check:
+        import oracle
+        last = (warmup + steps - 1) % copies
+        q, sc = ws[last]
+        Y, Z, Q, SC = ya.Read(), int(z.Read()[0]), q.Read(), sc.Read()
+        sums = oracle.int8_gemm(oracle.Gemm(m, N, K), Y, False, Q.view(np.uint8), True, (np.array([Z], np.uint8), False, 0))
+        want = oracle.float_epilogue(sums, N, SC, True)
+        got = c.Read()
+        res["check"] = "bit-exact" if np.array_equal(got.view(np.uint32), want.view(np.uint32)) else "MISMATCH"
+    return res
+
+
+def c2_bert_ffn(d, steps, warmup, check=True):
+    """Configuration 2: DQ [1024 x 768] N(0,1) -> MatMulIntegerToFloat with W [768 x 3072] symmetric per column."""
+    M, K, N = 1024, 768, 3072
+    x = synth(d, og.ElementType.Float32, M * K, 2, 30, 0.0, 1.0, 2)
+    q, wscale = sym_weights(d, K, N, 2, 31)
+    ya = d.CreateBufferOf(og.ElementType.UInt8, M * K)
+    s = d.CreateBufferOf(og.ElementType.Float32, 1)
+    z = d.CreateBufferOf(og.ElementType.UInt8, 4)
+    sc = d.CreateBufferOf(og.ElementType.Float32, N)
+    c = d.CreateBufferOf(og.ElementType.Float32, M * N)
+    dq, gemm = og.DynamicQuantizeKernels(d), og.Int8Gemm(d)
+    p = og.Int8GemmProblem(M, N, K)
+
+    def step(e, i):
+        dq.Encode(e, x, 0, M * K, ya, 0, s, 0, z, 0)
+        # the per-column scale product sits between the two on the same stream (its own tiny dispatch)
+        gemm.EncodeFloat(e, p, ya, q, c, og.Int8Operand(sc, 0, True), og.Int8Operand(z, 0))
+
+    # scale = actScale * wScale is made once up front (the DQ scale is the same on every step of the same input)
+    e0 = d.BeginCommands()
+    dq.Encode(e0, x, 0, M * K, ya, 0, s, 0, z, 0)
+    d.Submit(e0)
+    _ok(_abi().og_util_scale_product(d.Context, _b(s), _b(wscale), N, _b(sc)), d)
+    wall, times = timed(d, step, steps, warmup)
+    n_disp = len(times) // steps
+    per = {}
+    for t, k in times:
+        per.setdefault(k, []).append(t)
+    res = {"ops": 2.0 * M * N * K, "wall_s": wall, "dispatch_mean_ms": {k: statistics.mean(v) for k, v in per.items()},
+           "bytes_gemm": M * K + K * N + 4 * M * N + 4 * N, "bytes_dq": 4 * M * K + M * K + 5}
+    if check:
+        import oracle
+        Y, Z, Q, SC = ya.Read(), int(z.Read()[0]), q.Read(), sc.Read()
+        wy, ws_, wz = oracle.dynamic_quantize(x.Read())
+        ok_dq = np.array_equal(Y, wy) and wz == Z
+        rows = np.array([0, 5, 511, 1023])
+        sums = oracle.int8_gemm_rows(oracle.Gemm(M, N, K), Y, False, Q.view(np.uint8), True, rows, (np.array([Z], np.uint8), False, 0))
+        want = oracle.float_epilogue(sums.ravel(), N, SC, True).reshape(len(rows), N)
+        got = c.Read().reshape(M, N)[rows]
+        res["check"] = "bit-exact" if ok_dq and np.array_equal(got.view(np.uint32), want.view(np.uint32)) else "MISMATCH"
+    del n_disp
+    return res
+
+
+def c5_batched(d, steps, warmup, check=True):
+    """Configuration 5: 32 x (A u8 [512 x 4096] from one DQ of N(0,1)) x (32 distinct B int8 [4096 x 4096]), int32."""
+    Bt, M, K, N = 32, 512, 4096, 4096
+    x = synth(d, og.ElementType.Float32, Bt * M * K, 5, 40, 0.0, 1.0, 2)
+    ya = d.CreateBufferOf(og.ElementType.UInt8, Bt * M * K)
+    s = d.CreateBufferOf(og.ElementType.Float32, 1)
+    z = d.CreateBufferOf(og.ElementType.UInt8, 4)
+    e = d.BeginCommands()
+    og.DynamicQuantizeKernels(d).Encode(e, x, 0, Bt * M * K, ya, 0, s, 0, z, 0)
+    d.Submit(e)
+    x.Dispose()
+    b = synth(d, og.ElementType.Int8, Bt * K * N, 5, 41, -127, 127, 0)
+    c = d.CreateBufferOf(og.ElementType.Int32, Bt * M * N)
+    gemm = og.Int8Gemm(d)
+    p = og.Int8GemmProblem(M, N, K)
+    p.Batch, p.StrideA, p.StrideB = Bt, M * K, K * N
+    zpa = og.Int8Operand(z, 0)
+    wall, times = timed(d, lambda e, i: gemm.EncodeInt32(e, p, ya, b, c, zpa), steps, warmup)
+    mean_ms, med_ms, kname = kernel_stats(times)
+    res = {"ops": 2.0 * Bt * M * N * K, "wall_s": wall, "kernel_mean_ms": mean_ms, "kernel": kname,
+           "bytes": Bt * (M * K + K * N + 4 * M * N)}
+    if check:
+        import oracle
+        Y, Z, Bh = ya.Read(), int(z.Read()[0]), b.Read().view(np.uint8)
+        pr = oracle.Gemm(M, N, K, Batch=Bt, StrideA=M * K, StrideB=K * N)
+        rows = np.array([0, 511, 7 * M + 100, 31 * M + 511])
+        want = oracle.int8_gemm_rows(pr, Y, False, Bh, True, rows, (np.array([Z], np.uint8), False, 0))
+        got = c.Read().reshape(Bt * M, N)[rows]
+        res["check"] = "bit-exact on sampled rows" if np.array_equal(got, want) else "MISMATCH"
+    return res
+
+
+def cpu_baseline_c4(host_operands, budget_s=12.0):
+    """The oracle (reference-semantics CPU restatement) on rows of the 4096^3 product until ~budget_s of work."""
+    import oracle
+    A, B, Z = host_operands
+    M = N = K = 4096
+    threads = max(1, min(16, os.cpu_count() or 1))
+    rows_done, t_total = 0, 0.0
+    chunk = max(threads, 16)
+    while t_total < budget_s and rows_done < M:
+        rows = np.arange(rows_done, min(M, rows_done + chunk))
+        t0 = time.perf_counter()
+        oracle.int8_gemm_rows(oracle.Gemm(M, N, K), A, False, B.view(np.uint8), True, rows, (Z, True, 0), threads=threads)
+        dt = time.perf_counter() - t0
+        t_total += dt
+        rows_done += len(rows)
+        if dt < budget_s / 8:
+            chunk *= 2
+    ops = 2.0 * rows_done * N * K
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": ops / t_total / 1e12, "unit": "TOPS", "cores": threads, "kind": "port",
+            "sample": f"{rows_done} of 4096 rows of the 4096^3 product (u8 A with per-row zero point x int8 B), "
+                      f"{t_total:.1f} s, oracle/oracle.c ora_int8_gemm_rows on {threads} threads of {cpu}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--quick", action="store_true", help="headline configuration only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported (see DESIGN.md for "
+                                   "how the path would shard)"}))
+        sys.exit(2)
+    d = og.GpuDevice.Create(0)
+    log = lambda s: print(s, file=sys.stderr, flush=True)  # noqa: E731
+
+    log("config 4: 4096^3 MatMulInteger")
+    c4 = c4_square(d, args.steps, args.warmup)
+    tops = c4["ops"] * args.steps / c4["wall_s"] / 1e12
+    kern_tops = c4["ops"] / (c4["kernel_mean_ms"] * 1e-3) / 1e12
+    configs = {"c4_square_4096": {"tops_wall": tops, "tops_kernel": kern_tops, "kernel": c4["kernel"],
+                                  "kernel_mean_us": c4["kernel_mean_ms"] * 1e3, "check": c4["check"]}}
+    log(json.dumps(configs["c4_square_4096"]))
+
+    gemv = {}
+    for m in ((1,) if args.quick else (1, 4, 16)):
+        log(f"config 3: GEMV M={m}")
+        r = c3_gemv(d, m, args.steps, args.warmup)
+        gbs = r["bytes"] / (r["step_mean_ms"] * 1e-3) / 1e9
+        gemv[m] = {"gbs": gbs, "frac": gbs / PEAK_HBM_GBS, "step_mean_us": r["step_mean_ms"] * 1e3,
+                   "tops": r["ops"] / (r["step_mean_ms"] * 1e-3) / 1e12, "kernels": r["kernels"],
+                   "dispatch_mean_us": [t * 1e3 for t in r["dispatch_mean_ms"]], "bytes": r["bytes"],
+                   "check": r["check"]}
+        configs[f"c3_gemv_m{m}"] = gemv[m]
+        log(json.dumps(gemv[m]))
+    if not args.quick:
+        log("config 2: BERT FFN chain")
+        r = c2_bert_ffn(d, args.steps, args.warmup)
+        configs["c2_bert_ffn"] = {"chain_wall_us": r["wall_s"] / args.steps * 1e6,
+                                  "dispatch_mean_us": {k: v * 1e3 for k, v in r["dispatch_mean_ms"].items()},
+                                  "check": r["check"]}
+        log(json.dumps(configs["c2_bert_ffn"]))
+        log("config 5: batched 32 x 512 x 4096 x 4096")
+        r = c5_batched(d, max(3, args.steps // 5), 2)
+        configs["c5_batched"] = {"tops_kernel": r["ops"] / (r["kernel_mean_ms"] * 1e-3) / 1e12,
+                                 "kernel_mean_us": r["kernel_mean_ms"] * 1e3, "kernel": r["kernel"], "check": r["check"]}
+        log(json.dumps(configs["c5_batched"]))
+
+    roof = {"bound": "mfma", "achieved": kern_tops, "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+            "frac": kern_tops / PEAK_INT8_TOPS, "traffic": None,
+            "note": "int8 ops (a multiply-add counts 2), 2*M*N*K per launch over the mean HIP-event launch time; "
+                    "unit is tera-ops/s"}
+    cpu = None if args.no_cpu else cpu_baseline_c4(c4["host_operands"])
+    g1 = gemv.get(1)
+    line = {
+        "metric": METRIC, "value": round(tops, 2), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": c4["wall_s"] / args.steps * 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic (device-side SplitMix64)",
+        "config": {"workload": "MatMulInteger M=N=K=4096, uint8 A per-row zero point, int8 B (K x N), int32 out",
+                   "global_batch": 1, "m": 4096, "n": 4096, "k": 4096, "parallelism": "single GPU"},
+        "roofline": roof,
+        "gemv_m1": None if g1 is None else {
+            "metric": "GB/s at M=1 K=4096 N=11008 (MatMulIntegerToFloat, 9 rotating weight copies)",
+            "value": round(g1["gbs"], 1), "unit": "GB/s",
+            "roofline": {"bound": "hbm", "achieved": g1["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": g1["frac"], "traffic": None}},
+        "cpu_baseline": cpu,
+        "configs": configs,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
