@@ -374,8 +374,13 @@ static int check_gemm_params(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t
 int og_int8_gemm_kernel_name(const og_int8_gemm_params *p, uint32_t batch, char *buf, size_t len)
 {
     if (!p || !buf || len == 0) return fail(nullptr, OG_ERR_INVALID_ARG, "params", "null pointer");
-    og::GemmKernel k = og::choose_gemm_kernel((int32_t)p->M, (int32_t)p->N, (int32_t)p->K, (int32_t)(batch ? batch : 1), p->Flags);
-    snprintf(buf, len, "%s", og::gemm_kernel_name(k));
+    const int32_t b = (int32_t)(batch ? batch : 1);
+    og::GemmKernel k = og::choose_gemm_kernel((int32_t)p->M, (int32_t)p->N, (int32_t)p->K, b, p->Flags);
+    const char *name = og::gemm_kernel_name(k);
+    // The tiled family's name also says the tile (the aligned kernel; unaligned operands take the generic one).
+    if (k == og::GemmKernel::Tiled)
+        name = og::tiled_uses_large((int32_t)p->M, (int32_t)p->N, b) ? "mfma-i8-tile256x256x64" : "mfma-i8-tile128x128x128";
+    snprintf(buf, len, "%s", name);
     return OG_OK;
 }
 

@@ -48,7 +48,11 @@ const char *gemm_kernel_name(GemmKernel k);
 
 // Launchers (one per kernel family); each returns the launch status. `kernel` receives the name of the kernel run.
 hipError_t launch_gemm_portable(const GemmArgs &g, hipStream_t s, const char **kernel);
+// The MFMA tiled product: the aligned kernel when tiled_fast_ok(g), else the generic one.
 hipError_t launch_gemm_tiled(const GemmArgs &g, hipStream_t s, const char **kernel);
+hipError_t launch_gemm_generic(const GemmArgs &g, hipStream_t s, const char **kernel);
+bool tiled_fast_ok(const GemmArgs &g);
+bool tiled_uses_large(int32_t M, int32_t N, int32_t batch);
 // Few rows (M <= 16), B stored K x N: split-k partial sums into ws.partials, then a pass that adds them up, corrects for
 // the zero points and applies the epilogue. `slices` is the split chosen by skinny_slices().
 hipError_t launch_gemm_skinny(const GemmArgs &g, const Workspace &ws, hipStream_t s, const char **kernel, int step);
