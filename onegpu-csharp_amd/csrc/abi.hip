@@ -342,7 +342,8 @@ const char *gemm_kernel_name(GemmKernel k)
 
 extern "C" {
 
-static const uint32_t kKnownGemmFlags = 0x7Fu | 0x380u | OG_GEMM_PORTABLE | OG_GEMM_NO_SKINNY | OG_GEMM_NO_DIRECT;
+static const uint32_t kKnownGemmFlags =
+    0x7Fu | 0x380u | OG_GEMM_PORTABLE | OG_GEMM_NO_SKINNY | OG_GEMM_NO_DIRECT | OG_GEMM_LARGE_TILE;
 
 // Checks the parameter block alone; returns OG_OK or the failing status (message and argument set).
 static int check_gemm_params(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch)
@@ -377,9 +378,12 @@ int og_int8_gemm_kernel_name(const og_int8_gemm_params *p, uint32_t batch, char 
     const int32_t b = (int32_t)(batch ? batch : 1);
     og::GemmKernel k = og::choose_gemm_kernel((int32_t)p->M, (int32_t)p->N, (int32_t)p->K, b, p->Flags);
     const char *name = og::gemm_kernel_name(k);
-    // The tiled family's name also says the tile (the aligned kernel; unaligned operands take the generic one).
-    if (k == og::GemmKernel::Tiled)
-        name = og::tiled_uses_large((int32_t)p->M, (int32_t)p->N, b) ? "mfma-i8-tile256x256x64" : "mfma-i8-tile128x128x128";
+    // The tiled family's name also says the tile, for operands at 16-byte aligned offsets and row lengths (buffers
+    // from og_alloc are); other alignments take the register-staged or the generic kernel.
+    if (k == og::GemmKernel::Tiled) {
+        const bool large = (p->Flags & OG_GEMM_LARGE_TILE) || og::tiled_uses_large((int32_t)p->M, (int32_t)p->N, b);
+        name = large ? "mfma-i8-direct256x256x64" : "mfma-i8-tile128x128x128";
+    }
     snprintf(buf, len, "%s", name);
     return OG_OK;
 }

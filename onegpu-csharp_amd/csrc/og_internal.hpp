@@ -51,6 +51,9 @@ hipError_t launch_gemm_portable(const GemmArgs &g, hipStream_t s, const char **k
 // The MFMA tiled product: the aligned kernel when tiled_fast_ok(g), else the generic one.
 hipError_t launch_gemm_tiled(const GemmArgs &g, hipStream_t s, const char **kernel);
 hipError_t launch_gemm_generic(const GemmArgs &g, hipStream_t s, const char **kernel);
+// The large-product kernel fed by LDS DMA (16-byte aligned operands); launch_gemm_tiled picks it when it applies.
+hipError_t launch_gemm_direct(const GemmArgs &g, hipStream_t s, const char **kernel);
+bool direct_ok(const GemmArgs &g);
 bool tiled_fast_ok(const GemmArgs &g);
 bool tiled_uses_large(int32_t M, int32_t N, int32_t batch);
 // Few rows (M <= 16), B stored K x N: split-k partial sums into ws.partials, then a pass that adds them up, corrects for

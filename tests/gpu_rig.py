@@ -106,6 +106,7 @@ def configs(d, all_: bool):
     if all_:
         lst.append(("tiled only", og.Int8Gemm(d, og.Int8GemmOptions(Tile=64))))
         lst.append(("split k", og.Int8Gemm(d, og.Int8GemmOptions(Tile=32))))
+        lst.append(("large tile", og.Int8Gemm(d, og.Int8GemmOptions(Tile=256))))
     return lst
 
 

@@ -23,7 +23,7 @@ def test_closed_form():
         assert c.Read().tolist() == [-3, 5, -4, -5, 9, -6]
 
 
-@pytest.mark.parametrize("config", ["default", "portable", "tiled only", "split k"])
+@pytest.mark.parametrize("config", ["default", "portable", "tiled only", "split k", "large tile"])
 def test_edge_shapes_are_bit_exact(config):
     # EdgeShapesAreBitExact (Int8Tests.cs:214-283): every case, each kernel forced in turn.
     d = device()
@@ -114,21 +114,23 @@ def _requant_case(d, gemm, m, n, k, mult_vec, unsigned, zero_y, with_bias, seed,
     return bad
 
 
-def test_float_and_requantized_forms_are_bit_exact():
-    # FloatAndRequantizedFormsAreBitExact (Int8Tests.cs:468-501)
+@pytest.mark.parametrize("config", ["default", "large tile"])
+def test_float_and_requantized_forms_are_bit_exact(config):
+    # FloatAndRequantizedFormsAreBitExact (Int8Tests.cs:468-501); "large tile" runs the same cases on the 256 x 256
+    # kernels, whose epilogue is their own.
     d = device()
-    gemm = og.Int8Gemm(d)
+    gemm = dict(configs(d, True))[config]
     bad_f = bad_q = 0
     seed = 10
     for (m, n, k) in cases.FLOAT_SHAPES:
         for vec in (False, True):
             for ib, fb in ((False, False), (True, False), (False, True), (True, True)):
-                say(f"float {m}x{n}x{k} vec {vec} ib {ib} fb {fb}")
+                say(f"float [{config}] {m}x{n}x{k} vec {vec} ib {ib} fb {fb}")
                 bad_f += _float_case(d, gemm, m, n, k, vec, ib, fb, seed)
                 seed += 1
         for vec in (False, True):
             for unsigned, zero in cases.REQUANT_OUT:
-                say(f"requant {m}x{n}x{k} vec {vec} u8 {unsigned} zero {zero}")
+                say(f"requant [{config}] {m}x{n}x{k} vec {vec} u8 {unsigned} zero {zero}")
                 bad_q += _requant_case(d, gemm, m, n, k, vec, unsigned, zero, (seed & 1) == 0, seed, (seed & 2) != 0,
                                        (seed & 4) != 0)
                 seed += 1
