@@ -1,0 +1,485 @@
+// The large-product int8 MFMA kernel: operands go from HBM straight into a ring of LDS stages (buffer_load ... lds,
+// no staging registers), and B stored K x N is read in its own layout with the gfx950 transpose read
+// ds_read_b64_tr_b8, so no VALU transposition is needed.
+//
+//  - Tile 256 x 256 per workgroup, 64 deep per stage, 4 waves (2 x 2) of 128 x 128, v_mfma_i32_16x16x64_i8, a ring
+//    of 5 stages filling the 160 KB of LDS. K must be a multiple of 64 (other products take the register-staged
+//    kernel).
+//  - One wave per SIMD, so the wave's own instruction stream has to keep the matrix core busy: a 16-cycle MFMA leaves
+//    room for about two other instructions. Everything else in a stage is spread between the MFMAs and kept short:
+//    the DMA of a later stage (2 instructions a load), the fragment reads, one flip per unsigned A fragment, and the
+//    operands' byte sums (v_sad_u8, which issues beside an MFMA where v_dot4 does not).
+//  - Operands stay as stored in LDS; each MFMA fragment of an unsigned operand is moved to the signed domain
+//    (s = u ^ 0x80) after it is read, and the zero points are applied at the store from the byte sums:
+//        sum (s - z')(t - w') = sum s t - w' sum s - z' sum t + K z' w'   (mod 2^32; Int8GemmDot.hlsl:1-11 rearranges the same)
+//  - LDS layouts (16-byte chunks, conflict-free for the fragment reads as measured with SQ_LDS_BANK_CONFLICT):
+//      A (and B stored N x K): row r of 64 bytes, chunk q at position q ^ ((r >> 1) & 3);
+//      B stored K x N: row k of 256 bytes, chunk c at position c ^ fB(k), fB(k) = (k & 7) | (((k >> 4) & 1) << 3).
+//    A buffer load writes 64 lanes x 16 bytes to consecutive LDS, so each lane loads the global chunk that belongs in
+//    its slot.
+//  - A fragment (lane l: row l % 16, k 16 (l / 16) .. + 15) is one ds_read_b128. A B fragment (lane l: column l % 16,
+//    the same 16 k) is two ds_read_b64_tr_b8: within each 16-lane group, lane i < 8 receives byte i of the 8-byte
+//    segments the even lanes address and lane 8 + i byte i of the odd lanes' segments, so even lanes address rows
+//    k..k+7 at columns n..n+7 and odd lanes the same rows at columns n+8..n+15.
+#pragma once
+
+#include <type_traits>
+
+#include "og_internal.hpp"
+
+namespace og {
+
+typedef int32_t v4i __attribute__((ext_vector_type(4)));
+typedef int32_t v2i __attribute__((ext_vector_type(2)));
+typedef uint32_t u4w __attribute__((ext_vector_type(4)));
+#define OG_LDS2(p) ((__attribute__((address_space(3))) v2i *)(p))
+
+namespace {
+
+constexpr int DBM = 256, DBN = 256, DBK = 64, DTHREADS = 256;
+constexpr int A_STAGE = DBM * DBK;   // bytes
+constexpr int B_STAGE = DBK * DBN;
+constexpr int STAGE = A_STAGE + B_STAGE;
+constexpr int NS = 5;                                   // stages in the ring
+constexpr int LOADS_A = A_STAGE / 16 / DTHREADS;        // 16-byte loads per thread per stage
+constexpr int LOADS_B = B_STAGE / 16 / DTHREADS;
+constexpr int LOADS = LOADS_A + LOADS_B;
+
+// Buffer resource words for `bytes` bytes at `base` (raw buffer: no stride, no swizzle; reads past the range
+// return zero).
+__device__ __forceinline__ u4w drsrc(const uint8_t *base, int32_t bytes)
+{
+    const uint64_t p = (uint64_t)(uintptr_t)base;
+    return (u4w){(uint32_t)p, (uint32_t)(p >> 32) & 0xFFFFu, (uint32_t)max(bytes, 0), 0x00020000u};
+}
+
+// LDS byte address of a __shared__ location.
+__device__ __forceinline__ uint32_t lds_addr(const void *p)
+{
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// One LDS DMA: lane l's 16 bytes at rsrc + voff land at LDS address base + OFF + 16 l. Issued from inline assembly
+// so that the compiler neither reorders LDS accesses across it nor adds waits of its own for it: the stages wait for
+// exactly the loads they need (vmcnt counts these loads in issue order). M0 holds the LDS address; nothing else in
+// the kernel uses M0 (no indexed register access, messages or LDS intrinsics), so it is set without being saved.
+template <int OFF>
+__device__ __forceinline__ void dma16(u4w rsrc, uint32_t base, uint32_t voff)
+{
+    asm volatile("s_add_u32 m0, %0, %1\n\tbuffer_load_dwordx4 %2, %3, 0 offen lds" : : "s"(base), "n"(OFF), "v"(voff),
+                 "s"(rsrc) : "memory");
+}
+
+__device__ __forceinline__ int a_pos(int r, int q) { return q ^ ((r >> 1) & 3); }
+__device__ __forceinline__ int b_pos(int k, int c) { return c ^ ((k & 7) | (((k >> 4) & 1) << 3)); }
+
+// Waits until at most N of this wave's DMA loads are outstanding, then meets the other waves. A compiler barrier as
+// well: no LDS access moves across it.
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(N) : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// This wave's LDS accesses done, then meet the other waves.
+__device__ __forceinline__ void wait_lgkm_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory"); }
+
+// Both: at most N DMA loads outstanding and no LDS access, then meet the other waves.
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm_barrier()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
+}
+
+template <bool FLIP>
+__device__ __forceinline__ v4i to_signed(v4i v)
+{
+    if constexpr (FLIP) return v ^ (int32_t)0x80808080;
+    else return v;
+}
+
+__device__ __forceinline__ v4i mfma(v4i a, v4i b, v4i c) { return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0); }
+
+// Sum of the 16 bytes of a fragment read as unsigned, added to acc (v_sad_u8 against zero). Applied to biased bytes
+// (signed-domain value + 128, i.e. value ^ 0x80): the signed sum is the biased sum minus 128 per byte.
+__device__ __forceinline__ uint32_t sad16(v4i v, uint32_t acc)
+{
+    acc = __builtin_amdgcn_sad_u8((uint32_t)v.x, 0u, acc);
+    acc = __builtin_amdgcn_sad_u8((uint32_t)v.y, 0u, acc);
+    acc = __builtin_amdgcn_sad_u8((uint32_t)v.z, 0u, acc);
+    return __builtin_amdgcn_sad_u8((uint32_t)v.w, 0u, acc);
+}
+
+// Calls f(integral_constant<I>) for I = B .. E - 1.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F &&f)
+{
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+// Scheduling pattern of one block of 8 MFMAs: its DS reads first, then each MFMA followed by its share of the VALU
+// work (the byte sums VS over the first six, the flips VF, which wait for a read, over the last two).
+template <int VS, int VF, int DS>
+__device__ __forceinline__ void sched_block()
+{
+    __builtin_amdgcn_sched_group_barrier(0x100, DS, 0);
+    static_for<0, 8>([](auto m_tag) {
+        constexpr int m = decltype(m_tag)::value;
+        constexpr int v = m < 6 ? (VS * (m + 1) / 6 - VS * m / 6) : (VF * (m - 5) / 2 - VF * (m - 6) / 2);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x002, v, 0);
+    });
+}
+
+}  // namespace
+
+// FLIP_A / FLIP_B: the operand is unsigned (moved to the signed domain fragment by fragment). SUM_A / SUM_B: the row
+// sums of A / column sums of B are needed (the other operand's zero point in the signed domain can be non-zero).
+template <bool TRANS_B, bool SUM_A, bool SUM_B, bool FLIP_A, bool FLIP_B>
+__global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t tiles_n, int32_t tiles_m)
+{
+    // The whole LDS (160 KB): the ring of NS stages, A (256 x 64) then B (64 x 256) each. After the loop its start
+    // holds the epilogue's per-row and per-column arrays.
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int i16 = lane & 15, g4 = lane >> 4;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // Tile order: an XCD-contiguous run of tiles, walked in groups of 8 row-tiles (see the aligned kernel).
+    const int64_t tiles = (int64_t)tiles_n * tiles_m;
+    const int64_t nblocks = tiles * g.batch;
+    int64_t bid = blockIdx.x;
+    if ((nblocks & 7) == 0) bid = (bid & 7) * (nblocks >> 3) + (bid >> 3);
+    const int32_t batch = (int32_t)(bid / tiles);
+    const int64_t t = bid % tiles;
+    int32_t tm, tn;
+    {
+        const int32_t GROUP = 8;
+        const int64_t per_group = (int64_t)GROUP * tiles_n;
+        const int32_t first_m = (int32_t)(t / per_group * GROUP);
+        const int32_t gsize = min(tiles_m - first_m, GROUP);
+        const int64_t in = t % per_group;
+        tm = first_m + (int32_t)(in % gsize);
+        tn = (int32_t)(in / gsize);
+    }
+    const int32_t m0 = tm * DBM, n0 = tn * DBN;
+    const int32_t lda = g.lda, ldb = g.ldb, K = g.K;
+    constexpr bool a_signed = !FLIP_A, b_signed = !FLIP_B;
+
+    // The epilogue's per-row and per-column parameters, fetched now so that their latency hides behind the loop:
+    // thread t holds row m0 + t's zero point and column n0 + t's zero point, int bias, scale and float bias.
+    const uint32_t epi = g.epi;
+    const int32_t my_m = min(m0 + tid, g.M - 1), my_n = min(n0 + tid, g.N - 1);
+    // Raw zero-point bytes (0 when absent); moved to the signed domain after the loop, so nothing waits for them here.
+    const uint32_t za_raw = (SUM_B && g.ZA) ? g.ZA[(g.flags & OG_GEMM_ZA_PER_ROW) ? my_m : 0] : 0u;
+    const uint32_t zb_raw = (SUM_A && g.ZB) ? g.ZB[(g.flags & OG_GEMM_ZB_PER_COL) ? my_n : 0] : 0u;
+    const int32_t my_ib = (epi & OG_EPI_INT_BIAS) ? g.bias[my_n] : 0;
+    const float my_sc = (epi & OG_EPI_FLOAT) ? g.scale[(epi & OG_EPI_SCALE_PER_COL) ? my_n : 0] : 0.0f;
+    const float my_fb = (epi & OG_EPI_FLOAT_BIAS) ? g.fbias[my_n] : 0.0f;
+
+    // This tile's operand ranges (under 2^31 bytes, as the launcher checks): loads past the last valid byte return
+    // zeros. With K = 0 the operands may be absent and nothing is read (the prologue still issues its loads, over
+    // empty ranges).
+    const uint8_t *a_base = g.A + batch * g.strideA + (int64_t)m0 * lda;
+    const int32_t a_valid = K > 0 ? (min(g.M - m0, DBM) - 1) * lda + K : 0;
+    const uint8_t *b_base;
+    int32_t b_valid, b_step;
+    if constexpr (TRANS_B) {
+        b_base = g.B + batch * g.strideB + (int64_t)n0 * ldb;
+        b_valid = K > 0 ? (min(g.N - n0, DBN) - 1) * ldb + K : 0;
+        b_step = 1;
+    } else {
+        b_base = g.B + batch * g.strideB + n0;
+        b_valid = K > 0 ? (K - 1) * ldb + min(g.N - n0, DBN) : 0;
+        b_step = ldb;
+    }
+
+    // Per-thread global offsets of the chunks that land in this thread's LDS slots (the same at every stage): load i
+    // of a wave fills 1 KB at i * 4 KB + wave * 1 KB of the operand's tile.
+    uint32_t off_a[LOADS_A], off_b[LOADS_B];
+#pragma unroll
+    for (int i = 0; i < LOADS_A; i++) {
+        const int s = (i * 4 + wave) * 64 + lane, r = s >> 2, p = s & 3;
+        off_a[i] = (uint32_t)r * (uint32_t)lda + 16u * (uint32_t)a_pos(r, p);
+    }
+#pragma unroll
+    for (int i = 0; i < LOADS_B; i++) {
+        const int s = (i * 4 + wave) * 64 + lane;
+        if constexpr (TRANS_B) {
+            const int r = s >> 2, p = s & 3;
+            off_b[i] = (uint32_t)r * (uint32_t)ldb + 16u * (uint32_t)a_pos(r, p);
+        } else {
+            const int k = s >> 4, p = s & 15;
+            off_b[i] = (uint32_t)k * (uint32_t)ldb + 16u * (uint32_t)b_pos(k, p);
+        }
+    }
+    const uint32_t wave_lds = lds_addr(smem) + (uint32_t)wave * 1024u;
+
+    // The DMA of the stage at depth k0 into ring buffer U: load I < 4 is A's, the rest B's. A k0 past K (the loads
+    // beyond the last stage) is clamped to K, which keeps the offsets in range; those loads are never used.
+    struct StageRsrc {
+        u4w a, b;
+    };
+    auto stage_rsrc = [&](int32_t k0) {
+        k0 = min(k0, K);
+        return StageRsrc{drsrc(a_base + k0, a_valid - k0), drsrc(b_base + k0 * b_step, b_valid - k0 * b_step)};
+    };
+    auto dma = [&](auto u_tag, auto i_tag, const StageRsrc &rr) {
+        constexpr int U = decltype(u_tag)::value, I = decltype(i_tag)::value;
+        if constexpr (I < LOADS_A) dma16<U * STAGE + I * 4096>(rr.a, wave_lds, off_a[I]);
+        else dma16<U * STAGE + A_STAGE + (I - LOADS_A) * 4096>(rr.b, wave_lds, off_b[I - LOADS_A]);
+    };
+
+    // Fragments as stored (unsigned operands not yet flipped) from ring buffer u.
+    auto read_a = [&](int u, int i) {
+        const int r = wm * 128 + 16 * i + i16;
+        return *reinterpret_cast<const v4i *>(smem + u * STAGE + r * 64 + 16 * a_pos(r, g4));
+    };
+    auto read_b = [&](int u, v4i (&bf)[8], int j0, int j1) {
+        const uint8_t *bs = smem + u * STAGE + A_STAGE;
+#pragma unroll
+        for (int j = j0; j < j1; j++) {
+            const int nl = wn * 128 + 16 * j;   // first column of the block
+            if constexpr (TRANS_B) {
+                const int r = nl + i16;
+                bf[j] = *reinterpret_cast<const v4i *>(bs + r * 64 + 16 * a_pos(r, g4));
+            } else {
+                const int c = nl >> 4;   // 16-byte chunk of the block's columns
+                v2i h[2];
+#pragma unroll
+                for (int hh = 0; hh < 2; hh++) {
+                    const int k = 16 * g4 + 8 * hh + (i16 >> 1);
+                    h[hh] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(OG_LDS2(bs + k * DBN + 16 * b_pos(k, c) + 8 * (i16 & 1)));
+                }
+                bf[j] = (v4i){h[0].x, h[0].y, h[1].x, h[1].y};
+            }
+        }
+    };
+
+    v4i acc[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[i][j] = (v4i){0, 0, 0, 0};
+    // This lane's biased byte sums (its k-group, 16 bytes per stage) of the wave's A rows / B columns, block by block.
+    // Biased bytes: an unsigned operand's bytes as stored, a signed one's with the top bit flipped.
+    uint32_t rs[8], cs[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) { rs[i] = 0; cs[i] = 0; }
+    // VALU instructions per block beside the MFMAs: byte sums, and the flip of the next A fragment.
+    constexpr int VS = (SUM_A ? (FLIP_A ? 4 : 8) : 0) + (SUM_B ? (FLIP_B ? 4 : 8) : 0), VF = FLIP_A ? 4 : 0;
+
+    const int32_t nk = K / DBK;   // K is a multiple of DBK here
+
+    // Prologue: stages 0 .. NS - 2 in flight; stage 0 landed and its first fragments read.
+    static_for<0, NS - 1>([&](auto u_tag) {
+        const StageRsrc r = stage_rsrc(decltype(u_tag)::value * DBK);
+        static_for<0, LOADS>([&](auto i_tag) { dma(u_tag, i_tag, r); });
+    });
+    wait_vm_barrier<LOADS * (NS - 2)>();
+    // The stage being computed: its B fragments and current A fragment in the signed domain, and both as stored
+    // where an unsigned operand's byte sums need them.
+    v4i bf[8], a_cur, a_st, b_st[FLIP_B && SUM_B ? 8 : 1];
+    {
+        v4i nb[8];
+        read_b(0, nb, 0, 8);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            bf[j] = to_signed<FLIP_B>(nb[j]);
+            if constexpr (FLIP_B && SUM_B) b_st[j] = nb[j];
+        }
+        a_st = read_a(0, 0);
+        a_cur = to_signed<FLIP_A>(a_st);
+    }
+    auto sum_a = [&](uint32_t acc) { return FLIP_A ? sad16(a_st, acc) : sad16(a_cur ^ (int32_t)0x80808080, acc); };
+    auto sum_b = [&](int j, uint32_t acc) {
+        if constexpr (FLIP_B) return sad16(b_st[SUM_B ? j : 0], acc);
+        else return sad16(bf[j] ^ (int32_t)0x80808080, acc);
+    };
+
+    // One stage s in ring buffer U, in 8 blocks (one A fragment against the 8 B fragments, plus the sums). Block i
+    // reads the A fragment of block i + 1 (block 7: the first of stage s + 1). At block 4 the waves wait for stage
+    // s + 1 (this wave's loads landed, then everyone's) and meet: from then on nobody reads the buffer of stage s - 1,
+    // so blocks 4..7 each issue two loads of stage s + NS - 1 into it and read two B fragments of stage s + 1,
+    // spreading the DMA and the LDS reads over the stage. Stages past the last still wait and read (their loads cover
+    // empty or unused ranges and what is read is not used), so every stage is the same.
+    auto run_stage = [&](auto u_tag, int32_t s) {
+        constexpr int U = decltype(u_tag)::value, DU = (U + NS - 1) % NS, NU = (U + 1) % NS;
+        const StageRsrc rr = stage_rsrc((s + NS - 1) * DBK);
+        v4i nb[8];
+        static_for<0, 8>([&](auto i_tag) {
+            constexpr int i = decltype(i_tag)::value;
+            if constexpr (i == 4) {
+                wait_vm_lgkm_barrier<LOADS * (NS - 3)>();   // stages s + 2 .. s + NS - 2 may still be in flight
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if constexpr (i >= 4) {
+                dma(std::integral_constant<int, DU>{}, std::integral_constant<int, 2 * (i - 4)>{}, rr);
+                dma(std::integral_constant<int, DU>{}, std::integral_constant<int, 2 * (i - 4) + 1>{}, rr);
+                read_b(NU, nb, 2 * (i - 4), 2 * (i - 4) + 2);
+            }
+            const v4i a_raw = i < 7 ? read_a(U, i + 1) : read_a(NU, 0);
+            if constexpr (SUM_A) rs[i] = sum_a(rs[i]);   // every wave sums (no branch in the block); one publishes
+            if constexpr (SUM_B) cs[i] = sum_b(i, cs[i]);
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc[i][j] = mfma(a_cur, bf[j], acc[i][j]);
+            a_st = a_raw;
+            a_cur = to_signed<FLIP_A>(a_raw);
+            sched_block<VS, VF, (i < 4 ? 1 : (TRANS_B ? 3 : 5))>();
+            __builtin_amdgcn_sched_barrier(0);
+        });
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            bf[j] = to_signed<FLIP_B>(nb[j]);
+            if constexpr (FLIP_B && SUM_B) b_st[j] = nb[j];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    static_assert(NS == 5, "the loop below is unrolled for 5 stages");
+    for (int32_t kt = 0; kt < nk; kt += NS) {
+        static_for<0, NS>([&](auto u_tag) {
+            if (kt + decltype(u_tag)::value < nk) run_stage(u_tag, kt + decltype(u_tag)::value);
+        });
+    }
+    // Every DMA landed and every wave done with the stage buffers before the epilogue's arrays take their place.
+    wait_vm<0>();
+    wait_lgkm_barrier();
+    int32_t *const RowSum = reinterpret_cast<int32_t *>(smem);
+    int32_t *const RowZ = RowSum + DBM;
+    int32_t *const ColSum = RowZ + DBM;
+    int32_t *const ColW = ColSum + DBN;
+    int32_t *const ColIB = ColW + DBN;
+    float *const ColSc = reinterpret_cast<float *>(ColIB + DBN);
+    float *const ColFb = ColSc + DBN;
+
+    // Byte sums: the four k-groups of a row / column sit in lanes l, l + 16, l + 32, l + 48. The biased sums cover 64
+    // bytes per stage; the signed sums are 128 less per byte (mod 2^32).
+    const uint32_t bias_total = 128u * (uint32_t)DBK * (uint32_t)nk;
+    if (SUM_A && wn == 0) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            uint32_t v = rs[i] + (uint32_t)__shfl_xor((int32_t)rs[i], 16);
+            v += (uint32_t)__shfl_xor((int32_t)v, 32);
+            if (g4 == 0) RowSum[wm * 128 + 16 * i + i16] = (int32_t)(v - bias_total);
+        }
+    }
+    if (SUM_B && wm == 0) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            uint32_t v = cs[j] + (uint32_t)__shfl_xor((int32_t)cs[j], 16);
+            v += (uint32_t)__shfl_xor((int32_t)v, 32);
+            if (g4 == 0) ColSum[wn * 128 + 16 * j + i16] = (int32_t)(v - bias_total);
+        }
+    }
+    if (SUM_B) RowZ[tid] = a_signed ? sext8(za_raw) : (int32_t)za_raw - 128;
+    if (SUM_A) ColW[tid] = b_signed ? sext8(zb_raw) : (int32_t)zb_raw - 128;
+    ColIB[tid] = my_ib;
+    ColSc[tid] = my_sc;
+    ColFb[tid] = my_fb;
+    wait_lgkm_barrier();
+
+    // Store. With z' = zero of A's row, w' = zero of B's column, s_m / t_n the byte sums of the row / column:
+    //     C = acc - w' s_m - z' (t_n - K w')   (+ int bias; float: fl(fl(float(C)) * scale) (+ float bias))
+    // MFMA 16 x 16 output layout: lane l holds rows 4 (l / 16) + r, column l % 16 of each block.
+    const uint32_t Ku = (uint32_t)K;
+    uint32_t wz[8], ct[8], ib[8];
+    float sc[8], fb[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int nl = wn * 128 + 16 * j + i16;
+        wz[j] = SUM_A ? (uint32_t)ColW[nl] : 0u;
+        ct[j] = SUM_B ? (uint32_t)ColSum[nl] - Ku * wz[j] : 0u;
+        ib[j] = (uint32_t)ColIB[nl];
+        sc[j] = ColSc[nl];
+        fb[j] = ColFb[nl];
+    }
+    int32_t *const Cb = static_cast<int32_t *>(g.C) + batch * g.strideC;   // int32 and float32 results alike
+    const int32_t ncol0 = n0 + wn * 128 + i16;
+    const int32_t M = g.M, N = g.N;
+    auto store_all = [&](auto float_tag, bool has_fb) {
+        constexpr bool F = decltype(float_tag)::value;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int ml = wm * 128 + 16 * i + 4 * g4;
+            const v4i ssv = SUM_A ? *reinterpret_cast<const v4i *>(&RowSum[ml]) : (v4i){0, 0, 0, 0};
+            const v4i zzv = SUM_B ? *reinterpret_cast<const v4i *>(&RowZ[ml]) : (v4i){0, 0, 0, 0};
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int32_t m = m0 + ml + r;
+                if (m >= M) continue;
+                int32_t *const row = Cb + m * N;   // batch * M * N < 2^31 (checked at the boundary)
+                const uint32_t ss = (uint32_t)ssv[r], zz = (uint32_t)zzv[r];
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const int32_t n = ncol0 + 16 * j;
+                    if (n >= N) continue;
+                    const uint32_t v = (uint32_t)acc[i][j][r] - wz[j] * ss - zz * ct[j] + ib[j];
+                    if constexpr (F) {
+                        float f = __fmul_rn((float)(int32_t)v, sc[j]);
+                        if (has_fb) f = __fadd_rn(f, fb[j]);
+                        row[n] = __float_as_int(f);
+                    } else {
+                        row[n] = (int32_t)v;
+                    }
+                }
+            }
+        }
+    };
+    if (epi & OG_EPI_FLOAT) {
+        if (epi & OG_EPI_FLOAT_BIAS) store_all(std::true_type{}, true);
+        else store_all(std::true_type{}, false);
+    } else {
+        store_all(std::false_type{}, false);
+    }
+}
+
+// One instantiation per operand signedness and needed byte sums (an unsigned operand always needs the other's sums).
+template <bool T, bool FA, bool FB>
+inline void launch_direct_flips(const GemmArgs &g, hipStream_t s, dim3 grid, int32_t tn, int32_t tm, bool sa, bool sb)
+{
+#define OG_D(SA, SB) hipLaunchKernelGGL((k_gemm_direct<T, SA, SB, FA, FB>), grid, dim3(DTHREADS), 0, s, g, tn, tm)
+    if constexpr (FA && FB) {
+        OG_D(true, true);
+    } else if constexpr (FA) {
+        if (sa) OG_D(true, true);
+        else OG_D(false, true);
+    } else if constexpr (FB) {
+        if (sb) OG_D(true, true);
+        else OG_D(true, false);
+    } else {
+        if (sa && sb) OG_D(true, true);
+        else if (sa) OG_D(true, false);
+        else if (sb) OG_D(false, true);
+        else OG_D(false, false);
+    }
+#undef OG_D
+}
+
+template <bool T>
+inline void launch_direct_t(const GemmArgs &g, hipStream_t s, dim3 grid, int32_t tn, int32_t tm)
+{
+    const bool fa = !(g.flags & OG_GEMM_A_INT8), fb = !(g.flags & OG_GEMM_B_INT8);
+    const bool sa = (g.flags & OG_GEMM_ZB) || fb, sb = (g.flags & OG_GEMM_ZA) || fa;
+    if (fa && fb) launch_direct_flips<T, true, true>(g, s, grid, tn, tm, sa, sb);
+    else if (fa) launch_direct_flips<T, true, false>(g, s, grid, tn, tm, sa, sb);
+    else if (fb) launch_direct_flips<T, false, true>(g, s, grid, tn, tm, sa, sb);
+    else launch_direct_flips<T, false, false>(g, s, grid, tn, tm, sa, sb);
+}
+
+// B stored N x K (instantiated in its own translation unit).
+void launch_direct_nk(const GemmArgs &g, hipStream_t s, dim3 grid, int32_t tn, int32_t tm);
+
+}  // namespace og
