@@ -559,7 +559,7 @@ void Int8Gemm::Multiply(GpuCommandEncoder &encoder, const Int8GemmProblem &p, co
     if (!options_.AllowPackedDot) flags |= OG_GEMM_PORTABLE;
     if (options_.Tile == 64) flags |= OG_GEMM_NO_SKINNY;
     if (options_.Tile == 256) flags |= OG_GEMM_NO_SKINNY | OG_GEMM_LARGE_TILE;
-    if (options_.Tile == 32) flags |= OG_GEMM_NO_DIRECT;
+    if (options_.Tile == 32) flags |= OG_GEMM_NO_DIRECT | OG_GEMM_NO_STREAM;
 
     og_int8_gemm_params w{};
     w.M = (uint32_t)p.M;

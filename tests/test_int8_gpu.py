@@ -272,3 +272,29 @@ def test_scratch_semantics():
     with pytest.raises(og.GpuKernelShapeException) as ex:
         gemm.EncodeRequantized(d.BeginCommands(), og.Int8GemmProblem(64, 64, 8), a, b, y, mult, 0, scratch=og.Int8Scratch(small))
     assert ex.value.Argument == "scratch"
+
+
+def test_streamed_rows_are_bit_exact():
+    # The few-rows products (M <= 16, B stored K x N) on the streamed kernel, which splits K over the CUs and finishes
+    # each column slab in whichever workgroup comes last: one slab or many, one part per slab or several, K past the
+    # last full 64 rows, batches, every signedness and zero-point form; one case three times in a row (the per-slab
+    # counters reset themselves). Aligned operands, so that the streamed kernel is the one chosen.
+    d = device()
+    gemm = og.Int8Gemm(d)
+    shapes = [(1, 16, 4, 1), (1, 256, 64, 1), (4, 272, 100, 1), (16, 1024, 4096, 1), (7, 528, 1500, 1),
+              (16, 4096, 64, 1), (2, 4096, 8192, 1), (3, 512, 320, 3), (1, 11008, 4096, 1), (5, 48, 12, 2)]
+    bad_total = 0
+    for i, (m, n, k, batch) in enumerate(shapes):
+        a_s, b_s = (i & 1) != 0, (i & 2) == 0
+        za_mode, zb_mode = i % 3, (i // 3) % 3
+        c = cases.Case(f"stream {m}x{n}x{k} b{batch}", cases.problem(m, n, k, batch=batch), a_s, b_s, za_mode, zb_mode)
+        for rep in range(3 if i == 2 else 1):
+            say(f"stream case {c.name} signed {a_s}/{b_s} zp {za_mode}/{zb_mode} rep {rep}")
+            bad, kernel = run_int32(d, gemm, c, 100 + i)
+            assert kernel == "mfma-i8-rows16-stream", kernel
+            bad_total += bad
+    for vec in (False, True):
+        say(f"stream float vec {vec}")
+        bad_total += _float_case(d, gemm, 4, 256, 128, vec, True, True, 77 + vec)
+    say(f"ROW int8 gemm | streamed rows | mismatches {bad_total}")
+    assert bad_total == 0
