@@ -53,6 +53,8 @@ def _abi():
         _L.og_util_col_absmax_scale.argtypes = [ctypes.c_void_p, _Buf, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_float,
                                                 _Buf]
         _L.og_util_scale_product.argtypes = [ctypes.c_void_p, _Buf, _Buf, ctypes.c_uint32, _Buf]
+        _L.og_timing_region_begin.argtypes = [ctypes.c_void_p]
+        _L.og_timing_region_end.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_float)]
         _L.og_last_error.argtypes = [ctypes.c_void_p]
         _L.og_last_error.restype = ctypes.c_char_p
     return _L
@@ -90,24 +92,34 @@ def sym_weights(d, k, n, seed, tensor):
 # ------------------------------------------------------------------ timing
 
 def timed(d, record, steps, warmup):
-    """Runs `record(encoder, i)` warmup times untimed, then `steps` times in one encoder with per-dispatch events.
-    Returns (wall seconds for the timed steps, [(ms, kernel)] per dispatch)."""
+    """Runs `record(encoder, i)` warmup times untimed; then `steps` times back to back in one encoder, bracketed by
+    device synchronisation for the wall time and by one HIP event pair on the library's stream for the device time;
+    then `steps` more times with an event pair around every dispatch, for the kernel names and a per-dispatch split.
+    Returns (wall seconds, event seconds of the back-to-back steps, [(ms, kernel)] per dispatch of the second run)."""
+    L = _abi()
     for i in range(warmup):
         e = d.BeginCommands()
         record(e, i)
         d.Submit(e)
     d.WaitIdle()
     e = d.BeginCommands()
-    e.BeginPassTiming(steps)
     for i in range(steps):
         record(e, warmup + i)
-    e.EndPassTiming()
-    d.WaitIdle()
+    region = ctypes.c_float(0.0)
     t0 = time.perf_counter()
+    _ok(L.og_timing_region_begin(d.Context), d)
     d.Submit(e)
+    _ok(L.og_timing_region_end(d.Context, ctypes.byref(region)), d)
     d.WaitIdle()
     wall = time.perf_counter() - t0
-    return wall, d.ReadPassTimes()
+    e = d.BeginCommands()
+    e.BeginPassTiming(steps)
+    for i in range(steps):
+        record(e, warmup + steps + i)
+    e.EndPassTiming()
+    d.Submit(e)
+    d.WaitIdle()
+    return wall, region.value * 1e-3, d.ReadPassTimes()
 
 
 def kernel_stats(times, name_prefix=None):
@@ -127,10 +139,10 @@ def c4_square(d, steps, warmup, check=True):
     gemm = og.Int8Gemm(d)
     p = og.Int8GemmProblem(M, N, K)
     zpa = og.Int8Operand(za, 0, True)
-    wall, times = timed(d, lambda e, i: gemm.EncodeInt32(e, p, a, b, c, zpa), steps, warmup)
-    mean_ms, med_ms, kname = kernel_stats(times)
-    res = {"ops": 2.0 * M * N * K, "wall_s": wall, "kernel_mean_ms": mean_ms, "kernel_median_ms": med_ms,
-           "kernel": kname, "bytes": M * K + K * N + M + 4 * M * N}
+    wall, region, times = timed(d, lambda e, i: gemm.EncodeInt32(e, p, a, b, c, zpa), steps, warmup)
+    pair_ms, pair_med_ms, kname = kernel_stats(times)
+    res = {"ops": 2.0 * M * N * K, "wall_s": wall, "kernel_mean_ms": region / steps * 1e3,
+           "event_pair_mean_ms": pair_ms, "kernel": kname, "bytes": M * K + K * N + M + 4 * M * N}
     if check:
         import oracle
         rows = np.array([0, 1, 777, 2048, 4095])
@@ -163,18 +175,19 @@ def c3_gemv(d, m, steps, warmup, copies=9, check=True):
     gemm = og.Int8Gemm(d)
     p = og.Int8GemmProblem(m, N, K)
     zpa = og.Int8Operand(z, 0)
-    wall, times = timed(d, lambda e, i: gemm.EncodeFloat(e, p, ya, ws[i % copies][0], c,
-                                                          og.Int8Operand(ws[i % copies][1], 0, True), zpa), steps, warmup)
+    wall, region, times = timed(d, lambda e, i: gemm.EncodeFloat(e, p, ya, ws[i % copies][0], c,
+                                                                  og.Int8Operand(ws[i % copies][1], 0, True), zpa),
+                                steps, warmup)
     # A few-rows product may be split into two dispatches (partial sums, then their sum); its time is both.
     n_disp = len(times) // steps
     step_ms = [sum(times[i * n_disp + j][0] for j in range(n_disp)) for i in range(steps)]
     bytes_ = K * N + m * K + 4 * m * N + 4 * N + 4 + 1
-    res = {"m": m, "ops": 2.0 * m * N * K, "bytes": bytes_, "wall_s": wall, "step_mean_ms": statistics.mean(step_ms),
-           "step_median_ms": statistics.median(step_ms), "kernels": [k for _, k in times[:n_disp]],
+    res = {"m": m, "ops": 2.0 * m * N * K, "bytes": bytes_, "wall_s": wall, "step_mean_ms": region / steps * 1e3,
+           "event_pair_step_mean_ms": statistics.mean(step_ms), "kernels": [k for _, k in times[:n_disp]],
            "dispatch_mean_ms": [statistics.mean(times[i * n_disp + j][0] for i in range(steps)) for j in range(n_disp)]}
     if check:
         import oracle
-        last = (warmup + steps - 1) % copies
+        last = (warmup + 2 * steps - 1) % copies   # the weight copy of the last launch timed() recorded
         q, sc = ws[last]
         Y, Z, Q, SC = ya.Read(), int(z.Read()[0]), q.Read(), sc.Read()
         sums = oracle.int8_gemm(oracle.Gemm(m, N, K), Y, False, Q.view(np.uint8), True, (np.array([Z], np.uint8), False, 0))
@@ -207,12 +220,13 @@ def c2_bert_ffn(d, steps, warmup, check=True):
     dq.Encode(e0, x, 0, M * K, ya, 0, s, 0, z, 0)
     d.Submit(e0)
     _ok(_abi().og_util_scale_product(d.Context, _b(s), _b(wscale), N, _b(sc)), d)
-    wall, times = timed(d, step, steps, warmup)
+    wall, region, times = timed(d, step, steps, warmup)
     n_disp = len(times) // steps
     per = {}
     for t, k in times:
         per.setdefault(k, []).append(t)
-    res = {"ops": 2.0 * M * N * K, "wall_s": wall, "dispatch_mean_ms": {k: statistics.mean(v) for k, v in per.items()},
+    res = {"ops": 2.0 * M * N * K, "wall_s": wall, "chain_mean_ms": region / steps * 1e3,
+           "dispatch_mean_ms": {k: statistics.mean(v) for k, v in per.items()},
            "bytes_gemm": M * K + K * N + 4 * M * N + 4 * N, "bytes_dq": 4 * M * K + M * K + 5}
     if check:
         import oracle
@@ -245,9 +259,9 @@ def c5_batched(d, steps, warmup, check=True):
     p = og.Int8GemmProblem(M, N, K)
     p.Batch, p.StrideA, p.StrideB = Bt, M * K, K * N
     zpa = og.Int8Operand(z, 0)
-    wall, times = timed(d, lambda e, i: gemm.EncodeInt32(e, p, ya, b, c, zpa), steps, warmup)
-    mean_ms, med_ms, kname = kernel_stats(times)
-    res = {"ops": 2.0 * Bt * M * N * K, "wall_s": wall, "kernel_mean_ms": mean_ms, "kernel": kname,
+    wall, region, times = timed(d, lambda e, i: gemm.EncodeInt32(e, p, ya, b, c, zpa), steps, warmup)
+    kname = kernel_stats(times)[2]
+    res = {"ops": 2.0 * Bt * M * N * K, "wall_s": wall, "kernel_mean_ms": region / steps * 1e3, "kernel": kname,
            "bytes": Bt * (M * K + K * N + 4 * M * N)}
     if check:
         import oracle
@@ -260,22 +274,24 @@ def c5_batched(d, steps, warmup, check=True):
     return res
 
 
-def cpu_baseline_c4(host_operands, budget_s=12.0):
-    """The oracle (reference-semantics CPU restatement) on rows of the 4096^3 product until ~budget_s of work."""
+def cpu_baseline_c4(host_operands, budget_s=10.0):
+    """The oracle (reference-semantics CPU restatement) on rows of the 4096^3 product, repeated over the rows until
+    about budget_s of CPU work (a whole pass of 4096 rows takes well under a second on a many-core host)."""
     import oracle
     A, B, Z = host_operands
     M = N = K = 4096
     threads = max(1, min(16, os.cpu_count() or 1))
     rows_done, t_total = 0, 0.0
     chunk = max(threads, 16)
-    while t_total < budget_s and rows_done < M:
-        rows = np.arange(rows_done, min(M, rows_done + chunk))
+    while t_total < budget_s:
+        start = rows_done % M
+        rows = np.arange(start, min(M, start + chunk))
         t0 = time.perf_counter()
         oracle.int8_gemm_rows(oracle.Gemm(M, N, K), A, False, B.view(np.uint8), True, rows, (Z, True, 0), threads=threads)
         dt = time.perf_counter() - t0
         t_total += dt
         rows_done += len(rows)
-        if dt < budget_s / 8:
+        if dt < budget_s / 16 and chunk < M:
             chunk *= 2
     ops = 2.0 * rows_done * N * K
     cpu = "unknown"
@@ -288,8 +304,51 @@ def cpu_baseline_c4(host_operands, budget_s=12.0):
     except OSError:
         pass
     return {"value": ops / t_total / 1e12, "unit": "TOPS", "cores": threads, "kind": "port",
-            "sample": f"{rows_done} of 4096 rows of the 4096^3 product (u8 A with per-row zero point x int8 B), "
-                      f"{t_total:.1f} s, oracle/oracle.c ora_int8_gemm_rows on {threads} threads of {cpu}"}
+            "sample": f"{rows_done} rows ({rows_done / M:.1f} passes over the 4096 rows) of the 4096^3 product (u8 A "
+                      f"with per-row zero point x int8 B), {t_total:.1f} s, oracle/oracle.c ora_int8_gemm_rows on {threads} threads of {cpu}"}
+
+
+def traffic_of(kernel, workload):
+    """HBM bytes per launch of `kernel` on `workload` from profiles/traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE per
+    dispatch, scaled by the same counters' reading for a device copy of known size), or None when not measured."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    e = t.get("kernels", {}).get(f"{kernel} {workload}")
+    return None if e is None else e.get("hbm_bytes_per_launch")
+
+
+def copy_workload(d, steps, warmup, mib=256):
+    """A device-to-device copy of a known size (the counters' calibration for the traffic figures)."""
+    n = mib << 20
+    src, dst = d.CreateBufferOf(og.ElementType.UInt8, n), d.CreateBufferOf(og.ElementType.UInt8, n)
+    L = _abi()
+    L.og_memcpy_d2d.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64]
+    for _ in range(warmup + steps):
+        _ok(L.og_memcpy_d2d(d.Context, dst.DevicePointer, src.DevicePointer, n), d)
+    d.WaitIdle()
+    return {"bytes_read": n, "bytes_written": n, "launches": warmup + steps}
+
+
+def only(d, name, steps, warmup):
+    """One workload alone (for rocprofv3 runs of committed files); prints a one-line summary."""
+    if name == "c4":
+        r = c4_square(d, steps, warmup, check=False)
+        r.pop("host_operands", None)
+    elif name.startswith("gemv"):
+        r = c3_gemv(d, int(name[4:] or 1), steps, warmup, check=False)
+    elif name == "c2":
+        r = c2_bert_ffn(d, steps, warmup, check=False)
+    elif name == "c5":
+        r = c5_batched(d, steps, warmup, check=False)
+    elif name == "copy":
+        r = copy_workload(d, steps, warmup)
+    else:
+        raise SystemExit(f"unknown workload {name}")
+    print(json.dumps({"workload": name, **{k: v for k, v in r.items() if isinstance(v, (int, float, str, list))}}))
 
 
 def main():
@@ -299,6 +358,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline configuration only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", choices=["c4", "gemv1", "gemv4", "gemv16", "c2", "c5", "copy"],
+                    help="run one workload alone and print its summary (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported (see DESIGN.md for "
@@ -306,13 +367,17 @@ def main():
         sys.exit(2)
     d = og.GpuDevice.Create(0)
     log = lambda s: print(s, file=sys.stderr, flush=True)  # noqa: E731
+    if args.only:
+        only(d, args.only, args.steps, args.warmup)
+        return
 
     log("config 4: 4096^3 MatMulInteger")
     c4 = c4_square(d, args.steps, args.warmup)
     tops = c4["ops"] * args.steps / c4["wall_s"] / 1e12
     kern_tops = c4["ops"] / (c4["kernel_mean_ms"] * 1e-3) / 1e12
     configs = {"c4_square_4096": {"tops_wall": tops, "tops_kernel": kern_tops, "kernel": c4["kernel"],
-                                  "kernel_mean_us": c4["kernel_mean_ms"] * 1e3, "check": c4["check"]}}
+                                  "kernel_mean_us": c4["kernel_mean_ms"] * 1e3,
+                                  "event_pair_mean_us": c4["event_pair_mean_ms"] * 1e3, "check": c4["check"]}}
     log(json.dumps(configs["c4_square_4096"]))
 
     gemv = {}
@@ -322,7 +387,8 @@ def main():
         gbs = r["bytes"] / (r["step_mean_ms"] * 1e-3) / 1e9
         gemv[m] = {"gbs": gbs, "frac": gbs / PEAK_HBM_GBS, "step_mean_us": r["step_mean_ms"] * 1e3,
                    "tops": r["ops"] / (r["step_mean_ms"] * 1e-3) / 1e12, "kernels": r["kernels"],
-                   "dispatch_mean_us": [t * 1e3 for t in r["dispatch_mean_ms"]], "bytes": r["bytes"],
+                   "dispatch_mean_us": [t * 1e3 for t in r["dispatch_mean_ms"]],
+                   "event_pair_step_mean_us": r["event_pair_step_mean_ms"] * 1e3, "bytes": r["bytes"],
                    "check": r["check"]}
         configs[f"c3_gemv_m{m}"] = gemv[m]
         log(json.dumps(gemv[m]))
@@ -330,6 +396,7 @@ def main():
         log("config 2: BERT FFN chain")
         r = c2_bert_ffn(d, args.steps, args.warmup)
         configs["c2_bert_ffn"] = {"chain_wall_us": r["wall_s"] / args.steps * 1e6,
+                                  "chain_mean_us": r["chain_mean_ms"] * 1e3,
                                   "dispatch_mean_us": {k: v * 1e3 for k, v in r["dispatch_mean_ms"].items()},
                                   "check": r["check"]}
         log(json.dumps(configs["c2_bert_ffn"]))
@@ -340,9 +407,10 @@ def main():
         log(json.dumps(configs["c5_batched"]))
 
     roof = {"bound": "mfma", "achieved": kern_tops, "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
-            "frac": kern_tops / PEAK_INT8_TOPS, "traffic": None,
-            "note": "int8 ops (a multiply-add counts 2), 2*M*N*K per launch over the mean HIP-event launch time; "
-                    "unit is tera-ops/s"}
+            "frac": kern_tops / PEAK_INT8_TOPS, "traffic": traffic_of(c4["kernel"], "c4"),
+            "note": "int8 ops (a multiply-add counts 2), 2*M*N*K per launch over the average launch duration (one HIP "
+                    "event pair on the library's stream around the back-to-back timed launches, / steps); unit is "
+                    "tera-ops/s"}
     cpu = None if args.no_cpu else cpu_baseline_c4(c4["host_operands"])
     g1 = gemv.get(1)
     line = {
@@ -356,7 +424,7 @@ def main():
             "metric": "GB/s at M=1 K=4096 N=11008 (MatMulIntegerToFloat, 9 rotating weight copies)",
             "value": round(g1["gbs"], 1), "unit": "GB/s",
             "roofline": {"bound": "hbm", "achieved": g1["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": g1["frac"], "traffic": None}},
+                         "frac": g1["frac"], "traffic": traffic_of(g1["kernels"][0], "gemv1")}},
         "cpu_baseline": cpu,
         "configs": configs,
     }

@@ -80,6 +80,11 @@ int og_fill_bytes(og_ctx *ctx, void *dst, uint8_t value, uint64_t bytes);
 int og_timing_begin(og_ctx *ctx, int max_dispatches);
 int og_timing_end(og_ctx *ctx, int *dispatches);
 int og_timing_read(og_ctx *ctx, int index, float *ms, const char **kernel_name);
+/* One event pair around everything recorded between the two calls (GpuCommandEncoder.BeginPassTiming /
+ * EndPassTiming around a whole run of passes, Resources.cs:216-222): back-to-back launches stay back to back.
+ * og_timing_region_end waits for the stop event and returns the elapsed milliseconds. */
+int og_timing_region_begin(og_ctx *ctx);
+int og_timing_region_end(og_ctx *ctx, float *ms);
 
 /* ------------------------------------------------------------------ Int8Gemm */
 

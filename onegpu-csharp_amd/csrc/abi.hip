@@ -29,6 +29,8 @@ struct og_ctx {
     int timing_n = 0;
     std::vector<hipEvent_t> ev_start, ev_stop;
     std::vector<const char *> ev_name;
+    hipEvent_t region_start = nullptr, region_stop = nullptr;
+    bool region_open = false;
 };
 
 namespace {
@@ -183,6 +185,8 @@ int og_destroy(og_ctx *ctx)
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     for (auto e : ctx->ev_start) (void)hipEventDestroy(e);
     for (auto e : ctx->ev_stop) (void)hipEventDestroy(e);
+    if (ctx->region_start) (void)hipEventDestroy(ctx->region_start);
+    if (ctx->region_stop) (void)hipEventDestroy(ctx->region_stop);
     if (ctx->ws.partials) (void)hipFree(ctx->ws.partials);
     if (ctx->ws.dq_ranges) (void)hipFree(ctx->ws.dq_ranges);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
@@ -274,10 +278,13 @@ int og_timing_begin(og_ctx *ctx, int max_dispatches)
     if (!ctx) return fail(ctx, OG_ERR_INVALID_ARG, "ctx", "null context");
     if (max_dispatches < 1) return fail(ctx, OG_ERR_INVALID_ARG, "max_dispatches", "must be at least 1, got %d", max_dispatches);
     (void)hipSetDevice(ctx->device);
+    // Timing-only events: no system-scope fence (an L2 writeback and invalidate) when an event completes, so a pair
+    // around a short dispatch measures the dispatch rather than the cache maintenance.
+    constexpr unsigned kTimingEvent = hipEventDisableSystemFence;
     while ((int)ctx->ev_start.size() < max_dispatches) {
         hipEvent_t a, b;
-        if (hipEventCreate(&a) != hipSuccess) return fail(ctx, OG_ERR_OUT_OF_MEMORY, nullptr, "hipEventCreate");
-        if (hipEventCreate(&b) != hipSuccess) { (void)hipEventDestroy(a); return fail(ctx, OG_ERR_OUT_OF_MEMORY, nullptr, "hipEventCreate"); }
+        if (hipEventCreateWithFlags(&a, kTimingEvent) != hipSuccess) return fail(ctx, OG_ERR_OUT_OF_MEMORY, nullptr, "hipEventCreate");
+        if (hipEventCreateWithFlags(&b, kTimingEvent) != hipSuccess) { (void)hipEventDestroy(a); return fail(ctx, OG_ERR_OUT_OF_MEMORY, nullptr, "hipEventCreate"); }
         ctx->ev_start.push_back(a);
         ctx->ev_stop.push_back(b);
         ctx->ev_name.push_back("");
@@ -307,6 +314,34 @@ int og_timing_read(og_ctx *ctx, int index, float *ms, const char **kernel_name)
     if (e != hipSuccess) return hip_status(ctx, e, "og_timing_read");
     if (ms) *ms = t;
     if (kernel_name) *kernel_name = ctx->ev_name[index];
+    return ok(ctx);
+}
+
+int og_timing_region_begin(og_ctx *ctx)
+{
+    if (!ctx) return fail(ctx, OG_ERR_INVALID_ARG, "ctx", "null context");
+    (void)hipSetDevice(ctx->device);
+    for (hipEvent_t *e : {&ctx->region_start, &ctx->region_stop})
+        if (!*e && hipEventCreateWithFlags(e, hipEventDisableSystemFence) != hipSuccess)
+            return fail(ctx, OG_ERR_OUT_OF_MEMORY, nullptr, "hipEventCreate");
+    hipError_t e = hipEventRecord(ctx->region_start, ctx->stream);
+    if (e != hipSuccess) return hip_status(ctx, e, "og_timing_region_begin");
+    ctx->region_open = true;
+    return ok(ctx);
+}
+
+int og_timing_region_end(og_ctx *ctx, float *ms)
+{
+    if (!ctx) return fail(ctx, OG_ERR_INVALID_ARG, "ctx", "null context");
+    if (!ctx->region_open) return fail(ctx, OG_ERR_INVALID_ARG, "ctx", "og_timing_region_begin was not called");
+    ctx->region_open = false;
+    (void)hipSetDevice(ctx->device);
+    hipError_t e = hipEventRecord(ctx->region_stop, ctx->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(ctx->region_stop);
+    float t = 0.0f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&t, ctx->region_start, ctx->region_stop);
+    if (e != hipSuccess) return hip_status(ctx, e, "og_timing_region_end");
+    if (ms) *ms = t;
     return ok(ctx);
 }
 

@@ -298,3 +298,29 @@ def test_streamed_rows_are_bit_exact():
         bad_total += _float_case(d, gemm, 4, 256, 128, vec, True, True, 77 + vec)
     say(f"ROW int8 gemm | streamed rows | mismatches {bad_total}")
     assert bad_total == 0
+
+
+def test_golden_fixtures_on_every_kernel():
+    # The committed smoke and closed-form fixtures (tests/golden) through every kernel the chooser and the test hooks
+    # reach, bit for bit.
+    import os
+    golden = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    f = np.load(os.path.join(golden, "c1_smoke.npz"), allow_pickle=False)
+    m, n, k = (int(v) for v in f["shape"])
+    cf = np.load(os.path.join(golden, "closed_form.npz"), allow_pickle=False)
+    d = device()
+    ba, bb = d.CreateBuffer(f["a"]), d.CreateBuffer(f["b"])
+    bza, bzb = d.CreateBuffer(f["za"]), d.CreateBuffer(f["zb"])
+    ca, cb = d.CreateBuffer(cf["a"]), d.CreateBuffer(cf["b"])
+    bad = 0
+    for config, gemm in configs(d, True):
+        c = d.CreateBufferOf(og.ElementType.Int32, m * n)
+        run(d, lambda e: gemm.EncodeInt32(e, og.Int8GemmProblem(m, n, k), ba, bb, c, og.Int8Operand(bza, 0),
+                                          og.Int8Operand(bzb, 0, True)))
+        got = c.Read()
+        say(f"golden smoke [{config}] {d.LastKernel}: {int(np.count_nonzero(got != f['c']))} mismatches")
+        bad += int(np.count_nonzero(got != f["c"]))
+        c2 = d.CreateBufferOf(og.ElementType.Int32, 6)
+        run(d, lambda e: gemm.EncodeInt32(e, og.Int8GemmProblem(2, 3, 2), ca, cb, c2))
+        bad += int(np.count_nonzero(c2.Read() != cf["c"]))
+    assert bad == 0

@@ -101,3 +101,24 @@ def test_quantize_is_exact():
                 seed += 1
                 count += 1
     assert bad == 0
+
+
+def test_dynamic_quantize_golden_fixture():
+    # The committed DynamicQuantizeLinear fixture (tests/golden/dq_vectors.npz) on the GPU quantizer, bit for bit.
+    import os
+    f = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "dq_vectors.npz"), allow_pickle=False)
+    d = device()
+    k = og.DynamicQuantizeKernels(d)
+    offs = f["offsets"]
+    bad = 0
+    for i in range(len(offs) - 1):
+        x = f["x"][offs[i]:offs[i + 1]]
+        bx, by = d.CreateBuffer(x), d.CreateBufferOf(og.ElementType.UInt8, x.size)
+        bs, bz = d.CreateBufferOf(og.ElementType.Float32, 1), d.CreateBufferOf(og.ElementType.UInt8, 4)
+        run(d, lambda e: k.Encode(e, bx, 0, x.size, by, 0, bs, 0, bz, 0))
+        here = int(np.count_nonzero(by.Read()[:x.size] != f["y"][offs[i]:offs[i + 1]]))
+        here += int(bs.Read()[0].view(np.uint32) != f["scale"][i].view(np.uint32)) + int(bz.Read()[0] != f["zero"][i])
+        if here:
+            say(f"MISMATCH dq fixture vector {i}: {here}")
+        bad += here
+    assert bad == 0
