@@ -102,6 +102,9 @@ def test_float_epilogue_is_two_float32_roundings():
     acc = ((sums.astype(np.int64) + ib[cols] + 2**31) % 2**32 - 2**31).astype(np.int32)
     want = (acc.astype(np.float32) * scale[cols]).astype(np.float32) + fb[cols]
     np.testing.assert_array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
+    # One rounding instead of two (a multiply-add contracted to an FMA) gives different bits on these inputs.
+    fused = (acc.astype(np.float64) * scale[cols].astype(np.float64) + fb[cols]).astype(np.float32)
+    assert np.any(fused.view(np.uint32) != got.view(np.uint32))
     # Without biases, scalar scale.
     got = oracle.float_epilogue(sums, n, scale[:1], False)
     np.testing.assert_array_equal(got.view(np.uint32), (sums.astype(np.float32) * scale[0]).view(np.uint32))
