@@ -2,25 +2,26 @@
 // no staging registers), and B stored K x N is read in its own layout with the gfx950 transpose read
 // ds_read_b64_tr_b8, so no VALU transposition is needed.
 //
-//  - Tile 256 x 256 per workgroup, 64 deep per stage, 4 waves (2 x 2) of 128 x 128, v_mfma_i32_16x16x64_i8, a ring
-//    of 5 stages filling the 160 KB of LDS. K must be a multiple of 64 (other products take the register-staged
-//    kernel).
-//  - One wave per SIMD, so the wave's own instruction stream has to keep the matrix core busy: a 16-cycle MFMA leaves
-//    room for about two other instructions. Everything else in a stage is spread between the MFMAs and kept short:
-//    the DMA of a later stage (2 instructions a load), the fragment reads, one flip per unsigned A fragment, and the
-//    operands' byte sums (v_sad_u8, which issues beside an MFMA where v_dot4 does not).
+//  - Tile 256 x 256 per workgroup, 64 deep per stage, 4 waves (2 x 2) of 128 x 128, each 4 x 4 blocks of
+//    v_mfma_i32_32x32x32_i8, a ring of 5 stages filling the 160 KB of LDS. K must be a multiple of 64 (other products
+//    take the register-staged kernel).
+//  - One wave per SIMD, so the wave's own instruction stream has to keep the matrix core busy. The 32 x 32 x 32 MFMA
+//    (32 cycles) does the work of two 16 x 16 x 64 ones with the same fragment reads, and leaves room for about
+//    seven other instructions: the DMA of a later stage (2 instructions a load), the fragment reads, one flip per
+//    unsigned fragment, and the operands' byte sums (v_sad_u8, which issues beside an MFMA where v_dot4 does not).
 //  - Operands stay as stored in LDS; each MFMA fragment of an unsigned operand is moved to the signed domain
 //    (s = u ^ 0x80) after it is read, and the zero points are applied at the store from the byte sums:
 //        sum (s - z')(t - w') = sum s t - w' sum s - z' sum t + K z' w'   (mod 2^32; Int8GemmDot.hlsl:1-11 rearranges the same)
-//  - LDS layouts (16-byte chunks, conflict-free for the fragment reads as measured with SQ_LDS_BANK_CONFLICT):
+//  - LDS layouts (16-byte chunks):
 //      A (and B stored N x K): row r of 64 bytes, chunk q at position q ^ ((r >> 1) & 3);
 //      B stored K x N: row k of 256 bytes, chunk c at position c ^ fB(k), fB(k) = (k & 7) | (((k >> 4) & 1) << 3).
 //    A buffer load writes 64 lanes x 16 bytes to consecutive LDS, so each lane loads the global chunk that belongs in
 //    its slot.
-//  - A fragment (lane l: row l % 16, k 16 (l / 16) .. + 15) is one ds_read_b128. A B fragment (lane l: column l % 16,
-//    the same 16 k) is two ds_read_b64_tr_b8: within each 16-lane group, lane i < 8 receives byte i of the 8-byte
-//    segments the even lanes address and lane 8 + i byte i of the odd lanes' segments, so even lanes address rows
-//    k..k+7 at columns n..n+7 and odd lanes the same rows at columns n+8..n+15.
+//  - An A fragment (lane l: row l % 32, k 16 (l / 32) .. + 15 of a 32-deep half stage) is one ds_read_b128. A B
+//    fragment (lane l: column l % 32, the same 16 k) is two ds_read_b64_tr_b8: within each 16-lane group, lane i < 8
+//    receives byte i of the 8-byte segments the even lanes address and lane 8 + i byte i of the odd lanes' segments,
+//    so even lanes address rows k..k+7 at columns n..n+7 and odd lanes the same rows at columns n+8..n+15. A and B
+//    give byte b of a lane the same k, which is all the MFMA's sum needs.
 #pragma once
 
 #include <type_traits>
@@ -30,6 +31,7 @@
 namespace og {
 
 typedef int32_t v4i __attribute__((ext_vector_type(4)));
+typedef int32_t v16i __attribute__((ext_vector_type(16)));
 typedef int32_t v2i __attribute__((ext_vector_type(2)));
 typedef uint32_t u4w __attribute__((ext_vector_type(4)));
 #define OG_LDS2(p) ((__attribute__((address_space(3))) v2i *)(p))
@@ -107,7 +109,7 @@ __device__ __forceinline__ v4i to_signed(v4i v)
     else return v;
 }
 
-__device__ __forceinline__ v4i mfma(v4i a, v4i b, v4i c) { return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0); }
+__device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) { return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0); }
 
 // Sum of the 16 bytes of a fragment read as unsigned, added to acc (v_sad_u8 against zero). Applied to biased bytes
 // (signed-domain value + 128, i.e. value ^ 0x80): the signed sum is the biased sum minus 128 per byte.
@@ -155,10 +157,12 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int i16 = lane & 15, g4 = lane >> 4;
+    const int i32 = lane & 31, h2 = lane >> 5;   // MFMA roles: row / column within a 32-block, k half
+    const int i16 = lane & 15, g4 = lane >> 4;   // transpose-read roles
     const int wm = wave >> 1, wn = wave & 1;
 
-    // Tile order: an XCD-contiguous run of tiles, walked in groups of 8 row-tiles (see the aligned kernel).
+    // Tile order: the hardware deals workgroups round-robin to the 8 XCDs; remap so that each XCD gets one contiguous
+    // run of tiles, walked in groups of 8 row tiles, and the A and B tiles the run reuses stay in its L2.
     const int64_t tiles = (int64_t)tiles_n * tiles_m;
     const int64_t nblocks = tiles * g.batch;
     int64_t bid = blockIdx.x;
@@ -243,110 +247,118 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
         else dma16<U * STAGE + A_STAGE + (I - LOADS_A) * 4096>(rr.b, wave_lds, off_b[I - LOADS_A]);
     };
 
-    // Fragments as stored (unsigned operands not yet flipped) from ring buffer u.
-    auto read_a = [&](int u, int i) {
-        const int r = wm * 128 + 16 * i + i16;
-        return *reinterpret_cast<const v4i *>(smem + u * STAGE + r * 64 + 16 * a_pos(r, g4));
+    // Fragments as stored (unsigned operands not yet flipped) from ring buffer u. A: row block i (32 rows) at k half
+    // ks; lane l holds row 32 i + l % 32, k 32 ks + 16 (l / 32) .. + 15: one ds_read_b128.
+    auto read_a = [&](int u, int i, int ks) {
+        const int r = wm * 128 + 32 * i + i32;
+        return *reinterpret_cast<const v4i *>(smem + u * STAGE + r * 64 + 16 * a_pos(r, 2 * ks + h2));
     };
-    auto read_b = [&](int u, v4i (&bf)[8], int j0, int j1) {
+    // B: column block j (32 columns) at k half ks; lane l holds column 32 j + l % 32 and the same 16 k as A.
+    auto read_b = [&](int u, int j, int ks) -> v4i {
         const uint8_t *bs = smem + u * STAGE + A_STAGE;
+        if constexpr (TRANS_B) {
+            const int r = wn * 128 + 32 * j + i32;
+            return *reinterpret_cast<const v4i *>(bs + r * 64 + 16 * a_pos(r, 2 * ks + h2));
+        } else {
+            // Each 16-lane group g transposes 16 columns (16 (g & 1) .. + 15 of the block) x 8 rows per read; groups
+            // 2 and 3 take the second 16 k.
+            const int c = (wn * 128 + 32 * j + 16 * (g4 & 1)) >> 4;   // 16-byte chunk of the group's columns
+            v2i h[2];
 #pragma unroll
-        for (int j = j0; j < j1; j++) {
-            const int nl = wn * 128 + 16 * j;   // first column of the block
-            if constexpr (TRANS_B) {
-                const int r = nl + i16;
-                bf[j] = *reinterpret_cast<const v4i *>(bs + r * 64 + 16 * a_pos(r, g4));
-            } else {
-                const int c = nl >> 4;   // 16-byte chunk of the block's columns
-                v2i h[2];
-#pragma unroll
-                for (int hh = 0; hh < 2; hh++) {
-                    const int k = 16 * g4 + 8 * hh + (i16 >> 1);
-                    h[hh] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(OG_LDS2(bs + k * DBN + 16 * b_pos(k, c) + 8 * (i16 & 1)));
-                }
-                bf[j] = (v4i){h[0].x, h[0].y, h[1].x, h[1].y};
+            for (int hh = 0; hh < 2; hh++) {
+                const int k = 32 * ks + 16 * (g4 >> 1) + 8 * hh + (i16 >> 1);
+                h[hh] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(OG_LDS2(bs + k * DBN + 16 * b_pos(k, c) + 8 * (i16 & 1)));
             }
+            return (v4i){h[0].x, h[0].y, h[1].x, h[1].y};
         }
     };
 
-    v4i acc[8][8];
+    v16i acc[4][4];
 #pragma unroll
-    for (int i = 0; i < 8; i++)
+    for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 8; j++) acc[i][j] = (v4i){0, 0, 0, 0};
-    // This lane's biased byte sums (its k-group, 16 bytes per stage) of the wave's A rows / B columns, block by block.
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+    // This lane's biased byte sums (its k half, 16 bytes per fragment) of the wave's A row blocks / B column blocks.
     // Biased bytes: an unsigned operand's bytes as stored, a signed one's with the top bit flipped.
-    uint32_t rs[8], cs[8];
+    uint32_t rs[4], cs[4];
 #pragma unroll
-    for (int i = 0; i < 8; i++) { rs[i] = 0; cs[i] = 0; }
-    // VALU instructions per block beside the MFMAs: byte sums, and the flip of the next A fragment.
-    constexpr int VS = (SUM_A ? (FLIP_A ? 4 : 8) : 0) + (SUM_B ? (FLIP_B ? 4 : 8) : 0), VF = FLIP_A ? 4 : 0;
+    for (int i = 0; i < 4; i++) { rs[i] = 0; cs[i] = 0; }
+    // VALU instructions per block beside the MFMAs: byte sums of two A and two B fragments, and the flips of the two
+    // A and two B fragments read in the block.
+    constexpr int VS = (SUM_A ? (FLIP_A ? 8 : 16) : 0) + (SUM_B ? 16 : 0);
+    constexpr int VF = (FLIP_A ? 8 : 0) + (FLIP_B ? 8 : 0);
+    constexpr int DS = 2 + (TRANS_B ? 2 : 4);
 
     const int32_t nk = K / DBK;   // K is a multiple of DBK here
 
-    // Prologue: stages 0 .. NS - 2 in flight; stage 0 landed and its first fragments read.
+    // Prologue: stages 0 .. NS - 2 in flight; stage 0 landed, its first k half of B and the first block's A read.
     static_for<0, NS - 1>([&](auto u_tag) {
         const StageRsrc r = stage_rsrc(decltype(u_tag)::value * DBK);
         static_for<0, LOADS>([&](auto i_tag) { dma(u_tag, i_tag, r); });
     });
     wait_vm_barrier<LOADS * (NS - 2)>();
-    // The stage being computed: its B fragments and current A fragment in the signed domain, and both as stored
-    // where an unsigned operand's byte sums need them.
-    v4i bf[8], a_cur, a_st, b_st[FLIP_B && SUM_B ? 8 : 1];
-    {
-        v4i nb[8];
-        read_b(0, nb, 0, 8);
+    // B fragments in the signed domain, [k half][column block]; the current block's A fragments as stored and signed.
+    v4i bf[2][4], a_st[2], a_cur[2];
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            bf[j] = to_signed<FLIP_B>(nb[j]);
-            if constexpr (FLIP_B && SUM_B) b_st[j] = nb[j];
-        }
-        a_st = read_a(0, 0);
-        a_cur = to_signed<FLIP_A>(a_st);
+    for (int j = 0; j < 4; j++) bf[0][j] = to_signed<FLIP_B>(read_b(0, j, 0));
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        a_st[t] = read_a(0, t, 0);
+        a_cur[t] = to_signed<FLIP_A>(a_st[t]);
     }
-    auto sum_a = [&](uint32_t acc) { return FLIP_A ? sad16(a_st, acc) : sad16(a_cur ^ (int32_t)0x80808080, acc); };
-    auto sum_b = [&](int j, uint32_t acc) {
-        if constexpr (FLIP_B) return sad16(b_st[SUM_B ? j : 0], acc);
-        else return sad16(bf[j] ^ (int32_t)0x80808080, acc);
-    };
 
-    // One stage s in ring buffer U, in 8 blocks (one A fragment against the 8 B fragments, plus the sums). Block i
-    // reads the A fragment of block i + 1 (block 7: the first of stage s + 1). At block 4 the waves wait for stage
-    // s + 1 (this wave's loads landed, then everyone's) and meet: from then on nobody reads the buffer of stage s - 1,
-    // so blocks 4..7 each issue two loads of stage s + NS - 1 into it and read two B fragments of stage s + 1,
-    // spreading the DMA and the LDS reads over the stage. Stages past the last still wait and read (their loads cover
-    // empty or unused ranges and what is read is not used), so every stage is the same.
+    // One stage s in ring buffer U, in 4 blocks of 8 MFMAs: block b multiplies A row blocks 2 (b & 1), + 1 at k half
+    // b / 2 against the 4 B column blocks. Block b reads the A fragments of block b + 1 (block 3: the first of stage
+    // s + 1) and two B fragments: blocks 0, 1 this stage's second k half, blocks 2, 3 the next stage's first (whose
+    // registers are free once block 1 is done). At block 2 the waves wait for stage s + 1 (this wave's loads landed,
+    // then everyone's) and meet: from then on nobody reads the buffer of stage s - 1, so blocks 2 and 3 each issue
+    // four loads of stage s + NS - 1 into it. Stages past the last still wait and read (their loads cover empty or
+    // unused ranges and what is read is not used), so every stage is the same.
     auto run_stage = [&](auto u_tag, int32_t s) {
         constexpr int U = decltype(u_tag)::value, DU = (U + NS - 1) % NS, NU = (U + 1) % NS;
         const StageRsrc rr = stage_rsrc((s + NS - 1) * DBK);
-        v4i nb[8];
-        static_for<0, 8>([&](auto i_tag) {
-            constexpr int i = decltype(i_tag)::value;
-            if constexpr (i == 4) {
+        static_for<0, 4>([&](auto b_tag) {
+            constexpr int b = decltype(b_tag)::value, ks = b >> 1, i0 = 2 * (b & 1);
+            constexpr int rks = b < 2 ? 1 : 0, rj = 2 * (b & 1), RU = b < 2 ? U : NU;
+            constexpr int nb = (b + 1) & 3, AU = b < 3 ? U : NU;
+            if constexpr (b == 2) {
                 wait_vm_lgkm_barrier<LOADS * (NS - 3)>();   // stages s + 2 .. s + NS - 2 may still be in flight
                 __builtin_amdgcn_sched_barrier(0);
             }
-            if constexpr (i >= 4) {
-                dma(std::integral_constant<int, DU>{}, std::integral_constant<int, 2 * (i - 4)>{}, rr);
-                dma(std::integral_constant<int, DU>{}, std::integral_constant<int, 2 * (i - 4) + 1>{}, rr);
-                read_b(NU, nb, 2 * (i - 4), 2 * (i - 4) + 2);
+            if constexpr (b >= 2) {
+                static_for<0, 4>([&](auto q_tag) {
+                    dma(std::integral_constant<int, DU>{}, std::integral_constant<int, 4 * (b - 2) + decltype(q_tag)::value>{}, rr);
+                });
             }
-            const v4i a_raw = i < 7 ? read_a(U, i + 1) : read_a(NU, 0);
-            if constexpr (SUM_A) rs[i] = sum_a(rs[i]);   // every wave sums (no branch in the block); one publishes
-            if constexpr (SUM_B) cs[i] = sum_b(i, cs[i]);
+            const v4i b0 = read_b(RU, rj, rks), b1 = read_b(RU, rj + 1, rks);
+            v4i a_nx[2];
+            a_nx[0] = read_a(AU, 2 * (nb & 1), nb >> 1);
+            a_nx[1] = read_a(AU, 2 * (nb & 1) + 1, nb >> 1);
+            if constexpr (SUM_A) {
 #pragma unroll
-            for (int j = 0; j < 8; j++) acc[i][j] = mfma(a_cur, bf[j], acc[i][j]);
-            a_st = a_raw;
-            a_cur = to_signed<FLIP_A>(a_raw);
-            sched_block<VS, VF, (i < 4 ? 1 : (TRANS_B ? 3 : 5))>();
+                for (int t = 0; t < 2; t++)
+                    rs[i0 + t] = FLIP_A ? sad16(a_st[t], rs[i0 + t]) : sad16(a_cur[t] ^ (int32_t)0x80808080, rs[i0 + t]);
+            }
+            if constexpr (SUM_B) {
+                cs[rj] = sad16(bf[ks][rj] ^ (int32_t)0x80808080, cs[rj]);
+                cs[rj + 1] = sad16(bf[ks][rj + 1] ^ (int32_t)0x80808080, cs[rj + 1]);
+            }
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i0 + t][j] = mfma32(a_cur[t], bf[ks][j], acc[i0 + t][j]);
+            bf[rks][rj] = to_signed<FLIP_B>(b0);
+            bf[rks][rj + 1] = to_signed<FLIP_B>(b1);
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                a_st[t] = a_nx[t];
+                a_cur[t] = to_signed<FLIP_A>(a_nx[t]);
+            }
+            sched_block<VS, VF, DS>();
             __builtin_amdgcn_sched_barrier(0);
         });
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            bf[j] = to_signed<FLIP_B>(nb[j]);
-            if constexpr (FLIP_B && SUM_B) b_st[j] = nb[j];
-        }
-        __builtin_amdgcn_sched_barrier(0);
     };
     static_assert(NS == 5, "the loop below is unrolled for 5 stages");
     for (int32_t kt = 0; kt < nk; kt += NS) {
@@ -365,23 +377,21 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
     float *const ColSc = reinterpret_cast<float *>(ColIB + DBN);
     float *const ColFb = ColSc + DBN;
 
-    // Byte sums: the four k-groups of a row / column sit in lanes l, l + 16, l + 32, l + 48. The biased sums cover 64
-    // bytes per stage; the signed sums are 128 less per byte (mod 2^32).
+    // Byte sums: the two k halves of a row / column sit in lanes l and l + 32. The biased sums cover 64 bytes per
+    // stage; the signed sums are 128 less per byte (mod 2^32).
     const uint32_t bias_total = 128u * (uint32_t)DBK * (uint32_t)nk;
     if (SUM_A && wn == 0) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            uint32_t v = rs[i] + (uint32_t)__shfl_xor((int32_t)rs[i], 16);
-            v += (uint32_t)__shfl_xor((int32_t)v, 32);
-            if (g4 == 0) RowSum[wm * 128 + 16 * i + i16] = (int32_t)(v - bias_total);
+        for (int i = 0; i < 4; i++) {
+            const uint32_t v = rs[i] + (uint32_t)__shfl_xor((int32_t)rs[i], 32);
+            if (h2 == 0) RowSum[wm * 128 + 32 * i + i32] = (int32_t)(v - bias_total);
         }
     }
     if (SUM_B && wm == 0) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            uint32_t v = cs[j] + (uint32_t)__shfl_xor((int32_t)cs[j], 16);
-            v += (uint32_t)__shfl_xor((int32_t)v, 32);
-            if (g4 == 0) ColSum[wn * 128 + 16 * j + i16] = (int32_t)(v - bias_total);
+        for (int j = 0; j < 4; j++) {
+            const uint32_t v = cs[j] + (uint32_t)__shfl_xor((int32_t)cs[j], 32);
+            if (h2 == 0) ColSum[wn * 128 + 32 * j + i32] = (int32_t)(v - bias_total);
         }
     }
     if (SUM_B) RowZ[tid] = a_signed ? sext8(za_raw) : (int32_t)za_raw - 128;
@@ -393,13 +403,14 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
 
     // Store. With z' = zero of A's row, w' = zero of B's column, s_m / t_n the byte sums of the row / column:
     //     C = acc - w' s_m - z' (t_n - K w')   (+ int bias; float: fl(fl(float(C)) * scale) (+ float bias))
-    // MFMA 16 x 16 output layout: lane l holds rows 4 (l / 16) + r, column l % 16 of each block.
+    // MFMA 32 x 32 output layout: lane l holds column l % 32 and, in register r, row 8 (r / 4) + 4 (l / 32) + r % 4
+    // of its block; one store writes two 128-byte row segments.
     const uint32_t Ku = (uint32_t)K;
-    uint32_t wz[8], ct[8], ib[8];
-    float sc[8], fb[8];
+    uint32_t wz[4], ct[4], ib[4];
+    float sc[4], fb[4];
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const int nl = wn * 128 + 16 * j + i16;
+    for (int j = 0; j < 4; j++) {
+        const int nl = wn * 128 + 32 * j + i32;
         wz[j] = SUM_A ? (uint32_t)ColW[nl] : 0u;
         ct[j] = SUM_B ? (uint32_t)ColSum[nl] - Ku * wz[j] : 0u;
         ib[j] = (uint32_t)ColIB[nl];
@@ -407,32 +418,35 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
         fb[j] = ColFb[nl];
     }
     int32_t *const Cb = static_cast<int32_t *>(g.C) + batch * g.strideC;   // int32 and float32 results alike
-    const int32_t ncol0 = n0 + wn * 128 + i16;
+    const int32_t ncol0 = n0 + wn * 128 + i32;
     const int32_t M = g.M, N = g.N;
     auto store_all = [&](auto float_tag, bool has_fb) {
         constexpr bool F = decltype(float_tag)::value;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int ml = wm * 128 + 16 * i + 4 * g4;
-            const v4i ssv = SUM_A ? *reinterpret_cast<const v4i *>(&RowSum[ml]) : (v4i){0, 0, 0, 0};
-            const v4i zzv = SUM_B ? *reinterpret_cast<const v4i *>(&RowZ[ml]) : (v4i){0, 0, 0, 0};
+        for (int i = 0; i < 4; i++) {
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int32_t m = m0 + ml + r;
-                if (m >= M) continue;
-                int32_t *const row = Cb + m * N;   // batch * M * N < 2^31 (checked at the boundary)
-                const uint32_t ss = (uint32_t)ssv[r], zz = (uint32_t)zzv[r];
+            for (int q = 0; q < 4; q++) {
+                const int ml = wm * 128 + 32 * i + 8 * q + 4 * h2;
+                const v4i ssv = SUM_A ? *reinterpret_cast<const v4i *>(&RowSum[ml]) : (v4i){0, 0, 0, 0};
+                const v4i zzv = SUM_B ? *reinterpret_cast<const v4i *>(&RowZ[ml]) : (v4i){0, 0, 0, 0};
 #pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const int32_t n = ncol0 + 16 * j;
-                    if (n >= N) continue;
-                    const uint32_t v = (uint32_t)acc[i][j][r] - wz[j] * ss - zz * ct[j] + ib[j];
-                    if constexpr (F) {
-                        float f = __fmul_rn((float)(int32_t)v, sc[j]);
-                        if (has_fb) f = __fadd_rn(f, fb[j]);
-                        row[n] = __float_as_int(f);
-                    } else {
-                        row[n] = (int32_t)v;
+                for (int r = 0; r < 4; r++) {
+                    const int32_t m = m0 + ml + r;
+                    if (m >= M) continue;
+                    int32_t *const row = Cb + m * N;   // batch * M * N < 2^31 (checked at the boundary)
+                    const uint32_t ss = (uint32_t)ssv[r], zz = (uint32_t)zzv[r];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int32_t n = ncol0 + 32 * j;
+                        if (n >= N) continue;
+                        const uint32_t v = (uint32_t)acc[i][j][4 * q + r] - wz[j] * ss - zz * ct[j] + ib[j];
+                        if constexpr (F) {
+                            float f = __fmul_rn((float)(int32_t)v, sc[j]);
+                            if (has_fb) f = __fadd_rn(f, fb[j]);
+                            row[n] = __float_as_int(f);
+                        } else {
+                            row[n] = (int32_t)v;
+                        }
                     }
                 }
             }
