@@ -124,7 +124,7 @@ typedef struct og_int8_gemm_params {
 #define OG_GEMM_NO_SKINNY     0x800u  /* never use the few-rows kernel (M <= 16) */
 #define OG_GEMM_NO_DIRECT     0x1000u /* never use the few-rows kernel's single-pass form (always split k) */
 #define OG_GEMM_LARGE_TILE    0x2000u /* take the 256 x 256 tile kernels whatever the size (with NO_SKINNY: every shape) */
-#define OG_GEMM_NO_STREAM     0x4000u /* never use the streamed few-rows kernel (the split-k one instead) */
+#define OG_GEMM_NO_STREAM     0x4000u /* never use the tiled few-rows kernel (the split-k one instead) */
 
 /* Epi (Int8GemmEpilogue.hlsli:1-12): bit 0 float32 result, bit 1 int32 bias per column, bit 2 scale per column (else one),
  * bit 3 float32 bias per column. 0 stores the raw int32 sums. */

@@ -153,15 +153,15 @@ int og_init(int device_ordinal, og_ctx **out)
         ctx->ws.partial_bytes = kInitialPartialBytes;
         void *p = nullptr;
         // ranges (2 * kDqMaxGroups floats), counter, result (2 floats), in one allocation
-        // + the streamed few-rows kernel's done-counters; all zero to start with
-        size_t bytes = 2 * og::kDqMaxGroups * sizeof(float) + 256 + 256 + og::kGemvMaxSlabs * sizeof(uint32_t);
+        size_t bytes = 2 * og::kDqMaxGroups * sizeof(float) + 256 + 256;
         e = hipMalloc(&p, bytes);
         if (e == hipSuccess) e = hipMemset(p, 0, bytes);
         if (e == hipSuccess) {
             ctx->ws.dq_ranges = static_cast<float *>(p);
             ctx->ws.dq_counter = reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(p) + 2 * og::kDqMaxGroups * sizeof(float));
             ctx->ws.dq_result = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(ctx->ws.dq_counter) + 256);
-            ctx->ws.gemv_counters = reinterpret_cast<uint32_t *>(reinterpret_cast<uint8_t *>(ctx->ws.dq_counter) + 512);
+        } else if (p) {
+            (void)hipFree(p);
         }
     }
     if (e != hipSuccess) {
@@ -371,7 +371,7 @@ const char *gemm_kernel_name(GemmKernel k)
     case GemmKernel::Portable: return "portable-tile64x64x16";
     case GemmKernel::Skinny: return "mfma-i8-rows16-splitk";
     case GemmKernel::SkinnyDirect: return "mfma-i8-rows16-direct";
-    case GemmKernel::Stream: return "mfma-i8-rows16-stream";
+    case GemmKernel::RowTiles: return "mfma-i8-rows16-tiles";
     default: return "mfma-i8-tile128x128x64";
     }
 }
@@ -422,7 +422,8 @@ int og_int8_gemm_kernel_name(const og_int8_gemm_params *p, uint32_t batch, char 
         const bool large = (p->Flags & OG_GEMM_LARGE_TILE) || og::tiled_uses_large((int32_t)p->M, (int32_t)p->N, b);
         name = large ? "mfma-i8-direct256x256x64" : "mfma-i8-tile128x128x128";
     }
-    // The few-rows products stream when the operands' rows are aligned (as in og_int8_gemm, with aligned buffers).
+    // The few-rows products take the tiled kernel when the operands' rows are aligned (as in og_int8_gemm, with aligned
+    // buffers).
     if ((k == og::GemmKernel::Skinny || k == og::GemmKernel::SkinnyDirect) && !(p->Flags & OG_GEMM_NO_STREAM)) {
         og::GemmArgs g{};
         g.A = reinterpret_cast<const uint8_t *>((uintptr_t)p->OffA);
@@ -436,7 +437,7 @@ int og_int8_gemm_kernel_name(const og_int8_gemm_params *p, uint32_t batch, char 
         g.strideA = p->StrideA;
         g.strideB = p->StrideB;
         g.flags = p->Flags;
-        if (og::gemv_stream_ok(g)) name = og::gemm_kernel_name(og::GemmKernel::Stream);
+        if (og::gemv_tiles_ok(g)) name = og::gemm_kernel_name(og::GemmKernel::RowTiles);
     }
     snprintf(buf, len, "%s", name);
     return OG_OK;
@@ -519,8 +520,8 @@ int og_int8_gemm(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_b
     (void)hipSetDevice(ctx->device);
     og::GemmKernel k = og::choose_gemm_kernel(g.M, g.N, g.K, g.batch, g.flags);
     if ((k == og::GemmKernel::Skinny || k == og::GemmKernel::SkinnyDirect) && !(g.flags & OG_GEMM_NO_STREAM) &&
-        og::gemv_stream_ok(g))
-        k = og::GemmKernel::Stream;
+        og::gemv_tiles_ok(g))
+        k = og::GemmKernel::RowTiles;
     switch (k) {
     case og::GemmKernel::Portable:
         st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_portable(g, ctx->stream, n); });
@@ -528,13 +529,16 @@ int og_int8_gemm(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_b
     case og::GemmKernel::Tiled:
         st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_tiled(g, ctx->stream, n); });
         break;
-    case og::GemmKernel::Stream: {
-        const int32_t cus = (int32_t)ctx->compute_units;
-        st = ensure_partials(ctx, og::gemv_stream_workspace_bytes(g, cus));
+    case og::GemmKernel::RowTiles:
+        st = ensure_partials(ctx, og::gemv_tiles_workspace_bytes(g));
         if (st != OG_OK) return st;
-        st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemv_stream(g, ctx->ws, cus, ctx->stream, n); });
+        st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemv_tiles(g, ctx->ws, ctx->stream, n, 0); });
+        if (st == OG_OK) {
+            const char *product = ctx->last_kernel;   // the product is named for its tile kernel, not the summing pass
+            st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemv_tiles(g, ctx->ws, ctx->stream, n, 1); });
+            ctx->last_kernel = product;
+        }
         break;
-    }
     case og::GemmKernel::SkinnyDirect:
         st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_skinny(g, ctx->ws, ctx->stream, n, 0); });
         break;
@@ -542,8 +546,11 @@ int og_int8_gemm(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_b
         st = ensure_partials(ctx, og::skinny_workspace_bytes(g.M, g.N, g.K, g.batch));
         if (st != OG_OK) return st;
         st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_skinny(g, ctx->ws, ctx->stream, n, 0); });
-        if (st == OG_OK)
+        if (st == OG_OK) {
+            const char *product = ctx->last_kernel;   // named for the split-k kernel, not the reduction pass
             st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_skinny(g, ctx->ws, ctx->stream, n, 1); });
+            ctx->last_kernel = product;
+        }
         break;
     }
     return st == OG_OK ? ok(ctx) : st;

@@ -37,14 +37,13 @@ struct Workspace {
     float *dq_ranges;        // 2 * kDqMaxGroups floats
     uint32_t *dq_counter;    // one done-counter, reset by the last workgroup
     float *dq_result;        // scale, zero point (as float) of the last dynamic quantization
-    uint32_t *gemv_counters; // kGemvMaxSlabs done-counters of the streamed few-rows kernel, each reset by its last user
 };
 
 constexpr int kDqMaxGroups = 1024;
-constexpr int kGemvMaxSlabs = 65536;
+
 
 // Kernel choice for a product, as og_int8_gemm_kernel_name reports it.
-enum class GemmKernel { Portable, Tiled, Skinny, SkinnyDirect, Stream };
+enum class GemmKernel { Portable, Tiled, Skinny, SkinnyDirect, RowTiles };
 GemmKernel choose_gemm_kernel(int32_t M, int32_t N, int32_t K, int32_t batch, uint32_t flags);
 const char *gemm_kernel_name(GemmKernel k);
 
@@ -63,10 +62,11 @@ bool tiled_uses_large(int32_t M, int32_t N, int32_t batch);
 hipError_t launch_gemm_skinny(const GemmArgs &g, const Workspace &ws, hipStream_t s, const char **kernel, int step);
 int skinny_slices(int32_t M, int32_t N, int32_t K, int32_t batch);
 uint64_t skinny_workspace_bytes(int32_t M, int32_t N, int32_t K, int32_t batch);
-// Few rows (M <= 16), B stored K x N, streamed with one workgroup per CU (`cus` of them); parts in ws.partials.
-bool gemv_stream_ok(const GemmArgs &g);
-uint64_t gemv_stream_workspace_bytes(const GemmArgs &g, int32_t cus);
-hipError_t launch_gemv_stream(const GemmArgs &g, const Workspace &ws, int32_t cus, hipStream_t s, const char **kernel);
+// Few rows (M <= 16), B stored K x N, one workgroup per 256 x 256 tile of B writing its part into ws.partials (step 0),
+// then a pass that adds the parts, corrects for the zero points and applies the epilogue (step 1).
+bool gemv_tiles_ok(const GemmArgs &g);
+uint64_t gemv_tiles_workspace_bytes(const GemmArgs &g);
+hipError_t launch_gemv_tiles(const GemmArgs &g, const Workspace &ws, hipStream_t s, const char **kernel, int step);
 
 struct EpilogueArgs {
     const int32_t *acc;

@@ -166,7 +166,7 @@ struct Int8GemmOptions {
     bool AllowPackedDot = true;  // false forces the portable kernel (Int8Gemm.cs:9-13)
     // Test hook (Int8Gemm.cs:15-16): 0 chooses by size; any other value keeps the few-rows kernel off so every shape
     // runs on the tiled MFMA kernel (64), or keeps the few-rows kernel but always splits k (32: the split-k kernel and
-    // its reduction pass, not the streamed one). 256 is this library's own: every shape on the 256 x 256 tile kernels,
+    // its reduction pass, not the tiled one). 256 is this library's own: every shape on the 256 x 256 tile kernels,
     // which otherwise only large products reach.
     int Tile = 0;
 };

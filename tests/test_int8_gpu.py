@@ -274,29 +274,38 @@ def test_scratch_semantics():
     assert ex.value.Argument == "scratch"
 
 
-def test_streamed_rows_are_bit_exact():
-    # The few-rows products (M <= 16, B stored K x N) on the streamed kernel, which splits K over the CUs and finishes
-    # each column slab in whichever workgroup comes last: one slab or many, one part per slab or several, K past the
-    # last full 64 rows, batches, every signedness and zero-point form; one case three times in a row (the per-slab
-    # counters reset themselves). Aligned operands, so that the streamed kernel is the one chosen.
+@pytest.mark.parametrize("config", ["tiles", "split k"])
+def test_few_rows_kernels_are_bit_exact(config):
+    # The few-rows products (M <= 16, B stored K x N) on the tiled kernel (one workgroup per 256 x 256 tile writing
+    # its part, then a pass adding a slab's parts) and on the split-k one (partial sums per k-slice, then their sum):
+    # one slab or many, one tile per slab or several, K past the last full tile or 64 rows, N past the last full slab,
+    # M = 16 (no spare MFMA row), batches, every signedness and zero-point form; one case three times in a row and a
+    # smaller M after a larger one. Aligned operands; the tiled kernel takes K and N multiples of 16, the split-k one
+    # the rest.
     d = device()
-    gemm = og.Int8Gemm(d)
+    gemm = og.Int8Gemm(d) if config == "tiles" else og.Int8Gemm(d, og.Int8GemmOptions(Tile=32))
     shapes = [(1, 16, 4, 1), (1, 256, 64, 1), (4, 272, 100, 1), (16, 1024, 4096, 1), (7, 528, 1500, 1),
-              (16, 4096, 64, 1), (2, 4096, 8192, 1), (3, 512, 320, 3), (1, 11008, 4096, 1), (5, 48, 12, 2)]
+              (16, 4096, 64, 1), (2, 4096, 8192, 1), (3, 512, 320, 3), (1, 11008, 4096, 1), (5, 48, 12, 2),
+              (16, 272, 4112, 2), (1, 32768, 512, 1), (15, 1040, 272, 1), (2, 1040, 272, 1)]
     bad_total = 0
     for i, (m, n, k, batch) in enumerate(shapes):
         a_s, b_s = (i & 1) != 0, (i & 2) == 0
         za_mode, zb_mode = i % 3, (i // 3) % 3
-        c = cases.Case(f"stream {m}x{n}x{k} b{batch}", cases.problem(m, n, k, batch=batch), a_s, b_s, za_mode, zb_mode)
-        for rep in range(3 if i == 2 else 1):
-            say(f"stream case {c.name} signed {a_s}/{b_s} zp {za_mode}/{zb_mode} rep {rep}")
+        c = cases.Case(f"rows {m}x{n}x{k} b{batch}", cases.problem(m, n, k, batch=batch), a_s, b_s, za_mode, zb_mode)
+        tiled = config == "tiles" and k % 16 == 0 and n % 16 == 0
+        for rep in range(3 if i == 2 or i == 8 else 1):
+            say(f"{config} case {c.name} signed {a_s}/{b_s} zp {za_mode}/{zb_mode} rep {rep}")
             bad, kernel = run_int32(d, gemm, c, 100 + i)
-            assert kernel == "mfma-i8-rows16-stream", kernel
+            if tiled:
+                assert kernel == "mfma-i8-rows16-tiles", kernel
+            else:
+                assert kernel in ("mfma-i8-rows16-splitk", "mfma-i8-rows16-direct"), kernel
             bad_total += bad
     for vec in (False, True):
-        say(f"stream float vec {vec}")
+        say(f"{config} float vec {vec}")
         bad_total += _float_case(d, gemm, 4, 256, 128, vec, True, True, 77 + vec)
-    say(f"ROW int8 gemm | streamed rows | mismatches {bad_total}")
+        bad_total += _float_case(d, gemm, 16, 1024, 512, vec, False, True, 79 + vec)
+    say(f"ROW int8 gemm | few rows [{config}] | mismatches {bad_total}")
     assert bad_total == 0
 
 
