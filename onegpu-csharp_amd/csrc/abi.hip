@@ -416,29 +416,32 @@ int og_int8_gemm_kernel_name(const og_int8_gemm_params *p, uint32_t batch, char 
     const int32_t b = (int32_t)(batch ? batch : 1);
     og::GemmKernel k = og::choose_gemm_kernel((int32_t)p->M, (int32_t)p->N, (int32_t)p->K, b, p->Flags);
     const char *name = og::gemm_kernel_name(k);
-    // The tiled family's name also says the tile, for operands at 16-byte aligned offsets and row lengths (buffers
-    // from og_alloc are); other alignments take the register-staged or the generic kernel.
+    // The operands as og_int8_gemm would see them, with the offsets standing in for the addresses (buffers from
+    // og_alloc are aligned), so that the alignment conditions of the kernels decide as they would.
+    og::GemmArgs g{};
+    g.A = reinterpret_cast<const uint8_t *>((uintptr_t)p->OffA);
+    g.B = reinterpret_cast<const uint8_t *>((uintptr_t)p->OffB);
+    g.M = (int32_t)p->M;
+    g.N = (int32_t)p->N;
+    g.K = (int32_t)p->K;
+    g.batch = b;
+    g.lda = (int32_t)(p->Lda ? p->Lda : (p->K ? p->K : 1));
+    const uint32_t cols_b = (p->Flags & OG_GEMM_TRANSPOSE_B) ? p->K : p->N;
+    g.ldb = (int32_t)(p->Ldb ? p->Ldb : (cols_b ? cols_b : 1));
+    g.strideA = p->StrideA;
+    g.strideB = p->StrideB;
+    g.flags = p->Flags;
+    // The tiled family's name also says the kernel and tile (the same choice as launch_gemm_tiled).
     if (k == og::GemmKernel::Tiled) {
-        const bool large = (p->Flags & OG_GEMM_LARGE_TILE) || og::tiled_uses_large((int32_t)p->M, (int32_t)p->N, b);
-        name = large ? "mfma-i8-direct256x256x64" : "mfma-i8-tile128x128x128";
+        const bool large = (p->Flags & OG_GEMM_LARGE_TILE) || og::tiled_uses_large(g.M, g.N, b);
+        if (!og::tiled_fast_ok(g)) name = "mfma-i8-generic128x128x64";
+        else if (og::direct_ok(g)) name = large ? "mfma-i8-direct256x256x64" : "mfma-i8-direct128x128x64";
+        else name = large ? "mfma-i8-tile256x256x64" : "mfma-i8-tile128x128x128";
     }
-    // The few-rows products take the tiled kernel when the operands' rows are aligned (as in og_int8_gemm, with aligned
-    // buffers).
-    if ((k == og::GemmKernel::Skinny || k == og::GemmKernel::SkinnyDirect) && !(p->Flags & OG_GEMM_NO_STREAM)) {
-        og::GemmArgs g{};
-        g.A = reinterpret_cast<const uint8_t *>((uintptr_t)p->OffA);
-        g.B = reinterpret_cast<const uint8_t *>((uintptr_t)p->OffB);
-        g.M = (int32_t)p->M;
-        g.N = (int32_t)p->N;
-        g.K = (int32_t)p->K;
-        g.batch = b;
-        g.lda = (int32_t)(p->Lda ? p->Lda : (p->K ? p->K : 1));
-        g.ldb = (int32_t)(p->Ldb ? p->Ldb : (p->N ? p->N : 1));
-        g.strideA = p->StrideA;
-        g.strideB = p->StrideB;
-        g.flags = p->Flags;
-        if (og::gemv_tiles_ok(g)) name = og::gemm_kernel_name(og::GemmKernel::RowTiles);
-    }
+    // The few-rows products take the tiled kernel when the operands' rows are aligned.
+    if ((k == og::GemmKernel::Skinny || k == og::GemmKernel::SkinnyDirect) && !(p->Flags & OG_GEMM_NO_STREAM) &&
+        og::gemv_tiles_ok(g))
+        name = og::gemm_kernel_name(og::GemmKernel::RowTiles);
     snprintf(buf, len, "%s", name);
     return OG_OK;
 }

@@ -478,7 +478,7 @@ hipError_t launch_gemm_tiled(const GemmArgs &g, hipStream_t s, const char **kern
     if (!tiled_fast_ok(g)) return launch_gemm_generic(g, s, kernel);
     const bool trans_b = g.flags & OG_GEMM_TRANSPOSE_B;
     const bool large = (g.flags & OG_GEMM_LARGE_TILE) || tiled_uses_large(g.M, g.N, g.batch);
-    if (large && direct_ok(g)) return launch_gemm_direct(g, s, kernel);
+    if (direct_ok(g)) return launch_gemm_direct(g, s, kernel, large);
     if (large) {
         *kernel = "mfma-i8-tile256x256x64";
         return trans_b ? launch_tiled_cfg<256, 256, 64, 2, 2, true>(g, s) : launch_tiled_cfg<256, 256, 64, 2, 2, false>(g, s);

@@ -1,5 +1,6 @@
-// The large-product kernel for B stored K x N, and the dispatch of both layouts (the kernel itself and its launch
-// templates are in int8_gemm_direct.hpp; B stored N x K is instantiated in int8_gemm_direct_nk.hip).
+// The 256 x 256 direct kernel for B stored K x N, and the dispatch of both tile sizes and layouts (the kernel itself
+// and its launch templates are in int8_gemm_direct.hpp; the other instances are in int8_gemm_direct_nk.hip and
+// int8_gemm_direct128.hip).
 #include "int8_gemm_direct.hpp"
 
 namespace og {
@@ -18,15 +19,17 @@ bool direct_ok(const GemmArgs &g)
     return true;
 }
 
-hipError_t launch_gemm_direct(const GemmArgs &g, hipStream_t s, const char **kernel)
+hipError_t launch_gemm_direct(const GemmArgs &g, hipStream_t s, const char **kernel, bool large)
 {
-    const int32_t tn = (g.N + DBN - 1) / DBN, tm = (g.M + DBM - 1) / DBM;
+    const int32_t bt = large ? 256 : 128;
+    const int32_t tn = (g.N + bt - 1) / bt, tm = (g.M + bt - 1) / bt;
     const int64_t blocks = (int64_t)tn * tm * g.batch;
-    *kernel = "mfma-i8-direct256x256x64";
+    *kernel = large ? "mfma-i8-direct256x256x64" : "mfma-i8-direct128x128x64";
     if (blocks <= 0) return hipSuccess;
     const dim3 grid((uint32_t)blocks);
-    if (g.flags & OG_GEMM_TRANSPOSE_B) launch_direct_nk(g, s, grid, tn, tm);
-    else launch_direct_t<false>(g, s, grid, tn, tm);
+    if (!large) launch_direct128(g, s, grid, tn, tm);
+    else if (g.flags & OG_GEMM_TRANSPOSE_B) launch_direct_nk256(g, s, grid, tn, tm);
+    else launch_direct_t<256, false>(g, s, grid, tn, tm);
     return hipGetLastError();
 }
 

@@ -2,9 +2,10 @@
 // no staging registers), and B stored K x N is read in its own layout with the gfx950 transpose read
 // ds_read_b64_tr_b8, so no VALU transposition is needed.
 //
-//  - Tile 256 x 256 per workgroup, 64 deep per stage, 4 waves (2 x 2) of 128 x 128, each 4 x 4 blocks of
-//    v_mfma_i32_32x32x32_i8, a ring of 5 stages filling the 160 KB of LDS. K must be a multiple of 64 (other products
-//    take the register-staged kernel).
+//  - Tile 256 x 256 per workgroup (large products) or 128 x 128 (medium ones), 64 deep per stage, 4 waves (2 x 2) of
+//    128 x 128 (4 x 4 blocks of v_mfma_i32_32x32x32_i8) or 64 x 64 (2 x 2 blocks), a ring of 5 stages filling the
+//    160 KB of LDS (half of it at 128, two workgroups a CU). K must be a multiple of 64 (other products take the
+//    register-staged kernel).
 //  - One wave per SIMD, so the wave's own instruction stream has to keep the matrix core busy. The 32 x 32 x 32 MFMA
 //    (32 cycles) does the work of two 16 x 16 x 64 ones with the same fragment reads, and leaves room for about
 //    seven other instructions: the DMA of a later stage (2 instructions a load), the fragment reads, one flip per
@@ -38,14 +39,19 @@ typedef uint32_t u4w __attribute__((ext_vector_type(4)));
 
 namespace {
 
-constexpr int DBM = 256, DBN = 256, DBK = 64, DTHREADS = 256;
-constexpr int A_STAGE = DBM * DBK;   // bytes
-constexpr int B_STAGE = DBK * DBN;
-constexpr int STAGE = A_STAGE + B_STAGE;
+constexpr int DBK = 64, DTHREADS = 256;
 constexpr int NS = 5;                                   // stages in the ring
-constexpr int LOADS_A = A_STAGE / 16 / DTHREADS;        // 16-byte loads per thread per stage
-constexpr int LOADS_B = B_STAGE / 16 / DTHREADS;
-constexpr int LOADS = LOADS_A + LOADS_B;
+
+// The shape of a BT x BT tile (BT = 256 or 128): 2 x 2 waves of WT x WT, each F x F blocks of 32 x 32; a stage of 64
+// k in NB blocks of 2 row blocks x F column blocks (HB blocks per 32-deep half).
+template <int BT>
+struct DCfg {
+    static constexpr int A_STAGE = BT * DBK, B_STAGE = DBK * BT, STAGE = A_STAGE + B_STAGE;   // bytes
+    static constexpr int LOADS_A = A_STAGE / 16 / DTHREADS, LOADS_B = B_STAGE / 16 / DTHREADS;   // 16-byte loads a thread
+    static constexpr int LOADS = LOADS_A + LOADS_B;
+    static constexpr int WT = BT / 2, F = WT / 32, HB = F / 2, NB = 2 * HB, BPB = F / HB;
+    static_assert(BT == 256 || BT == 128, "tile");
+};
 
 // Buffer resource words for `bytes` bytes at `base` (raw buffer: no stride, no swizzle; reads past the range
 // return zero).
@@ -73,7 +79,12 @@ __device__ __forceinline__ void dma16(u4w rsrc, uint32_t base, uint32_t voff)
 }
 
 __device__ __forceinline__ int a_pos(int r, int q) { return q ^ ((r >> 1) & 3); }
-__device__ __forceinline__ int b_pos(int k, int c) { return c ^ ((k & 7) | (((k >> 4) & 1) << 3)); }
+template <int BT>
+__device__ __forceinline__ int b_pos(int k, int c)
+{
+    if constexpr (BT == 256) return c ^ ((k & 7) | (((k >> 4) & 1) << 3));
+    else return c ^ (k & 7);
+}
 
 // Waits until at most N of this wave's DMA loads are outstanding, then meets the other waves. A compiler barrier as
 // well: no LDS access moves across it.
@@ -131,15 +142,16 @@ __device__ __forceinline__ void static_for(F &&f)
     }
 }
 
-// Scheduling pattern of one block of 8 MFMAs: its DS reads first, then each MFMA followed by its share of the VALU
-// work (the byte sums VS over the first six, the flips VF, which wait for a read, over the last two).
-template <int VS, int VF, int DS>
+// Scheduling pattern of one block of NM MFMAs: its DS reads first, then each MFMA followed by its share of the VALU
+// work (the byte sums VS over the first NM - 2, the flips VF, which wait for a read, over the last two).
+template <int NM, int VS, int VF, int DS>
 __device__ __forceinline__ void sched_block()
 {
+    constexpr int NS1 = NM - 2;
     __builtin_amdgcn_sched_group_barrier(0x100, DS, 0);
-    static_for<0, 8>([](auto m_tag) {
+    static_for<0, NM>([](auto m_tag) {
         constexpr int m = decltype(m_tag)::value;
-        constexpr int v = m < 6 ? (VS * (m + 1) / 6 - VS * m / 6) : (VF * (m - 5) / 2 - VF * (m - 6) / 2);
+        constexpr int v = m < NS1 ? (VS * (m + 1) / NS1 - VS * m / NS1) : (VF * (m - NS1 + 1) / 2 - VF * (m - NS1) / 2);
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x002, v, 0);
     });
@@ -149,11 +161,14 @@ __device__ __forceinline__ void sched_block()
 
 // FLIP_A / FLIP_B: the operand is unsigned (moved to the signed domain fragment by fragment). SUM_A / SUM_B: the row
 // sums of A / column sums of B are needed (the other operand's zero point in the signed domain can be non-zero).
-template <bool TRANS_B, bool SUM_A, bool SUM_B, bool FLIP_A, bool FLIP_B>
+template <int BT, bool TRANS_B, bool SUM_A, bool SUM_B, bool FLIP_A, bool FLIP_B>
 __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t tiles_n, int32_t tiles_m)
 {
-    // The whole LDS (160 KB): the ring of NS stages, A (256 x 64) then B (64 x 256) each. After the loop its start
-    // holds the epilogue's per-row and per-column arrays.
+    using D = DCfg<BT>;
+    constexpr int DBM = BT, DBN = BT, A_STAGE = D::A_STAGE, STAGE = D::STAGE, LOADS_A = D::LOADS_A;
+    constexpr int LOADS_B = D::LOADS_B, LOADS = D::LOADS, WT = D::WT, F = D::F, HB = D::HB, NB = D::NB, BPB = D::BPB;
+    // The ring of NS stages, A (BT x 64) then B (64 x BT) each: all 160 KB of LDS at BT = 256, half at 128 (two
+    // workgroups a CU). After the loop its start holds the epilogue's per-row and per-column arrays.
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -184,7 +199,7 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
     constexpr bool a_signed = !FLIP_A, b_signed = !FLIP_B;
 
     // The epilogue's per-row and per-column parameters, fetched now so that their latency hides behind the loop:
-    // thread t holds row m0 + t's zero point and column n0 + t's zero point, int bias, scale and float bias.
+    // thread t < BT holds row m0 + t's zero point and column n0 + t's zero point, int bias, scale and float bias.
     const uint32_t epi = g.epi;
     const int32_t my_m = min(m0 + tid, g.M - 1), my_n = min(n0 + tid, g.N - 1);
     // Raw zero-point bytes (0 when absent); moved to the signed domain after the loop, so nothing waits for them here.
@@ -226,8 +241,8 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
             const int r = s >> 2, p = s & 3;
             off_b[i] = (uint32_t)r * (uint32_t)ldb + 16u * (uint32_t)a_pos(r, p);
         } else {
-            const int k = s >> 4, p = s & 15;
-            off_b[i] = (uint32_t)k * (uint32_t)ldb + 16u * (uint32_t)b_pos(k, p);
+            const int k = s / (DBN / 16), p = s % (DBN / 16);
+            off_b[i] = (uint32_t)k * (uint32_t)ldb + 16u * (uint32_t)b_pos<BT>(k, p);
         }
     }
     const uint32_t wave_lds = lds_addr(smem) + (uint32_t)wave * 1024u;
@@ -250,46 +265,46 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
     // Fragments as stored (unsigned operands not yet flipped) from ring buffer u. A: row block i (32 rows) at k half
     // ks; lane l holds row 32 i + l % 32, k 32 ks + 16 (l / 32) .. + 15: one ds_read_b128.
     auto read_a = [&](int u, int i, int ks) {
-        const int r = wm * 128 + 32 * i + i32;
+        const int r = wm * WT + 32 * i + i32;
         return *reinterpret_cast<const v4i *>(smem + u * STAGE + r * 64 + 16 * a_pos(r, 2 * ks + h2));
     };
     // B: column block j (32 columns) at k half ks; lane l holds column 32 j + l % 32 and the same 16 k as A.
     auto read_b = [&](int u, int j, int ks) -> v4i {
         const uint8_t *bs = smem + u * STAGE + A_STAGE;
         if constexpr (TRANS_B) {
-            const int r = wn * 128 + 32 * j + i32;
+            const int r = wn * WT + 32 * j + i32;
             return *reinterpret_cast<const v4i *>(bs + r * 64 + 16 * a_pos(r, 2 * ks + h2));
         } else {
             // Each 16-lane group g transposes 16 columns (16 (g & 1) .. + 15 of the block) x 8 rows per read; groups
             // 2 and 3 take the second 16 k.
-            const int c = (wn * 128 + 32 * j + 16 * (g4 & 1)) >> 4;   // 16-byte chunk of the group's columns
+            const int c = (wn * WT + 32 * j + 16 * (g4 & 1)) >> 4;   // 16-byte chunk of the group's columns
             v2i h[2];
 #pragma unroll
             for (int hh = 0; hh < 2; hh++) {
                 const int k = 32 * ks + 16 * (g4 >> 1) + 8 * hh + (i16 >> 1);
-                h[hh] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(OG_LDS2(bs + k * DBN + 16 * b_pos(k, c) + 8 * (i16 & 1)));
+                h[hh] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(OG_LDS2(bs + k * DBN + 16 * b_pos<BT>(k, c) + 8 * (i16 & 1)));
             }
             return (v4i){h[0].x, h[0].y, h[1].x, h[1].y};
         }
     };
 
-    v16i acc[4][4];
+    v16i acc[F][F];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < F; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++)
+        for (int j = 0; j < F; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
     // This lane's biased byte sums (its k half, 16 bytes per fragment) of the wave's A row blocks / B column blocks.
     // Biased bytes: an unsigned operand's bytes as stored, a signed one's with the top bit flipped.
-    uint32_t rs[4], cs[4];
+    uint32_t rs[F], cs[F];
 #pragma unroll
-    for (int i = 0; i < 4; i++) { rs[i] = 0; cs[i] = 0; }
-    // VALU instructions per block beside the MFMAs: byte sums of two A and two B fragments, and the flips of the two
-    // A and two B fragments read in the block.
-    constexpr int VS = (SUM_A ? (FLIP_A ? 8 : 16) : 0) + (SUM_B ? 16 : 0);
-    constexpr int VF = (FLIP_A ? 8 : 0) + (FLIP_B ? 8 : 0);
-    constexpr int DS = 2 + (TRANS_B ? 2 : 4);
+    for (int i = 0; i < F; i++) { rs[i] = 0; cs[i] = 0; }
+    // VALU instructions per block beside the MFMAs: byte sums of two A and BPB B fragments, and the flips of the two
+    // A and BPB B fragments read in the block.
+    constexpr int VS = (SUM_A ? (FLIP_A ? 8 : 16) : 0) + (SUM_B ? 8 * BPB : 0);
+    constexpr int VF = (FLIP_A ? 8 : 0) + (FLIP_B ? 4 * BPB : 0);
+    constexpr int DS = 2 + BPB * (TRANS_B ? 1 : 2);
 
     const int32_t nk = K / DBK;   // K is a multiple of DBK here
 
@@ -300,42 +315,44 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
     });
     wait_vm_barrier<LOADS * (NS - 2)>();
     // B fragments in the signed domain, [k half][column block]; the current block's A fragments as stored and signed.
-    v4i bf[2][4], a_st[2], a_cur[2];
+    v4i bf[2][F], a_st[2], a_cur[2];
 #pragma unroll
-    for (int j = 0; j < 4; j++) bf[0][j] = to_signed<FLIP_B>(read_b(0, j, 0));
+    for (int j = 0; j < F; j++) bf[0][j] = to_signed<FLIP_B>(read_b(0, j, 0));
 #pragma unroll
     for (int t = 0; t < 2; t++) {
         a_st[t] = read_a(0, t, 0);
         a_cur[t] = to_signed<FLIP_A>(a_st[t]);
     }
 
-    // One stage s in ring buffer U, in 4 blocks of 8 MFMAs: block b multiplies A row blocks 2 (b & 1), + 1 at k half
-    // b / 2 against the 4 B column blocks. Block b reads the A fragments of block b + 1 (block 3: the first of stage
-    // s + 1) and two B fragments: blocks 0, 1 this stage's second k half, blocks 2, 3 the next stage's first (whose
-    // registers are free once block 1 is done). At block 2 the waves wait for stage s + 1 (this wave's loads landed,
-    // then everyone's) and meet: from then on nobody reads the buffer of stage s - 1, so blocks 2 and 3 each issue
-    // four loads of stage s + NS - 1 into it. Stages past the last still wait and read (their loads cover empty or
-    // unused ranges and what is read is not used), so every stage is the same.
+    // One stage s in ring buffer U, in NB blocks of 2F MFMAs: block b multiplies A row blocks 2 (b % HB), + 1 at k
+    // half b / HB against the F B column blocks. Block b reads the A fragments of block b + 1 (the last block: the
+    // first of stage s + 1) and BPB B fragments: the first half's blocks this stage's second k half, the second half's
+    // the next stage's first (whose registers are free once the first half is done). At the first block of the second
+    // half the waves wait for stage s + 1 (this wave's loads landed, then everyone's) and meet: from then on nobody
+    // reads the buffer of stage s - 1, so the second half's blocks issue the loads of stage s + NS - 1 into it. Stages
+    // past the last still wait and read (their loads cover empty or unused ranges and what is read is not used), so
+    // every stage is the same.
     auto run_stage = [&](auto u_tag, int32_t s) {
         constexpr int U = decltype(u_tag)::value, DU = (U + NS - 1) % NS, NU = (U + 1) % NS;
         const StageRsrc rr = stage_rsrc((s + NS - 1) * DBK);
-        static_for<0, 4>([&](auto b_tag) {
-            constexpr int b = decltype(b_tag)::value, ks = b >> 1, i0 = 2 * (b & 1);
-            constexpr int rks = b < 2 ? 1 : 0, rj = 2 * (b & 1), RU = b < 2 ? U : NU;
-            constexpr int nb = (b + 1) & 3, AU = b < 3 ? U : NU;
-            if constexpr (b == 2) {
+        static_for<0, NB>([&](auto b_tag) {
+            constexpr int b = decltype(b_tag)::value, ks = b / HB, i0 = 2 * (b % HB);
+            constexpr int rks = b < HB ? 1 : 0, rj = BPB * (b % HB), RU = b < HB ? U : NU;
+            constexpr int nb = (b + 1) % NB, AU = b < NB - 1 ? U : NU;
+            constexpr int LPB = LOADS / HB;   // loads per second-half block
+            if constexpr (b == HB) {
                 wait_vm_lgkm_barrier<LOADS * (NS - 3)>();   // stages s + 2 .. s + NS - 2 may still be in flight
                 __builtin_amdgcn_sched_barrier(0);
             }
-            if constexpr (b >= 2) {
-                static_for<0, 4>([&](auto q_tag) {
-                    dma(std::integral_constant<int, DU>{}, std::integral_constant<int, 4 * (b - 2) + decltype(q_tag)::value>{}, rr);
+            if constexpr (b >= HB) {
+                static_for<0, LPB>([&](auto q_tag) {
+                    dma(std::integral_constant<int, DU>{}, std::integral_constant<int, LPB * (b - HB) + decltype(q_tag)::value>{}, rr);
                 });
             }
             const v4i b0 = read_b(RU, rj, rks), b1 = read_b(RU, rj + 1, rks);
             v4i a_nx[2];
-            a_nx[0] = read_a(AU, 2 * (nb & 1), nb >> 1);
-            a_nx[1] = read_a(AU, 2 * (nb & 1) + 1, nb >> 1);
+            a_nx[0] = read_a(AU, 2 * (nb % HB), nb / HB);
+            a_nx[1] = read_a(AU, 2 * (nb % HB) + 1, nb / HB);
             if constexpr (SUM_A) {
 #pragma unroll
                 for (int t = 0; t < 2; t++)
@@ -348,7 +365,7 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
 #pragma unroll
             for (int t = 0; t < 2; t++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) acc[i0 + t][j] = mfma32(a_cur[t], bf[ks][j], acc[i0 + t][j]);
+                for (int j = 0; j < F; j++) acc[i0 + t][j] = mfma32(a_cur[t], bf[ks][j], acc[i0 + t][j]);
             bf[rks][rj] = to_signed<FLIP_B>(b0);
             bf[rks][rj + 1] = to_signed<FLIP_B>(b1);
 #pragma unroll
@@ -356,7 +373,7 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
                 a_st[t] = a_nx[t];
                 a_cur[t] = to_signed<FLIP_A>(a_nx[t]);
             }
-            sched_block<VS, VF, DS>();
+            sched_block<2 * F, VS, VF, DS>();
             __builtin_amdgcn_sched_barrier(0);
         });
     };
@@ -382,23 +399,25 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
     const uint32_t bias_total = 128u * (uint32_t)DBK * (uint32_t)nk;
     if (SUM_A && wn == 0) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < F; i++) {
             const uint32_t v = rs[i] + (uint32_t)__shfl_xor((int32_t)rs[i], 32);
-            if (h2 == 0) RowSum[wm * 128 + 32 * i + i32] = (int32_t)(v - bias_total);
+            if (h2 == 0) RowSum[wm * WT + 32 * i + i32] = (int32_t)(v - bias_total);
         }
     }
     if (SUM_B && wm == 0) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
+        for (int j = 0; j < F; j++) {
             const uint32_t v = cs[j] + (uint32_t)__shfl_xor((int32_t)cs[j], 32);
-            if (h2 == 0) ColSum[wn * 128 + 32 * j + i32] = (int32_t)(v - bias_total);
+            if (h2 == 0) ColSum[wn * WT + 32 * j + i32] = (int32_t)(v - bias_total);
         }
     }
-    if (SUM_B) RowZ[tid] = a_signed ? sext8(za_raw) : (int32_t)za_raw - 128;
-    if (SUM_A) ColW[tid] = b_signed ? sext8(zb_raw) : (int32_t)zb_raw - 128;
-    ColIB[tid] = my_ib;
-    ColSc[tid] = my_sc;
-    ColFb[tid] = my_fb;
+    if (tid < BT) {
+        if (SUM_B) RowZ[tid] = a_signed ? sext8(za_raw) : (int32_t)za_raw - 128;
+        if (SUM_A) ColW[tid] = b_signed ? sext8(zb_raw) : (int32_t)zb_raw - 128;
+        ColIB[tid] = my_ib;
+        ColSc[tid] = my_sc;
+        ColFb[tid] = my_fb;
+    }
     wait_lgkm_barrier();
 
     // Store. With z' = zero of A's row, w' = zero of B's column, s_m / t_n the byte sums of the row / column:
@@ -406,11 +425,11 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
     // MFMA 32 x 32 output layout: lane l holds column l % 32 and, in register r, row 8 (r / 4) + 4 (l / 32) + r % 4
     // of its block; one store writes two 128-byte row segments.
     const uint32_t Ku = (uint32_t)K;
-    uint32_t wz[4], ct[4], ib[4];
-    float sc[4], fb[4];
+    uint32_t wz[F], ct[F], ib[F];
+    float sc[F], fb[F];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int nl = wn * 128 + 32 * j + i32;
+    for (int j = 0; j < F; j++) {
+        const int nl = wn * WT + 32 * j + i32;
         wz[j] = SUM_A ? (uint32_t)ColW[nl] : 0u;
         ct[j] = SUM_B ? (uint32_t)ColSum[nl] - Ku * wz[j] : 0u;
         ib[j] = (uint32_t)ColIB[nl];
@@ -418,15 +437,15 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
         fb[j] = ColFb[nl];
     }
     int32_t *const Cb = static_cast<int32_t *>(g.C) + batch * g.strideC;   // int32 and float32 results alike
-    const int32_t ncol0 = n0 + wn * 128 + i32;
+    const int32_t ncol0 = n0 + wn * WT + i32;
     const int32_t M = g.M, N = g.N;
     auto store_all = [&](auto float_tag, bool has_fb) {
-        constexpr bool F = decltype(float_tag)::value;
+        constexpr bool FLT = decltype(float_tag)::value;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < F; i++) {
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                const int ml = wm * 128 + 32 * i + 8 * q + 4 * h2;
+                const int ml = wm * WT + 32 * i + 8 * q + 4 * h2;
                 const v4i ssv = SUM_A ? *reinterpret_cast<const v4i *>(&RowSum[ml]) : (v4i){0, 0, 0, 0};
                 const v4i zzv = SUM_B ? *reinterpret_cast<const v4i *>(&RowZ[ml]) : (v4i){0, 0, 0, 0};
 #pragma unroll
@@ -436,11 +455,11 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
                     int32_t *const row = Cb + m * N;   // batch * M * N < 2^31 (checked at the boundary)
                     const uint32_t ss = (uint32_t)ssv[r], zz = (uint32_t)zzv[r];
 #pragma unroll
-                    for (int j = 0; j < 4; j++) {
+                    for (int j = 0; j < F; j++) {
                         const int32_t n = ncol0 + 32 * j;
                         if (n >= N) continue;
                         const uint32_t v = (uint32_t)acc[i][j][4 * q + r] - wz[j] * ss - zz * ct[j] + ib[j];
-                        if constexpr (F) {
+                        if constexpr (FLT) {
                             float f = __fmul_rn((float)(int32_t)v, sc[j]);
                             if (has_fb) f = __fadd_rn(f, fb[j]);
                             row[n] = __float_as_int(f);
@@ -461,10 +480,10 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
 }
 
 // One instantiation per operand signedness and needed byte sums (an unsigned operand always needs the other's sums).
-template <bool T, bool FA, bool FB>
+template <int BT, bool T, bool FA, bool FB>
 inline void launch_direct_flips(const GemmArgs &g, hipStream_t s, dim3 grid, int32_t tn, int32_t tm, bool sa, bool sb)
 {
-#define OG_D(SA, SB) hipLaunchKernelGGL((k_gemm_direct<T, SA, SB, FA, FB>), grid, dim3(DTHREADS), 0, s, g, tn, tm)
+#define OG_D(SA, SB) hipLaunchKernelGGL((k_gemm_direct<BT, T, SA, SB, FA, FB>), grid, dim3(DTHREADS), 0, s, g, tn, tm)
     if constexpr (FA && FB) {
         OG_D(true, true);
     } else if constexpr (FA) {
@@ -482,18 +501,19 @@ inline void launch_direct_flips(const GemmArgs &g, hipStream_t s, dim3 grid, int
 #undef OG_D
 }
 
-template <bool T>
+template <int BT, bool T>
 inline void launch_direct_t(const GemmArgs &g, hipStream_t s, dim3 grid, int32_t tn, int32_t tm)
 {
     const bool fa = !(g.flags & OG_GEMM_A_INT8), fb = !(g.flags & OG_GEMM_B_INT8);
     const bool sa = (g.flags & OG_GEMM_ZB) || fb, sb = (g.flags & OG_GEMM_ZA) || fa;
-    if (fa && fb) launch_direct_flips<T, true, true>(g, s, grid, tn, tm, sa, sb);
-    else if (fa) launch_direct_flips<T, true, false>(g, s, grid, tn, tm, sa, sb);
-    else if (fb) launch_direct_flips<T, false, true>(g, s, grid, tn, tm, sa, sb);
-    else launch_direct_flips<T, false, false>(g, s, grid, tn, tm, sa, sb);
+    if (fa && fb) launch_direct_flips<BT, T, true, true>(g, s, grid, tn, tm, sa, sb);
+    else if (fa) launch_direct_flips<BT, T, true, false>(g, s, grid, tn, tm, sa, sb);
+    else if (fb) launch_direct_flips<BT, T, false, true>(g, s, grid, tn, tm, sa, sb);
+    else launch_direct_flips<BT, T, false, false>(g, s, grid, tn, tm, sa, sb);
 }
 
-// B stored N x K (instantiated in its own translation unit).
-void launch_direct_nk(const GemmArgs &g, hipStream_t s, dim3 grid, int32_t tn, int32_t tm);
+// Instantiated in translation units of their own (compiled in parallel): B stored N x K at 256, both layouts at 128.
+void launch_direct_nk256(const GemmArgs &g, hipStream_t s, dim3 grid, int32_t tn, int32_t tm);
+void launch_direct128(const GemmArgs &g, hipStream_t s, dim3 grid, int32_t tn, int32_t tm);
 
 }  // namespace og

@@ -52,8 +52,9 @@ hipError_t launch_gemm_portable(const GemmArgs &g, hipStream_t s, const char **k
 // The MFMA tiled product: the aligned kernel when tiled_fast_ok(g), else the generic one.
 hipError_t launch_gemm_tiled(const GemmArgs &g, hipStream_t s, const char **kernel);
 hipError_t launch_gemm_generic(const GemmArgs &g, hipStream_t s, const char **kernel);
-// The large-product kernel fed by LDS DMA (16-byte aligned operands); launch_gemm_tiled picks it when it applies.
-hipError_t launch_gemm_direct(const GemmArgs &g, hipStream_t s, const char **kernel);
+// The kernel fed by LDS DMA (16-byte aligned operands, K a multiple of 64), 256 x 256 tiles for large products, else
+// 128 x 128; launch_gemm_tiled picks it when it applies.
+hipError_t launch_gemm_direct(const GemmArgs &g, hipStream_t s, const char **kernel, bool large);
 bool direct_ok(const GemmArgs &g);
 bool tiled_fast_ok(const GemmArgs &g);
 bool tiled_uses_large(int32_t M, int32_t N, int32_t batch);

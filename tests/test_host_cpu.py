@@ -218,12 +218,15 @@ def test_kernel_choice_is_reported():
         return out.value.decode()
 
     assert name(M=4096, N=4096, K=4096) == "mfma-i8-direct256x256x64"
-    assert name(M=256, N=256, K=64) == "mfma-i8-tile128x128x128"
+    assert name(M=256, N=256, K=64) == "mfma-i8-direct128x128x64"
+    assert name(M=256, N=256, K=96) == "mfma-i8-tile128x128x128"          # K % 64 != 0: register-staged
+    assert name(M=256, N=256, K=64, Ldb=260) == "mfma-i8-tile128x128x128"   # rows of B 4-byte aligned only
+    assert name(M=256, N=256, K=64, Lda=72) == "mfma-i8-generic128x128x64"  # rows of A 8-byte aligned only
     assert name(M=256, N=256, K=64, Flags=0x2000) == "mfma-i8-direct256x256x64"
     assert name(M=1, N=11008, K=4096) == "mfma-i8-rows16-tiles"
     assert name(M=1, N=11008, K=4100) == "mfma-i8-rows16-splitk"          # K % 16 != 0: not tiled
     assert name(M=1, N=11008, K=4096, Flags=0x4000) == "mfma-i8-rows16-splitk"
     assert name(M=1, N=11000, K=4096) == "mfma-i8-rows16-splitk"          # N % 16 != 0: not tiled
     assert name(M=16, N=11008, K=4096).startswith("mfma-i8-rows16")
-    assert name(M=1, N=11008, K=4096, Flags=0x4).startswith("mfma-i8-tile")     # transposed B: tiled
+    assert name(M=1, N=11008, K=4096, Flags=0x4) == "mfma-i8-direct128x128x64"   # transposed B: tiled
     assert name(M=1, N=11008, K=4096, Flags=0x400) == "portable-tile64x64x16"
