@@ -152,14 +152,11 @@ int og_init(int device_ordinal, og_ctx **out)
     if (e == hipSuccess) {
         ctx->ws.partial_bytes = kInitialPartialBytes;
         void *p = nullptr;
-        // ranges (2 * kDqMaxGroups floats), counter, result (2 floats), in one allocation
-        size_t bytes = 2 * og::kDqMaxGroups * sizeof(float) + 256 + 256;
+        // the dynamic quantizer's per-workgroup ranges (2 * kDqMaxGroups floats)
+        size_t bytes = 2 * og::kDqMaxGroups * sizeof(float);
         e = hipMalloc(&p, bytes);
-        if (e == hipSuccess) e = hipMemset(p, 0, bytes);
         if (e == hipSuccess) {
             ctx->ws.dq_ranges = static_cast<float *>(p);
-            ctx->ws.dq_counter = reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(p) + 2 * og::kDqMaxGroups * sizeof(float));
-            ctx->ws.dq_result = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(ctx->ws.dq_counter) + 256);
         } else if (p) {
             (void)hipFree(p);
         }

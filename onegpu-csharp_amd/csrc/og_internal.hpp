@@ -28,15 +28,13 @@ struct GemmArgs {
     uint32_t epi;    // OG_EPI_*
 };
 
-// Device workspace owned by a context: the split-k partial sums of the few-rows kernel and the dynamic quantizer's
-// per-workgroup ranges, done-counter and result slot. Sized once at og_init; grown (outside any launch) when a larger
-// few-rows product arrives.
+// Device workspace owned by a context: the partial sums of the few-rows kernels and the dynamic quantizer's
+// per-workgroup ranges. Sized once at og_init; the partial sums grow (outside any launch) when a larger few-rows product
+// arrives.
 struct Workspace {
     int32_t *partials;       // split-k partial sums (int32)
     uint64_t partial_bytes;
-    float *dq_ranges;        // 2 * kDqMaxGroups floats
-    uint32_t *dq_counter;    // one done-counter, reset by the last workgroup
-    float *dq_result;        // scale, zero point (as float) of the last dynamic quantization
+    float *dq_ranges;        // 2 * kDqMaxGroups floats: the dynamic quantizer's per-workgroup ranges
 };
 
 constexpr int kDqMaxGroups = 1024;

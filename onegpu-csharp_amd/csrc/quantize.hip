@@ -1,7 +1,7 @@
 // The element-wise and reduction kernels around the int8 product, for gfx950:
-//  - DynamicQuantizeLinear: a min/max pass whose last workgroup to finish combines the per-workgroup ranges into the
-//    scale and zero point (one launch, no host round trip), then a quantize pass that streams x again with 16-byte
-//    loads and writes 16 output bytes per thread.
+//  - DynamicQuantizeLinear: a min/max pass writing one range per workgroup, then a quantize pass in which every
+//    workgroup combines those ranges into the scale and zero point and streams x again with 16-byte loads, writing 16
+//    output bytes per thread (no host round trip, no counters or fences: the kernel boundary orders the passes).
 //  - DequantizeLinear / QuantizeLinear and the QLinearMatMul requantization (the int8 epilogue's mode 2).
 // Division is IEEE float32 division (correctly rounded: built with -fhip-fp32-correctly-rounded-divide-sqrt and
 // denormals kept), rounding is rintf (half to even), and no multiply is contracted into an add (-ffp-contract=off),
@@ -61,15 +61,12 @@ __device__ void dq_params(float mn, float mx, float &scale, uint32_t &zp)
     }
 }
 
-__global__ __launch_bounds__(DQ_THREADS) void k_dq_minmax(const float *x, uint32_t count, float *ranges,
-                                                          uint32_t *counter, float *result, float *scale_out,
-                                                          uint8_t *zero_out)
+// Pass 1: each workgroup's range (NaN-ignoring min and max) over its grid-stride share of x.
+__global__ __launch_bounds__(DQ_THREADS) void k_dq_minmax(const float *x, uint32_t count, float *ranges)
 {
     __shared__ float smin[DQ_THREADS / 64], smax[DQ_THREADS / 64];
-    __shared__ bool last;
     float mn = __int_as_float(0x7F800000), mx = __int_as_float(0xFF800000);
-    const uint32_t groups = gridDim.x;
-    const uint32_t tid = blockIdx.x * DQ_THREADS + threadIdx.x, nthreads = groups * DQ_THREADS;
+    const uint32_t tid = blockIdx.x * DQ_THREADS + threadIdx.x, nthreads = gridDim.x * DQ_THREADS;
     if (((uintptr_t)x & 15) == 0) {
         const uint32_t n4 = count / 4;
         const f4 *x4 = reinterpret_cast<const f4 *>(x);
@@ -85,33 +82,6 @@ __global__ __launch_bounds__(DQ_THREADS) void k_dq_minmax(const float *x, uint32
     if (threadIdx.x == 0) {
         ranges[2 * blockIdx.x] = mn;
         ranges[2 * blockIdx.x + 1] = mx;
-        __threadfence();
-        uint32_t prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        last = (prev == groups - 1);
-    }
-    __syncthreads();
-    if (!last) return;
-    // The last workgroup to finish: combine every workgroup's range (order-free), derive scale and zero point.
-    __threadfence();
-    mn = __int_as_float(0x7F800000);
-    mx = __int_as_float(0xFF800000);
-    for (uint32_t g = threadIdx.x; g < groups; g += DQ_THREADS) {
-        float a = __hip_atomic_load(&ranges[2 * g], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        float b = __hip_atomic_load(&ranges[2 * g + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        mn = (a < mn) ? a : mn;
-        mx = (b > mx) ? b : mx;
-    }
-    __syncthreads();
-    block_minmax(mn, mx, smin, smax);
-    if (threadIdx.x == 0) {
-        float scale;
-        uint32_t zp;
-        dq_params(mn, mx, scale, zp);
-        result[0] = scale;
-        result[1] = (float)zp;
-        *scale_out = scale;
-        *zero_out = (uint8_t)zp;
-        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // ready for the next call
     }
 }
 
@@ -121,26 +91,52 @@ __device__ __forceinline__ uint32_t dq_one(float x, float scale, float zp)
     return is_nan_bits(v) ? 0u : (uint32_t)fminf(fmaxf(v, 0.0f), 255.0f);
 }
 
-// 16 elements per thread; 16-byte loads and one 16-byte store when both x and y are 16-byte aligned.
+// Pass 2: every workgroup combines pass 1's ranges (the kernel boundary orders them; min and max are order-free, so
+// every workgroup derives the same scale and zero point) and quantizes its grid-stride share of x, 16 elements a
+// thread with 16-byte loads and one 16-byte store when x and y are 16-byte aligned. Workgroup 0 writes the scale and
+// the zero point (one byte, its neighbours untouched).
 __global__ __launch_bounds__(DQ_THREADS) void k_dq_quantize(const float *x, uint8_t *y, uint32_t count,
-                                                            const float *result)
+                                                            const float *ranges, uint32_t groups, float *scale_out,
+                                                            uint8_t *zero_out)
 {
-    const float scale = result[0], zp = result[1];
-    const uint64_t i0 = ((uint64_t)blockIdx.x * DQ_THREADS + threadIdx.x) * 16;
-    if (i0 >= count) return;
-    if (i0 + 16 <= count && (((uintptr_t)x | (uintptr_t)y) & 15) == 0) {
-        const f4 *x4 = reinterpret_cast<const f4 *>(x + i0);
-        uint32_t w[4];
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            f4 v = __builtin_nontemporal_load(&x4[q]);
-            w[q] = dq_one(v.x, scale, zp) | (dq_one(v.y, scale, zp) << 8) | (dq_one(v.z, scale, zp) << 16) |
-                   (dq_one(v.w, scale, zp) << 24);
-        }
-        *reinterpret_cast<uint4 *>(y + i0) = make_uint4(w[0], w[1], w[2], w[3]);
-        return;
+    __shared__ float smin[DQ_THREADS / 64], smax[DQ_THREADS / 64], sparam[2];
+    float mn = __int_as_float(0x7F800000), mx = __int_as_float(0xFF800000);
+    for (uint32_t g = threadIdx.x; g < groups; g += DQ_THREADS) {
+        const float a = ranges[2 * g], b = ranges[2 * g + 1];
+        mn = (a < mn) ? a : mn;
+        mx = (b > mx) ? b : mx;
     }
-    for (uint64_t i = i0; i < i0 + 16 && i < count; i++) y[i] = (uint8_t)dq_one(x[i], scale, zp);
+    block_minmax(mn, mx, smin, smax);
+    if (threadIdx.x == 0) {
+        float sc;
+        uint32_t zp;
+        dq_params(mn, mx, sc, zp);
+        sparam[0] = sc;
+        sparam[1] = (float)zp;
+        if (blockIdx.x == 0) {
+            *scale_out = sc;
+            *zero_out = (uint8_t)zp;
+        }
+    }
+    __syncthreads();
+    const float scale = sparam[0], zp = sparam[1];
+    const bool vec = (((uintptr_t)x | (uintptr_t)y) & 15) == 0;
+    const uint64_t stride = (uint64_t)gridDim.x * DQ_THREADS * 16;
+    for (uint64_t i0 = ((uint64_t)blockIdx.x * DQ_THREADS + threadIdx.x) * 16; i0 < count; i0 += stride) {
+        if (vec && i0 + 16 <= count) {
+            const f4 *x4 = reinterpret_cast<const f4 *>(x + i0);
+            uint32_t w[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                f4 v = __builtin_nontemporal_load(&x4[q]);
+                w[q] = dq_one(v.x, scale, zp) | (dq_one(v.y, scale, zp) << 8) | (dq_one(v.z, scale, zp) << 16) |
+                       (dq_one(v.w, scale, zp) << 24);
+            }
+            *reinterpret_cast<uint4 *>(y + i0) = make_uint4(w[0], w[1], w[2], w[3]);
+        } else {
+            for (uint64_t i = i0; i < i0 + 16 && i < count; i++) y[i] = (uint8_t)dq_one(x[i], scale, zp);
+        }
+    }
 }
 
 static uint32_t dq_groups(uint32_t count)
@@ -152,15 +148,18 @@ static uint32_t dq_groups(uint32_t count)
 
 hipError_t launch_dynamic_quantize(const DqArgs &d, const Workspace &ws, hipStream_t s, const char **kernel, int step)
 {
+    const uint32_t groups = dq_groups(d.count);
     if (step == 0) {
         *kernel = "dq-minmax";
-        hipLaunchKernelGGL(k_dq_minmax, dim3(dq_groups(d.count)), dim3(DQ_THREADS), 0, s, d.x, d.count, ws.dq_ranges,
-                           ws.dq_counter, ws.dq_result, d.scale, d.zero);
+        hipLaunchKernelGGL(k_dq_minmax, dim3(groups), dim3(DQ_THREADS), 0, s, d.x, d.count, ws.dq_ranges);
     } else {
         *kernel = "dq-quantize";
-        uint64_t threads = ((uint64_t)d.count + 15) / 16;
-        hipLaunchKernelGGL(k_dq_quantize, dim3((uint32_t)((threads + DQ_THREADS - 1) / DQ_THREADS)), dim3(DQ_THREADS), 0,
-                           s, d.x, d.y, d.count, (const float *)ws.dq_result);
+        // 16 elements a thread, at most 2048 workgroups (each re-reads the ranges).
+        const uint64_t threads = ((uint64_t)d.count + 15) / 16;
+        uint64_t wgs = (threads + DQ_THREADS - 1) / DQ_THREADS;
+        wgs = wgs > 2048 ? 2048 : wgs;
+        hipLaunchKernelGGL(k_dq_quantize, dim3((uint32_t)wgs), dim3(DQ_THREADS), 0, s, d.x, d.y, d.count,
+                           (const float *)ws.dq_ranges, groups, d.scale, d.zero);
     }
     return hipGetLastError();
 }
