@@ -186,14 +186,27 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_tiles_sum(GemmArgs g, int32
     const int32_t gi = m0 / 4, groups = gemv_tile_groups(M);
     const bool cs_here = M / 4 == gi;   // the column sums (row M) share this row group
 
+    // Eight parts at a time, all their loads in flight together (parts past the last read the last one, inside the
+    // workspace, and are masked off).
     v4i v = {0, 0, 0, 0}, rs = {0, 0, 0, 0};
     uint32_t cs = 0;
-    for (int32_t p = 0; p < nkc; p++) {
-        const int32_t *part = pp + p * stride;
-        const v4i x = *reinterpret_cast<const v4i *>(part + (gi * GT_COLS + tid) * 4);
-        v += x;
-        if (SUM_A) rs += *reinterpret_cast<const v4i *>(part + groups * GT_COLS * 4 + 4 * gi);
-        if (SUM_B) cs += cs_here ? (uint32_t)x[M & 3] : (uint32_t)part[((M / 4) * GT_COLS + tid) * 4 + (M & 3)];
+    for (int32_t p0 = 0; p0 < nkc; p0 += 8) {
+        v4i x[8], r[8];
+        uint32_t c[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int32_t *part = pp + min(p0 + u, nkc - 1) * stride;
+            x[u] = *reinterpret_cast<const v4i *>(part + (gi * GT_COLS + tid) * 4);
+            r[u] = SUM_A ? *reinterpret_cast<const v4i *>(part + groups * GT_COLS * 4 + 4 * gi) : (v4i){0, 0, 0, 0};
+            c[u] = (SUM_B && !cs_here) ? (uint32_t)part[((M / 4) * GT_COLS + tid) * 4 + (M & 3)] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int32_t keep = p0 + u < nkc ? -1 : 0;
+            v += x[u] & keep;
+            rs += r[u] & keep;
+            cs += (cs_here ? (uint32_t)x[u][M & 3] : c[u]) & (uint32_t)keep;
+        }
     }
     if (n >= N) return;
     uint32_t wz = 0;
