@@ -129,16 +129,22 @@ def kernel_stats(times, name_prefix=None):
 
 # ------------------------------------------------------------------ configurations
 
-def c4_square(d, steps, warmup, check=True):
-    """Configuration 4: 4096^3, A uint8 U{0..255} with per-row a_zp U{100..156}, B int8 U{-127..127}, int32 out."""
+def c4_square(d, steps, warmup, check=True, constant=False, trans_b=False, plain=False):
+    """Configuration 4: 4096^3, A uint8 U{0..255} with per-row a_zp U{100..156}, B int8 U{-127..127}, int32 out.
+    constant=True fills A, B and the zero points with one value each instead (the same work on operands that do not
+    toggle: the matrix cores then draw less power and the chip holds a higher clock); trans_b=True reads the same bytes
+    of B as stored N x K (a different product, the same work: the layout's cost alone); plain=True reads A as int8
+    with no zero point (int8 x int8 as torch._int_mm computes it, no byte sums or flips)."""
     M = N = K = 4096
-    a = synth(d, og.ElementType.UInt8, M * K, 4, 0, 0, 255, 0)
-    za = synth(d, og.ElementType.UInt8, M, 4, 1, 100, 156, 0)
-    b = synth(d, og.ElementType.Int8, K * N, 4, 2, -127, 127, 0)
+    a = synth(d, og.ElementType.Int8 if plain else og.ElementType.UInt8, M * K, 4, 0,
+              *((0x37, 0x37) if constant else ((-128, 127) if plain else (0, 255))), 0)
+    za = synth(d, og.ElementType.UInt8, M, 4, 1, *((128, 128) if constant else (100, 156)), 0)
+    b = synth(d, og.ElementType.Int8, K * N, 4, 2, *((-13, -13) if constant else (-127, 127)), 0)
     c = d.CreateBufferOf(og.ElementType.Int32, M * N)
     gemm = og.Int8Gemm(d)
     p = og.Int8GemmProblem(M, N, K)
-    zpa = og.Int8Operand(za, 0, True)
+    p.TransposeB = trans_b
+    zpa = None if plain else og.Int8Operand(za, 0, True)
     wall, region, times = timed(d, lambda e, i: gemm.EncodeInt32(e, p, a, b, c, zpa), steps, warmup)
     pair_ms, pair_med_ms, kname = kernel_stats(times)
     res = {"ops": 2.0 * M * N * K, "wall_s": wall, "kernel_mean_ms": region / steps * 1e3,
@@ -333,6 +339,37 @@ def copy_workload(d, steps, warmup, mib=256):
     return {"bytes_read": n, "bytes_written": n, "launches": warmup + steps}
 
 
+def vendor_int8(steps, warmup):
+    """The vendor library's int8 product at 4096^3 for comparison: torch._int_mm (hipBLASLt on ROCm), int8 x int8 ->
+    int32 without zero points, B stored K x N (as configuration 4) and N x K, on random and on constant operands,
+    timed with torch's events over `steps` back-to-back launches."""
+    import torch
+    dev = torch.device("cuda", 0)
+    M = N = K = 4096
+    torch.manual_seed(4)
+    out = {}
+    for kind in ("random", "constant"):
+        if kind == "random":
+            a = torch.randint(-128, 128, (M, K), dtype=torch.int8, device=dev)
+            b = torch.randint(-128, 128, (K, N), dtype=torch.int8, device=dev)
+        else:
+            a = torch.full((M, K), 0x37, dtype=torch.int8, device=dev)
+            b = torch.full((K, N), -13, dtype=torch.int8, device=dev)
+        for layout, bb in (("B K x N", b), ("B N x K", b.t().contiguous().t())):
+            for _ in range(warmup):
+                torch._int_mm(a, bb)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                torch._int_mm(a, bb)
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) / steps * 1e3
+            out[f"{kind}, {layout}"] = {"us": us, "tops": 2.0 * M * N * K / us / 1e6}
+    return out
+
+
 def only(d, name, steps, warmup):
     """One workload alone (for rocprofv3 runs of committed files); prints a one-line summary."""
     if name == "c4":
@@ -346,9 +383,14 @@ def only(d, name, steps, warmup):
         r = c5_batched(d, steps, warmup, check=False)
     elif name == "copy":
         r = copy_workload(d, steps, warmup)
+    elif name in ("c4const", "c4nt", "c4plain", "c4plainnt"):
+        r = c4_square(d, steps, warmup, check=False, constant=name == "c4const", trans_b=name.endswith("nt"),
+                      plain=name.startswith("c4plain"))
+        r.pop("host_operands", None)
+        r["tops_kernel"] = r["ops"] / (r["kernel_mean_ms"] * 1e-3) / 1e12
     else:
         raise SystemExit(f"unknown workload {name}")
-    print(json.dumps({"workload": name, **{k: v for k, v in r.items() if isinstance(v, (int, float, str, list))}}))
+    print(json.dumps({"workload": name, **{k: v for k, v in r.items() if isinstance(v, (int, float, str, list, dict))}}))
 
 
 def main():
@@ -358,13 +400,17 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline configuration only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["c4", "gemv1", "gemv4", "gemv16", "c2", "c5", "copy"],
+    ap.add_argument("--only", choices=["c4", "c4const", "c4nt", "c4plain", "c4plainnt", "gemv1", "gemv4", "gemv16", "c2", "c5", "copy", "vendor"],
                     help="run one workload alone and print its summary (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported (see DESIGN.md for "
                                    "how the path would shard)"}))
         sys.exit(2)
+    if args.only == "vendor":
+        # torch's bundled HIP runtime must own the device in this process: no context of this library is opened.
+        print(json.dumps({"workload": "vendor", "hipblaslt_int_mm_4096": vendor_int8(args.steps, args.warmup)}))
+        return
     d = og.GpuDevice.Create(0)
     log = lambda s: print(s, file=sys.stderr, flush=True)  # noqa: E731
     if args.only:

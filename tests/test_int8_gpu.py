@@ -188,6 +188,32 @@ def test_dynamic_quantize_is_bit_exact():
     assert bad == 0
 
 
+def test_dynamic_quantize_large_inputs():
+    # Inputs past one pass of the quantize grid (2048 workgroups x 256 threads x 16 elements = 8,388,608): the
+    # grid-stride loop, aligned and unaligned x and y, a ragged tail; the minimum and maximum placed in the last
+    # elements, so the workgroup that reads them is one of the last.
+    d = device()
+    k = og.DynamicQuantizeKernels(d)
+    bad = 0
+    for count, off in ((9_000_003, 0), (8_388_608 * 2 + 5, 1)):
+        x = oracle.dq_input(count, 31 + off, 0)
+        x[-1], x[-2] = np.float32(7.5), np.float32(-6.25)
+        say(f"dq large count {count} offset {off}")
+        wy, ws, wz = oracle.dynamic_quantize(x)
+        xs = np.zeros(count + off, np.float32)
+        xs[off:] = x
+        bx, by = d.CreateBuffer(xs), d.CreateBufferOf(og.ElementType.UInt8, count + off + 4)
+        bs, bz = d.CreateBufferOf(og.ElementType.Float32, 1), d.CreateBufferOf(og.ElementType.UInt8, 4)
+        run(d, lambda e: k.Encode(e, bx, off, count, by, off, bs, 0, bz, 0))
+        y = by.Read()[off:off + count]
+        here = int(np.count_nonzero(y != wy)) + int(bs.Read()[0].view(np.uint32) != np.float32(ws).view(np.uint32))
+        here += int(bz.Read()[0] != wz)
+        if here:
+            say(f"MISMATCH dq large count {count}: {here}")
+        bad += here
+    assert bad == 0
+
+
 def test_dynamic_quantize_special_values():
     d = device()
     k = og.DynamicQuantizeKernels(d)
