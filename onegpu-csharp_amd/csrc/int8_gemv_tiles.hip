@@ -27,7 +27,8 @@ typedef int32_t v2i __attribute__((ext_vector_type(2)));
 typedef uint32_t u4w __attribute__((ext_vector_type(4)));
 
 constexpr int GT_COLS = 256, GT_THREADS = 256;
-constexpr int GT_KT = 256;                 // rows of B per tile
+constexpr int GT_KT = 256;                 // rows of B per tile (a multiple of 64, at most 256)
+constexpr int GT_AROW = 256;               // bytes of an A row in LDS (16 chunks, GT_KT / 16 of them used)
 constexpr int GT_SUB = 64;                 // rows per sub-stage (one MFMA deep)
 constexpr int GT_NSUB = GT_KT / GT_SUB;
 constexpr int GT_LPS = GT_SUB * GT_COLS / 16 / GT_THREADS;   // DMA loads per thread per sub-stage
@@ -85,7 +86,8 @@ __host__ __device__ inline int64_t gemv_tile_part(int32_t M) { return (int64_t)g
 template <bool SUM_A, bool SUM_B, bool FLIP_A, bool FLIP_B>
 __global__ __launch_bounds__(GT_THREADS) void k_gemv_tiles(GemmArgs g, int32_t slabs, int32_t nkc, int32_t *parts)
 {
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[GT_KT * GT_COLS + 16 * GT_KT];
+    static_assert(GT_KT % GT_SUB == 0 && GT_KT <= GT_AROW, "tile rows");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[GT_KT * GT_COLS + 16 * GT_AROW];
     uint8_t *const asmem = smem + GT_KT * GT_COLS;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -102,7 +104,8 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_tiles(GemmArgs g, int32_t s
     {
         const uint32_t lds = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)smem;
         // A in LDS: 16 rows of 256 bytes, chunk c of row r at position c ^ r (the 16 rows a fragment read touches
-        // spread over the banks); thread t fills slot t, row t / 16 at position t % 16.
+        // spread over the banks); thread t fills slot t, row t / 16 at position t % 16. With tiles under 256 rows the
+        // chunks past the tile are loaded too (the next k-range, or zeros past the operand) and never read.
         const int r = tid >> 4, c = (tid & 15) ^ r;
         const u4w ra = tile_rsrc(g.A + b * g.strideA + k0, (M - 1) * g.lda + min(GT_KT, K - k0));
         tile_dma16(ra, lds + GT_KT * GT_COLS + (uint32_t)wave * 1024u, (uint32_t)r * (uint32_t)g.lda + 16u * (uint32_t)c);
@@ -125,7 +128,7 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_tiles(GemmArgs g, int32_t s
         tile_wait_vm_barrier<GT_LPS * (GT_NSUB - 1 - ks)>();   // sub-stage ks landed (this wave's loads, then all)
         const bool kv = k0 + GT_SUB * ks + 16 * g4 < K;
         const bool av = kv && i16 < M;
-        v4i a = *reinterpret_cast<const v4i *>(asmem + i16 * GT_KT + 16 * ((4 * ks + g4) ^ i16));
+        v4i a = *reinterpret_cast<const v4i *>(asmem + i16 * GT_AROW + 16 * ((4 * ks + g4) ^ i16));
         if constexpr (!FLIP_A) a = av ? a : (v4i){0, 0, 0, 0};
         if constexpr (SUM_A) rsum = av ? tile_sad16(FLIP_A ? a : (a ^ (int32_t)0x80808080), rsum) : rsum;
         if constexpr (FLIP_A) a = av ? (a ^ (int32_t)0x80808080) : (v4i){0, 0, 0, 0};
