@@ -370,6 +370,46 @@ def vendor_int8(steps, warmup):
     return out
 
 
+def qlinear_c2(d, steps, warmup, fused, check=True):
+    """QLinearMatMul on configuration 2's product (1024 x 3072 x 768): u8 A with a zero point, int8 B symmetric per
+    column (N(0, 0.02)), int bias and multiplier per column, u8 output with zero point 128. `fused`: one launch, the
+    requantization in the product's store; else the reference's two passes (int32 sums into scratch, then the
+    requantize pass)."""
+    M, K, N = 1024, 768, 3072
+    a = synth(d, og.ElementType.UInt8, M * K, 2, 50, 0, 255, 0)
+    q, _ = sym_weights(d, K, N, 2, 51)
+    za = d.CreateBuffer(np.array([131, 0, 0, 0], np.uint8))
+    cols = np.arange(N)
+    multv = ((cols % 97).astype(np.float32) * np.float32(1e-6) + np.float32(2.5e-4)).astype(np.float32)
+    ibv = (((cols * 6007) % 4001) - 2000).astype(np.int32)
+    mult, ib = d.CreateBuffer(multv), d.CreateBuffer(ibv)
+    y = d.CreateBufferOf(og.ElementType.UInt8, M * N)
+    scratch = d.CreateBufferOf(og.ElementType.Int32, M * N)
+    gemm = og.Int8Gemm(d, og.Int8GemmOptions(FusedRequantize=fused))
+    p = og.Int8GemmProblem(M, N, K)
+    wall, region, times = timed(d, lambda e, i: gemm.EncodeRequantized(e, p, a, q, y, og.Int8Operand(mult, 0, True), 128,
+                                                                       og.Int8Operand(za, 0), None,
+                                                                       og.Int8Operand(ib, 0, True),
+                                                                       og.Int8Scratch(scratch)),
+                                steps, warmup)
+    per = {}
+    for t, k in times:
+        per.setdefault(k, []).append(t)
+    bytes_ = M * K + K * N + M * N + 8 * N + 1
+    res = {"ops": 2.0 * M * N * K, "wall_s": wall, "step_mean_ms": region / steps * 1e3, "bytes": bytes_,
+           "dispatch_mean_ms": {k: statistics.mean(v) for k, v in per.items()}}
+    if check:
+        import oracle
+        A, Q = a.Read(), q.Read()
+        rows = np.array([0, 7, 600, 1023])
+        sums = oracle.int8_gemm_rows(oracle.Gemm(M, N, K), A, False, Q.view(np.uint8), True, rows,
+                                     (np.array([131], np.uint8), False, 0))
+        want = oracle.requant_array(sums.ravel(), N, multv, True, 128, True, ibv).reshape(len(rows), N)
+        got = y.Read().reshape(M, N)[rows]
+        res["check"] = "bit-exact" if np.array_equal(got, want) else "MISMATCH"
+    return res
+
+
 def only(d, name, steps, warmup):
     """One workload alone (for rocprofv3 runs of committed files); prints a one-line summary."""
     if name == "c4":
@@ -381,6 +421,8 @@ def only(d, name, steps, warmup):
         r = c2_bert_ffn(d, steps, warmup, check=False)
     elif name == "c5":
         r = c5_batched(d, steps, warmup, check=False)
+    elif name in ("c2q", "c2q2"):
+        r = qlinear_c2(d, steps, warmup, fused=name == "c2q", check=False)
     elif name == "copy":
         r = copy_workload(d, steps, warmup)
     elif name in ("c4const", "c4nt", "c4plain", "c4plainnt"):
@@ -400,7 +442,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline configuration only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["c4", "c4const", "c4nt", "c4plain", "c4plainnt", "gemv1", "gemv4", "gemv16", "c2", "c5", "copy", "vendor"],
+    ap.add_argument("--only", choices=["c4", "c4const", "c4nt", "c4plain", "c4plainnt", "gemv1", "gemv4", "gemv16", "c2", "c2q", "c2q2", "c5", "copy", "vendor"],
                     help="run one workload alone and print its summary (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -446,6 +488,15 @@ def main():
                                   "dispatch_mean_us": {k: v * 1e3 for k, v in r["dispatch_mean_ms"].items()},
                                   "check": r["check"]}
         log(json.dumps(configs["c2_bert_ffn"]))
+        for fused, key in ((True, "qlinear_c2_one_launch"), (False, "qlinear_c2_two_passes")):
+            log(f"QLinearMatMul on configuration 2's product, {'one launch' if fused else 'two passes'}")
+            r = qlinear_c2(d, args.steps, args.warmup, fused)
+            configs[key] = {"step_mean_us": r["step_mean_ms"] * 1e3,
+                            "gbs": r["bytes"] / (r["step_mean_ms"] * 1e-3) / 1e9,
+                            "tops": r["ops"] / (r["step_mean_ms"] * 1e-3) / 1e12,
+                            "dispatch_mean_us": {k: v * 1e3 for k, v in r["dispatch_mean_ms"].items()},
+                            "check": r["check"]}
+            log(json.dumps(configs[key]))
         log("config 5: batched 32 x 512 x 4096 x 4096")
         r = c5_batched(d, max(3, args.steps // 5), 2)
         configs["c5_batched"] = {"tops_kernel": r["ops"] / (r["kernel_mean_ms"] * 1e-3) / 1e12,

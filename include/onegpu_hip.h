@@ -163,6 +163,17 @@ typedef struct og_int8_epilogue_params {
 int og_int8_epilogue(og_ctx *ctx, const og_int8_epilogue_params *params, og_buffer acc, og_buffer out, og_buffer bias,
                      og_buffer scale, og_buffer fbias);
 
+/* Int8Gemm.EncodeRequantized (Int8Gemm.cs:336-363) in one launch: the product of og_int8_gemm and the mode-2 pass of
+ * og_int8_epilogue, with the requantization applied where the product stores its sums, so the int32 sums never reach
+ * memory and no scratch is used. Replaces the Multiply (554-639) + Finish (649-682) pair; each output byte equals what
+ * the pair writes. params as for og_int8_gemm, except: C is Y, 8-bit, and OffC and StrideC count bytes; Epi may hold
+ * only OG_EPI_INT_BIAS and OG_EPI_SCALE_PER_COL (the multiplier is one value, or one per column, at OffScale of
+ * multiplier); zero_point_y lies in the output type's range; y_signed chooses int8 (else uint8) output. Bytes of Y
+ * outside the product are not touched. */
+int og_int8_gemm_requantized(og_ctx *ctx, const og_int8_gemm_params *params, uint32_t batch, og_buffer A, og_buffer B,
+                             og_buffer Y, og_buffer ZA, og_buffer ZB, og_buffer bias, og_buffer multiplier,
+                             int32_t zero_point_y, uint32_t y_signed);
+
 /* ------------------------------------------------------------------ DynamicQuantizeLinear */
 
 /* DqParams, 7 words (src/RecursiveAI.OneGpu.Kernels/Shaders/DynamicQuantize.hlsl:131-140). GridX and Groups are the

@@ -381,7 +381,8 @@ static const uint32_t kKnownGemmFlags =
     0x7Fu | 0x380u | OG_GEMM_PORTABLE | OG_GEMM_NO_SKINNY | OG_GEMM_NO_DIRECT | OG_GEMM_LARGE_TILE | OG_GEMM_NO_STREAM;
 
 // Checks the parameter block alone; returns OG_OK or the failing status (message and argument set).
-static int check_gemm_params(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch)
+// `requant`: the parameters of og_int8_gemm_requantized, whose Epi holds only the int bias and per-column bits.
+static int check_gemm_params(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, bool requant = false)
 {
     if (!p) return fail(ctx, OG_ERR_INVALID_ARG, "params", "null parameter block");
     const uint32_t imax = 0x7FFFFFFFu;
@@ -392,9 +393,14 @@ static int check_gemm_params(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t
     if (p->Flags & ~kKnownGemmFlags) return fail(ctx, OG_ERR_INVALID_ARG, "Flags", "unknown flag bits 0x%x", p->Flags & ~kKnownGemmFlags);
     if ((p->Flags & OG_GEMM_ZA_PER_ROW) && !(p->Flags & OG_GEMM_ZA)) return fail(ctx, OG_ERR_INVALID_ARG, "Flags", "per-row zero point without a zero point");
     if ((p->Flags & OG_GEMM_ZB_PER_COL) && !(p->Flags & OG_GEMM_ZB)) return fail(ctx, OG_ERR_INVALID_ARG, "Flags", "per-column zero point without a zero point");
-    if (p->Epi & ~0xFu) return fail(ctx, OG_ERR_INVALID_ARG, "Epi", "unknown epilogue bits 0x%x", p->Epi & ~0xFu);
-    if ((p->Epi & (OG_EPI_SCALE_PER_COL | OG_EPI_FLOAT_BIAS)) && !(p->Epi & OG_EPI_FLOAT))
-        return fail(ctx, OG_ERR_INVALID_ARG, "Epi", "a scale or float bias needs the float result bit");
+    if (requant) {
+        if (p->Epi & ~(OG_EPI_INT_BIAS | OG_EPI_SCALE_PER_COL))
+            return fail(ctx, OG_ERR_INVALID_ARG, "Epi", "a requantized product takes only the int bias and per-column multiplier bits, got 0x%x", p->Epi);
+    } else {
+        if (p->Epi & ~0xFu) return fail(ctx, OG_ERR_INVALID_ARG, "Epi", "unknown epilogue bits 0x%x", p->Epi & ~0xFu);
+        if ((p->Epi & (OG_EPI_SCALE_PER_COL | OG_EPI_FLOAT_BIAS)) && !(p->Epi & OG_EPI_FLOAT))
+            return fail(ctx, OG_ERR_INVALID_ARG, "Epi", "a scale or float bias needs the float result bit");
+    }
     const bool trans_b = p->Flags & OG_GEMM_TRANSPOSE_B;
     const uint64_t lda = p->Lda ? p->Lda : (p->K ? p->K : 1);
     const uint64_t cols_b = trans_b ? p->K : p->N;
@@ -443,10 +449,18 @@ int og_int8_gemm_kernel_name(const og_int8_gemm_params *p, uint32_t batch, char 
     return OG_OK;
 }
 
-int og_int8_gemm(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_buffer A, og_buffer B, og_buffer C,
-                 og_buffer ZA, og_buffer ZB, og_buffer bias, og_buffer scale, og_buffer fbias)
+// The output side of a requantized product (og_int8_gemm_requantized); absent for og_int8_gemm.
+struct RequantOut {
+    int32_t zero_point;
+    bool is_signed;
+};
+
+// og_int8_gemm and og_int8_gemm_requantized: validation, then the kernel choice and launch. With `rq`, C is the 8-bit
+// output Y (OffC and StrideC in bytes) and `scale` the multiplier.
+static int run_gemm(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_buffer A, og_buffer B, og_buffer C,
+                    og_buffer ZA, og_buffer ZB, og_buffer bias, og_buffer scale, og_buffer fbias, const RequantOut *rq)
 {
-    int st = check_gemm_params(ctx, p, batch);
+    int st = check_gemm_params(ctx, p, batch, rq != nullptr);
     if (st != OG_OK) return st;
     const bool trans_b = p->Flags & OG_GEMM_TRANSPOSE_B;
     const uint64_t M = p->M, N = p->N, K = p->K;
@@ -464,10 +478,19 @@ int og_int8_gemm(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_b
         if (last_b >= B.bytes) return fail(ctx, OG_ERR_INVALID_ARG, "OffsetB", "operand B reaches byte %llu but its buffer holds %llu", (unsigned long long)last_b, (unsigned long long)B.bytes);
     }
     const uint64_t count_c = M * N ? (uint64_t)(batch - 1) * stride_c + M * N : 0;
+    const uint64_t esize = rq ? 1 : 4;   // bytes per output element
     if (M > 0 && N > 0) {
-        if (!C.ptr) return fail(ctx, OG_ERR_INVALID_ARG, "c", "C is missing");
-        if (((uintptr_t)C.ptr & 3) != 0) return fail(ctx, OG_ERR_INVALID_ARG, "c", "C is not 4-byte aligned");
-        if (!fits((uint64_t)p->OffC * 4, count_c * 4, C)) return fail(ctx, OG_ERR_INVALID_ARG, "c", "elements %u..%llu reach past the buffer of %llu", p->OffC, (unsigned long long)(p->OffC + count_c), (unsigned long long)(C.bytes / 4));
+        const char *name = rq ? "y" : "c";
+        if (!C.ptr) return fail(ctx, OG_ERR_INVALID_ARG, name, "the output is missing");
+        if (!rq && ((uintptr_t)C.ptr & 3) != 0) return fail(ctx, OG_ERR_INVALID_ARG, "c", "C is not 4-byte aligned");
+        if (!fits((uint64_t)p->OffC * esize, count_c * esize, C)) return fail(ctx, OG_ERR_INVALID_ARG, name, "elements %u..%llu reach past the buffer of %llu", p->OffC, (unsigned long long)(p->OffC + count_c), (unsigned long long)(C.bytes / esize));
+    }
+    if (rq) {
+        if (rq->zero_point < (rq->is_signed ? -128 : 0) || rq->zero_point > (rq->is_signed ? 127 : 255))
+            return fail(ctx, OG_ERR_INVALID_ARG, "zeroPointY", "%d is outside the output type's range", rq->zero_point);
+        const uint64_t n = (p->Epi & OG_EPI_SCALE_PER_COL) ? N : 1;
+        if (!scale.ptr || ((uintptr_t)scale.ptr & 3)) return fail(ctx, OG_ERR_INVALID_ARG, "multiplier", "the multiplier is missing or misaligned");
+        if (!fits((uint64_t)p->OffScale * 4, n * 4, scale)) return fail(ctx, OG_ERR_INVALID_ARG, "multiplier", "elements %u..%llu reach past the buffer of %llu", p->OffScale, (unsigned long long)(p->OffScale + n), (unsigned long long)(scale.bytes / 4));
     }
     const bool has_za = p->Flags & OG_GEMM_ZA, has_zb = p->Flags & OG_GEMM_ZB;
     if (has_za) {
@@ -499,11 +522,11 @@ int og_int8_gemm(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_b
     og::GemmArgs g{};
     g.A = static_cast<const uint8_t *>(A.ptr) + p->OffA;
     g.B = static_cast<const uint8_t *>(B.ptr) + p->OffB;
-    g.C = static_cast<uint8_t *>(C.ptr) + (uint64_t)p->OffC * 4;
+    g.C = static_cast<uint8_t *>(C.ptr) + (uint64_t)p->OffC * esize;
     g.ZA = has_za ? static_cast<const uint8_t *>(ZA.ptr) + p->OffZA : nullptr;
     g.ZB = has_zb ? static_cast<const uint8_t *>(ZB.ptr) + p->OffZB : nullptr;
     g.bias = (p->Epi & OG_EPI_INT_BIAS) ? static_cast<const int32_t *>(bias.ptr) + p->OffBias : nullptr;
-    g.scale = (p->Epi & OG_EPI_FLOAT) ? static_cast<const float *>(scale.ptr) + p->OffScale : nullptr;
+    g.scale = (p->Epi & OG_EPI_FLOAT) || rq ? static_cast<const float *>(scale.ptr) + p->OffScale : nullptr;
     g.fbias = (p->Epi & OG_EPI_FLOAT_BIAS) ? static_cast<const float *>(fbias.ptr) + p->OffFBias : nullptr;
     g.strideA = p->StrideA;
     g.strideB = p->StrideB;
@@ -515,7 +538,8 @@ int og_int8_gemm(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_b
     g.lda = (int32_t)lda;
     g.ldb = (int32_t)ldb;
     g.flags = p->Flags;
-    g.epi = p->Epi;
+    g.epi = p->Epi | (rq ? (og::EPI_REQUANT | (rq->is_signed ? 0u : og::EPI_REQUANT_U8)) : 0u);
+    g.zp_y = rq ? rq->zero_point : 0;
 
     (void)hipSetDevice(ctx->device);
     og::GemmKernel k = og::choose_gemm_kernel(g.M, g.N, g.K, g.batch, g.flags);
@@ -554,6 +578,20 @@ int og_int8_gemm(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_b
         break;
     }
     return st == OG_OK ? ok(ctx) : st;
+}
+
+int og_int8_gemm(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_buffer A, og_buffer B, og_buffer C,
+                 og_buffer ZA, og_buffer ZB, og_buffer bias, og_buffer scale, og_buffer fbias)
+{
+    return run_gemm(ctx, p, batch, A, B, C, ZA, ZB, bias, scale, fbias, nullptr);
+}
+
+int og_int8_gemm_requantized(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_buffer A, og_buffer B,
+                             og_buffer Y, og_buffer ZA, og_buffer ZB, og_buffer bias, og_buffer multiplier,
+                             int32_t zero_point_y, uint32_t y_signed)
+{
+    const RequantOut rq{zero_point_y, y_signed != 0};
+    return run_gemm(ctx, p, batch, A, B, Y, ZA, ZB, bias, multiplier, og_buffer{nullptr, 0}, &rq);
 }
 
 int og_int8_epilogue(og_ctx *ctx, const og_int8_epilogue_params *p, og_buffer acc, og_buffer out, og_buffer bias,

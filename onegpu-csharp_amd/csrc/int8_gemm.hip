@@ -411,27 +411,35 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_tiled(GemmArgs g, int32_t
     // Store: MFMA 16 x 16 output layout, lane l holds rows 4 * (l / 16) + r, column l % 16.
     const bool za_row = g.flags & OG_GEMM_ZA_PER_ROW, zb_col = g.flags & OG_GEMM_ZB_PER_COL;
     const uint32_t Ku = (uint32_t)K;
-#pragma unroll
-    for (int j = 0; j < T::FN; j++) {
-        const int nl = wn * (BN / WN) + 16 * j + i16;
-        const int32_t n = n0 + nl;
-        if (n >= g.N) continue;
-        const uint32_t wz = (uint32_t)signed_zero(g.ZB, n, zb_col, b_signed);
-        const uint32_t st = SUM_B ? (uint32_t)ColSum[nl] : 0u;
-#pragma unroll
-        for (int i = 0; i < T::FM; i++) {
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int ml = wm * (BM / WM) + 16 * i + 4 * g4 + r;
-                const int32_t m = m0 + ml;
-                if (m >= g.M) continue;
-                const uint32_t zz = (uint32_t)signed_zero(g.ZA, m, za_row, a_signed);
-                const uint32_t ss = SUM_A ? (uint32_t)RowSum[ml] : 0u;
-                const uint32_t v = (uint32_t)acc[i][j][r] - wz * ss - zz * st + Ku * zz * wz;
-                store_value(g, batch * g.strideC + (int64_t)m * g.N + n, n, v);
-            }
-        }
+    // One copy of the loop per output kind, int32 / float32 or requantized bytes (written out twice: wrapping it in a
+    // lambda makes this kernel spill).
+#define OG_TILED_STORE_LOOP(STORE)                                                                                     \
+    for (int j = 0; j < T::FN; j++) {                                                                                  \
+        const int nl = wn * (BN / WN) + 16 * j + i16;                                                                  \
+        const int32_t n = n0 + nl;                                                                                     \
+        if (n >= g.N) continue;                                                                                        \
+        const uint32_t wz = (uint32_t)signed_zero(g.ZB, n, zb_col, b_signed);                                          \
+        const uint32_t st = SUM_B ? (uint32_t)ColSum[nl] : 0u;                                                         \
+        _Pragma("unroll") for (int i = 0; i < T::FM; i++) {                                                            \
+            _Pragma("unroll") for (int r = 0; r < 4; r++) {                                                            \
+                const int ml = wm * (BM / WM) + 16 * i + 4 * g4 + r;                                                   \
+                const int32_t m = m0 + ml;                                                                             \
+                if (m >= g.M) continue;                                                                                \
+                const uint32_t zz = (uint32_t)signed_zero(g.ZA, m, za_row, a_signed);                                  \
+                const uint32_t ss = SUM_A ? (uint32_t)RowSum[ml] : 0u;                                                 \
+                const uint32_t v = (uint32_t)acc[i][j][r] - wz * ss - zz * st + Ku * zz * wz;                          \
+                STORE(g, batch * g.strideC + (int64_t)m * g.N + n, n, v);                                              \
+            }                                                                                                          \
+        }                                                                                                              \
     }
+    if (g.epi & EPI_REQUANT) {
+#pragma unroll
+        OG_TILED_STORE_LOOP(store_requantized)
+    } else {
+#pragma unroll
+        OG_TILED_STORE_LOOP(store_sum)
+    }
+#undef OG_TILED_STORE_LOOP
 }
 
 template <int BM, int BN, int BK, int WM, int WN, bool TRANS_B>

@@ -206,7 +206,7 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
     const uint32_t za_raw = (SUM_B && g.ZA) ? g.ZA[(g.flags & OG_GEMM_ZA_PER_ROW) ? my_m : 0] : 0u;
     const uint32_t zb_raw = (SUM_A && g.ZB) ? g.ZB[(g.flags & OG_GEMM_ZB_PER_COL) ? my_n : 0] : 0u;
     const int32_t my_ib = (epi & OG_EPI_INT_BIAS) ? g.bias[my_n] : 0;
-    const float my_sc = (epi & OG_EPI_FLOAT) ? g.scale[(epi & OG_EPI_SCALE_PER_COL) ? my_n : 0] : 0.0f;
+    const float my_sc = (epi & (OG_EPI_FLOAT | EPI_REQUANT)) ? g.scale[(epi & OG_EPI_SCALE_PER_COL) ? my_n : 0] : 0.0f;
     const float my_fb = (epi & OG_EPI_FLOAT_BIAS) ? g.fbias[my_n] : 0.0f;
 
     // This tile's operand ranges (under 2^31 bytes, as the launcher checks): loads past the last valid byte return
@@ -436,11 +436,14 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
         sc[j] = ColSc[nl];
         fb[j] = ColFb[nl];
     }
-    int32_t *const Cb = static_cast<int32_t *>(g.C) + batch * g.strideC;   // int32 and float32 results alike
+    // int32 and float32 results are 4-byte elements, requantized ones bytes; strideC counts elements either way.
+    int32_t *const Cb = static_cast<int32_t *>(g.C) + batch * g.strideC;
+    uint8_t *const Yb = static_cast<uint8_t *>(g.C) + batch * g.strideC;
     const int32_t ncol0 = n0 + wn * WT + i32;
-    const int32_t M = g.M, N = g.N;
-    auto store_all = [&](auto float_tag, bool has_fb) {
-        constexpr bool FLT = decltype(float_tag)::value;
+    const int32_t M = g.M, N = g.N, zp_y = g.zp_y;
+    // MODE 0: int32 (+ bias); 1: float32, `opt` = float bias present; 2: requantized bytes, `opt` = uint8 output.
+    auto store_all = [&](auto mode_tag, bool opt) {
+        constexpr int MODE = decltype(mode_tag)::value;
 #pragma unroll
         for (int i = 0; i < F; i++) {
 #pragma unroll
@@ -453,16 +456,19 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
                     const int32_t m = m0 + ml + r;
                     if (m >= M) continue;
                     int32_t *const row = Cb + m * N;   // batch * M * N < 2^31 (checked at the boundary)
+                    uint8_t *const yrow = Yb + m * N;
                     const uint32_t ss = (uint32_t)ssv[r], zz = (uint32_t)zzv[r];
 #pragma unroll
                     for (int j = 0; j < F; j++) {
                         const int32_t n = ncol0 + 32 * j;
                         if (n >= N) continue;
                         const uint32_t v = (uint32_t)acc[i][j][4 * q + r] - wz[j] * ss - zz * ct[j] + ib[j];
-                        if constexpr (FLT) {
+                        if constexpr (MODE == 1) {
                             float f = __fmul_rn((float)(int32_t)v, sc[j]);
-                            if (has_fb) f = __fadd_rn(f, fb[j]);
+                            if (opt) f = __fadd_rn(f, fb[j]);
                             row[n] = __float_as_int(f);
+                        } else if constexpr (MODE == 2) {
+                            yrow[n] = (uint8_t)requantize_byte(v, sc[j], zp_y, opt);
                         } else {
                             row[n] = (int32_t)v;
                         }
@@ -471,11 +477,13 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
             }
         }
     };
-    if (epi & OG_EPI_FLOAT) {
-        if (epi & OG_EPI_FLOAT_BIAS) store_all(std::true_type{}, true);
-        else store_all(std::true_type{}, false);
+    if (epi & EPI_REQUANT) {
+        store_all(std::integral_constant<int, 2>{}, (epi & EPI_REQUANT_U8) != 0);
+    } else if (epi & OG_EPI_FLOAT) {
+        if (epi & OG_EPI_FLOAT_BIAS) store_all(std::integral_constant<int, 1>{}, true);
+        else store_all(std::integral_constant<int, 1>{}, false);
     } else {
-        store_all(std::false_type{}, false);
+        store_all(std::integral_constant<int, 0>{}, false);
     }
 }
 

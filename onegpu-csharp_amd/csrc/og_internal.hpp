@@ -25,8 +25,13 @@ struct GemmArgs {
     int32_t M, N, K, batch;
     int32_t lda, ldb;
     uint32_t flags;  // OG_GEMM_*
-    uint32_t epi;    // OG_EPI_*
+    uint32_t epi;    // OG_EPI_*, plus EPI_REQUANT / EPI_REQUANT_U8 below
+    int32_t zp_y;    // the output zero point of a requantized product
 };
+
+// Library-internal epilogue bits (above the public OG_EPI_* ones): C is 8-bit and each sum is requantized with the
+// multiplier at `scale` and the zero point zp_y; uint8 output when EPI_REQUANT_U8, else int8.
+constexpr uint32_t EPI_REQUANT = 0x100u, EPI_REQUANT_U8 = 0x200u;
 
 // Device workspace owned by a context: the partial sums of the few-rows kernels and the dynamic quantizer's
 // per-workgroup ranges. Sized once at og_init; the partial sums grow (outside any launch) when a larger few-rows product
@@ -137,9 +142,20 @@ __device__ __forceinline__ void transpose4x4(uint32_t r0, uint32_t r1, uint32_t 
 
 __device__ __forceinline__ int32_t sext8(uint32_t b) { return (int32_t)(int8_t)(uint8_t)b; }
 
+// QLinearMatMul's requantization of one sum (bias already added; Int8Epilogue.hlsl:54-68): v = fl(float(sum) * mult);
+// NaN to the lowest value; else round half to even, clamp to [lo - zp, hi - zp], add zp. Returns the byte.
+__device__ __forceinline__ uint32_t requantize_byte(uint32_t sum, float mult, int32_t zp, bool u8)
+{
+    const int32_t lo = u8 ? 0 : -128, hi = u8 ? 255 : 127;
+    const float v = __fmul_rn((float)(int32_t)sum, mult);
+    if ((__float_as_uint(v) & 0x7FFFFFFFu) > 0x7F800000u) return (uint32_t)lo & 0xFFu;   // NaN
+    const float r = fminf(fmaxf(rintf(v), (float)(lo - zp)), (float)(hi - zp));
+    return (uint32_t)((int32_t)r + zp) & 0xFFu;
+}
+
 // The int32 sum as the reference's StoreValue leaves it (Int8GemmEpilogue.hlsli:17-42): the raw sum; + int bias;
 // or fl(fl(float(sum + bias)) * scale), then + float bias as a separate rounding.
-__device__ __forceinline__ void store_value(const GemmArgs &g, int64_t ci, int32_t col, uint32_t sum)
+__device__ __forceinline__ void store_sum(const GemmArgs &g, int64_t ci, int32_t col, uint32_t sum)
 {
     uint32_t epi = g.epi;
     if (epi & OG_EPI_INT_BIAS) sum += (uint32_t)g.bias[col];
@@ -151,6 +167,22 @@ __device__ __forceinline__ void store_value(const GemmArgs &g, int64_t ci, int32
     float f = __fmul_rn((float)(int32_t)sum, s);
     if (epi & OG_EPI_FLOAT_BIAS) f = __fadd_rn(f, g.fbias[col]);
     static_cast<float *>(g.C)[ci] = f;
+}
+
+// A requantized product's byte (+ int bias, then requantize_byte with the multiplier and zp_y).
+__device__ __forceinline__ void store_requantized(const GemmArgs &g, int64_t ci, int32_t col, uint32_t sum)
+{
+    const uint32_t epi = g.epi;
+    if (epi & OG_EPI_INT_BIAS) sum += (uint32_t)g.bias[col];
+    const float mult = g.scale[(epi & OG_EPI_SCALE_PER_COL) ? col : 0];
+    static_cast<uint8_t *>(g.C)[ci] = (uint8_t)requantize_byte(sum, mult, g.zp_y, (epi & EPI_REQUANT_U8) != 0);
+}
+
+// Either of the two, as the product's epilogue bits say (for kernels that store few values a thread).
+__device__ __forceinline__ void store_value(const GemmArgs &g, int64_t ci, int32_t col, uint32_t sum)
+{
+    if (g.epi & EPI_REQUANT) store_requantized(g, ci, col, sum);
+    else store_sum(g, ci, col, sum);
 }
 
 // Zero point in the signed domain: an unsigned operand's bytes move by -128 (s = u ^ 0x80), and so does its zero point.

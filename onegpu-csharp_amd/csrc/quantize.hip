@@ -276,23 +276,12 @@ __global__ __launch_bounds__(256) void k_int8_epilogue(EpilogueArgs e)
         return;
     }
     const float s = e.scale[(e.flags & 2u) ? col : 0u];
-    const float v = __fmul_rn((float)(int32_t)acc, s);
     if (e.mode == 1) {
-        static_cast<float *>(e.out)[t] = v;
+        static_cast<float *>(e.out)[t] = __fmul_rn((float)(int32_t)acc, s);
         return;
     }
     // Mode 2 (Int8Epilogue.hlsl:54-68): NaN to the lowest value; rne; clamp to [lo - zp, hi - zp]; + zp.
-    const bool u8 = (e.flags & 8u) != 0u;
-    const int32_t lo = u8 ? 0 : -128, hi = u8 ? 255 : 127;
-    uint32_t q;
-    if (is_nan_bits(v)) {
-        q = (uint32_t)lo & 0xFFu;
-    } else {
-        float r = rintf(v);
-        r = fminf(fmaxf(r, (float)(lo - e.zero_point)), (float)(hi - e.zero_point));
-        q = (uint32_t)((int32_t)r + e.zero_point) & 0xFFu;
-    }
-    static_cast<uint8_t *>(e.out)[t] = (uint8_t)q;
+    static_cast<uint8_t *>(e.out)[t] = (uint8_t)requantize_byte(acc, s, e.zero_point, (e.flags & 8u) != 0u);
 }
 
 hipError_t launch_int8_epilogue(const EpilogueArgs &e, hipStream_t s, const char **kernel)

@@ -472,6 +472,28 @@ void Int8Gemm::EncodeRequantized(GpuCommandEncoder &encoder, const Int8GemmProbl
     if (multiplier.Buffer.Valid()) RequireType(kGemm, multiplier.Buffer, ElementType::Float32, "multiplier");
     CheckVector("multiplier", multiplier.Buffer, multiplier.Offset, multiplier.IsVector, problem.N);
     if (!prep.Ok) return;
+    if (options_.FusedRequantize) {
+        // One launch; a given scratch is still checked as the two-pass form checks it (Int8Gemm.cs:503-523), and the
+        // int bias as Finish checks it (655-661).
+        if (scratch) Scratch(count, scratch);
+        Epilogue rq;
+        rq.Requantized = true;
+        rq.ZeroPointY = zeroPointY;
+        rq.SignedY = outSigned;
+        rq.Scale = multiplier.Buffer;
+        rq.OffScale = (uint32_t)multiplier.Offset;
+        rq.Flags = multiplier.IsVector ? OG_EPI_SCALE_PER_COL : 0u;
+        if (intBias) {
+            if (intBias->Buffer.Valid()) RequireType(kGemm, intBias->Buffer, ElementType::Int32, "intBias");
+            CheckVector("intBias", intBias->Buffer, intBias->Offset, true, problem.N);
+            rq.Flags |= OG_EPI_INT_BIAS;
+            rq.IntBias = intBias->Buffer;
+            rq.OffIntBias = (uint32_t)intBias->Offset;
+        }
+        Multiply(encoder, problem, a, a.Type() == ElementType::Int8, b, b.Type() == ElementType::Int8, y,
+                 problem.OffsetC, zeroPointA, zeroPointB, rq);
+        return;
+    }
     auto [sums, at] = Scratch(count, scratch);
     Epilogue none;
     Multiply(encoder, problem, a, a.Type() == ElementType::Int8, b, b.Type() == ElementType::Int8, sums, at, zeroPointA,
@@ -583,6 +605,16 @@ void Int8Gemm::Multiply(GpuCommandEncoder &encoder, const Int8GemmProblem &p, co
     w.GridX = 0;
     uint32_t batch = (uint32_t)p.Batch;
     GpuBuffer A = a, B = b, C = c, ib = epi.IntBias, sc = epi.Scale, fb = epi.FloatBias;
+    if (epi.Requantized) {
+        const int32_t zy = epi.ZeroPointY;
+        const uint32_t ys = epi.SignedY ? 1u : 0u;
+        encoder.Record(
+            [w, batch, A, B, C, zaBuf, zbBuf, ib, sc, zy, ys](og_ctx *ctx) {
+                ThrowIfFailed(ctx, og_int8_gemm_requantized(ctx, &w, batch, bind(A), bind(B), bind(C), bind(zaBuf), bind(zbBuf), bind(ib), bind(sc), zy, ys), kGemm);
+            },
+            keep_of({&A, &B, &C, &zaBuf, &zbBuf, &ib, &sc}));
+        return;
+    }
     encoder.Record(
         [w, batch, A, B, C, zaBuf, zbBuf, ib, sc, fb](og_ctx *ctx) {
             ThrowIfFailed(ctx, og_int8_gemm(ctx, &w, batch, bind(A), bind(B), bind(C), bind(zaBuf), bind(zbBuf), bind(ib), bind(sc), bind(fb)), kGemm);

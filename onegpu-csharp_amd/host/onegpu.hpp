@@ -169,6 +169,10 @@ struct Int8GemmOptions {
     // its reduction pass, not the tiled one). 256 is this library's own: every shape on the 256 x 256 tile kernels,
     // which otherwise only large products reach.
     int Tile = 0;
+    // This library's own: EncodeRequantized in one launch, the requantization applied where the product stores its
+    // sums (og_int8_gemm_requantized), so no scratch is written. false keeps the reference's two passes (the product
+    // into scratch, then Finish). The bytes written are the same either way.
+    bool FusedRequantize = true;
 };
 
 // A zero point, scale, multiplier or bias operand (Int8Gemm.cs:23-29).
@@ -232,6 +236,9 @@ private:
     };
     struct Epilogue {
         uint32_t Flags = 0;
+        bool Requantized = false;   // C is the 8-bit output; Scale holds the multiplier (og_int8_gemm_requantized)
+        int ZeroPointY = 0;
+        bool SignedY = false;
         GpuBuffer IntBias;
         uint32_t OffIntBias = 0;
         GpuBuffer Scale;

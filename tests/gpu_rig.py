@@ -100,14 +100,15 @@ def run_int32(d, gemm, c: cases.Case, seed: int, want: np.ndarray | None = None)
     return bad, kernel
 
 
-def configs(d, all_: bool):
-    """Int8Tests.Configs (Int8Tests.cs:23-34): as chosen, portable, and the test hooks that force each kernel."""
-    lst = [("default", og.Int8Gemm(d)), ("portable", og.Int8Gemm(d, og.Int8GemmOptions(AllowPackedDot=False)))]
-    if all_:
-        lst.append(("tiled only", og.Int8Gemm(d, og.Int8GemmOptions(Tile=64))))
-        lst.append(("split k", og.Int8Gemm(d, og.Int8GemmOptions(Tile=32))))
-        lst.append(("large tile", og.Int8Gemm(d, og.Int8GemmOptions(Tile=256))))
-    return lst
+# The options of each configuration: as chosen, portable, and the test hooks that force each kernel.
+CONFIG_OPTIONS = {"default": {}, "portable": {"AllowPackedDot": False}, "tiled only": {"Tile": 64},
+                  "split k": {"Tile": 32}, "large tile": {"Tile": 256}}
+
+
+def configs(d, all_: bool, **extra):
+    """Int8Tests.Configs (Int8Tests.cs:23-34); `extra` adds options (FusedRequantize) to every configuration."""
+    names = ["default", "portable"] + (["tiled only", "split k", "large tile"] if all_ else [])
+    return [(n, og.Int8Gemm(d, og.Int8GemmOptions(**CONFIG_OPTIONS[n], **extra))) for n in names]
 
 
 _ABI = None

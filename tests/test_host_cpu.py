@@ -207,6 +207,31 @@ def test_abi_validates_before_touching_a_device():
     st, _ = call(GemmParams(M=4, N=4, K=4, Flags=0x08 | 0x10), ZA=Buf(addr, 3))
     assert lib.og_last_error_argument(None).decode() == "zpA"
 
+    # The one-launch requantized product: Y counts bytes (no alignment), the multiplier is required, the output zero
+    # point lies in the output type's range, and Epi holds only the int bias and per-column bits.
+    lib.og_int8_gemm_requantized.argtypes = ([ctypes.c_void_p, ctypes.POINTER(GemmParams), ctypes.c_uint32] + [Buf] * 7
+                                             + [ctypes.c_int32, ctypes.c_uint32])
+
+    def rq(p, y=16, mult=4, zero=0, signed=0, **kw):
+        bufs = dict(A=Buf(addr, 64), B=Buf(addr, 64), Y=Buf(addr + 1, y), ZA=none, ZB=none, bias=none,
+                    mult=Buf(addr, mult))
+        bufs.update(kw)
+        st = lib.og_int8_gemm_requantized(None, ctypes.byref(p), 1, *bufs.values(), zero, signed)
+        return st, lib.og_last_error_argument(None).decode()
+
+    assert rq(p) == (6, "ctx")                                    # 16 bytes at an odd address: valid
+    assert rq(p, y=15) == (1, "y")
+    assert rq(GemmParams(M=4, N=4, K=4, OffC=1)) == (1, "y")      # 16 bytes from byte 1 of a 16-byte buffer
+    assert rq(p, mult=0) == (1, "multiplier")
+    assert rq(GemmParams(M=4, N=4, K=4, Epi=0x4), mult=12) == (1, "multiplier")   # per column: 4 floats
+    assert rq(GemmParams(M=4, N=4, K=4, Epi=0x4), mult=16) == (6, "ctx")
+    assert rq(GemmParams(M=4, N=4, K=4, Epi=0x1)) == (1, "Epi")   # a float result is not a requantized one
+    assert rq(p, zero=256) == (1, "zeroPointY")
+    assert rq(p, zero=-1) == (1, "zeroPointY")
+    assert rq(p, zero=-128, signed=1) == (6, "ctx")
+    assert rq(p, zero=128, signed=1) == (1, "zeroPointY")
+    assert rq(GemmParams(M=4, N=4, K=4, Epi=0x2))[1] == "bias"
+
 
 def test_kernel_choice_is_reported():
     lib = ctypes.CDLL(og.LIB_PATH)

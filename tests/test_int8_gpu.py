@@ -6,7 +6,7 @@ import pytest
 import cases
 import oracle
 import onegpu_hip as og
-from gpu_rig import as_i8, as_u8, configs, device, run, run_int32, say, to_problem, binding, abi, check
+from gpu_rig import CONFIG_OPTIONS, as_i8, as_u8, configs, device, run, run_int32, say, to_problem, binding, abi, check
 
 pytestmark = pytest.mark.gpu
 
@@ -138,24 +138,71 @@ def test_float_and_requantized_forms_are_bit_exact(config):
     assert bad_f + bad_q == 0
 
 
-def test_requantization_rounds_half_to_even_and_saturates():
-    # Int8Tests.cs:503-547
+# Shapes that reach every kernel: few rows on the tiled few-rows kernel (or split k), the 128 and 256 direct kernels
+# (ragged M included), the register-staged 128 tile (K = 96), the generic kernel (unaligned rows), tiny products.
+REQUANT_KERNEL_SHAPES = [(1, 1, 1), (5, 7, 9), (4, 272, 512), (16, 256, 1024), (64, 64, 96), (33, 257, 77),
+                         (128, 384, 384), (130, 256, 512)]
+
+
+@pytest.mark.parametrize("fused", [True, False], ids=["one launch", "two passes"])
+@pytest.mark.parametrize("config", list(CONFIG_OPTIONS))
+def test_requantized_product_on_every_kernel(config, fused):
+    # EncodeRequantized (Int8Gemm.cs:336-363) with the requantization in the product's store (one launch), and as the
+    # reference runs it (the product into scratch, then Finish, 649-682), on each kernel a configuration reaches.
     d = device()
-    gemm = og.Int8Gemm(d)
+    gemm = og.Int8Gemm(d, og.Int8GemmOptions(**CONFIG_OPTIONS[config], FusedRequantize=fused))
+    bad, seed, kernels = 0, 300, set()
+    for (m, n, k) in REQUANT_KERNEL_SHAPES:
+        for i, vec in enumerate((False, True, False, True)):
+            unsigned, zero = cases.REQUANT_OUT[(seed + i) % len(cases.REQUANT_OUT)]
+            say(f"requant [{config}, {'one launch' if fused else 'two passes'}] {m}x{n}x{k} vec {vec} u8 {unsigned} "
+                f"zero {zero}")
+            bad += _requant_case(d, gemm, m, n, k, vec, unsigned, zero, (seed & 1) == 0, seed, (seed & 2) != 0,
+                                 (seed & 4) != 0)
+            kernels.add(d.LastKernel)
+            seed += 1
+    say(f"ROW requantized [{config}, {'one launch' if fused else 'two passes'}] wrong bytes {bad}; kernels "
+        f"{sorted(kernels)}")
+    assert bad == 0
+    if fused and config == "default":
+        assert {"mfma-i8-rows16-tiles", "mfma-i8-direct128x128x64", "mfma-i8-tile128x128x128",
+                "mfma-i8-generic128x128x64"} <= kernels, kernels
+    if fused and config == "large tile":
+        assert "mfma-i8-direct256x256x64" in kernels, kernels
+    if not fused:
+        assert kernels == {"int8-epilogue"}, kernels
+
+
+@pytest.mark.parametrize("fused", [True, False], ids=["one launch", "two passes"])
+@pytest.mark.parametrize("shape", [(1, 1, 1), (4, 256, 64), (128, 128, 64)])
+def test_requantization_rounds_half_to_even_and_saturates(shape, fused):
+    # Int8Tests.cs:503-547 (there on a 1 x 1 x 1 product); here also on the few-rows tiled kernel and the 128 direct
+    # kernel. Row m of A starts with the value under test and B's first row is all ones, so every byte of output row m
+    # is that value requantized (rows past the values hold 0).
+    m_, n_, k_ = shape
+    d = device()
+    gemm = og.Int8Gemm(d, og.Int8GemmOptions(FusedRequantize=fused))
     bad = 0
+    values = list(range(-9, 10))
     for mult, zero_y, unsigned in cases.REQUANT_TIES:
-        for av in range(-9, 10):
-            a = np.zeros(4, np.int8)
-            a[0] = av
-            b = np.zeros(4, np.int8)
-            b[0] = 1
+        for c0 in range(0, len(values), m_):
+            avs = values[c0:c0 + m_]
+            a = np.zeros((m_, k_), np.int8)
+            a[:len(avs), 0] = avs
+            b = np.zeros((k_, n_), np.int8)
+            b[0, :] = 1
             with np.errstate(all="ignore"):
-                want = oracle.requant(av, mult, zero_y, unsigned) & 0xFF
-            ba, bb = d.CreateBuffer(a), d.CreateBuffer(b)
+                want = np.array([oracle.requant(av, mult, zero_y, unsigned) & 0xFF for av in avs]
+                                + [oracle.requant(0, mult, zero_y, unsigned) & 0xFF] * (m_ - len(avs)), np.uint8)
+            ba, bb = d.CreateBuffer(a.ravel()), d.CreateBuffer(b.ravel())
             bm = d.CreateBuffer(np.array([mult], np.float32))
-            y = d.CreateBufferOf(og.ElementType.UInt8 if unsigned else og.ElementType.Int8, 4)
-            run(d, lambda e: gemm.EncodeRequantized(e, og.Int8GemmProblem(1, 1, 1), ba, bb, y, og.Int8Operand(bm, 0), zero_y))
-            bad += int(y.Read().view(np.uint8)[0] != want)
+            y = d.CreateBufferOf(og.ElementType.UInt8 if unsigned else og.ElementType.Int8, m_ * n_)
+            run(d, lambda e: gemm.EncodeRequantized(e, og.Int8GemmProblem(m_, n_, k_), ba, bb, y, og.Int8Operand(bm, 0),
+                                                    zero_y))
+            got = y.Read().view(np.uint8)[:m_ * n_].reshape(m_, n_)
+            bad += int(np.count_nonzero(got != want[:, None]))
+    say(f"ROW requantization ties {shape} {'one launch' if fused else 'two passes'}: wrong bytes {bad}, kernel "
+        f"{d.LastKernel}")
     assert bad == 0
 
 
