@@ -163,6 +163,17 @@ typedef struct og_int8_epilogue_params {
 int og_int8_epilogue(og_ctx *ctx, const og_int8_epilogue_params *params, og_buffer acc, og_buffer out, og_buffer bias,
                      og_buffer scale, og_buffer fbias);
 
+/* MatMulIntegerToFloat with the scale product folded into the product's epilogue: the column scale is
+ * fl(act_scale * scale[n or 0]), the f32 product the reference makes with a separate elementwise Mul before EncodeFloat
+ * (Int8Tests.cs:738-745: DynamicQuantizeLinear's scale times the per-column weight scale), and each result is then what
+ * og_int8_gemm with OG_EPI_FLOAT writes with that scale vector: fl(fl(float(sum + bias)) * s_n) (+ fbias as a separate
+ * rounding). Replaces the Mul dispatch + Int8Gemm.EncodeFloat (Int8Gemm.cs:270-314) pair with one launch. params as
+ * for og_int8_gemm with OG_EPI_FLOAT set; act_scale is one float32 at element act_offset of its buffer (e.g.
+ * og_dynamic_quantize's scale output). */
+int og_int8_gemm_float_scaled(og_ctx *ctx, const og_int8_gemm_params *params, uint32_t batch, og_buffer A, og_buffer B,
+                              og_buffer C, og_buffer ZA, og_buffer ZB, og_buffer bias, og_buffer act_scale,
+                              uint32_t act_offset, og_buffer scale, og_buffer fbias);
+
 /* Int8Gemm.EncodeRequantized (Int8Gemm.cs:336-363) in one launch: the product of og_int8_gemm and the mode-2 pass of
  * og_int8_epilogue, with the requantization applied where the product stores its sums, so the int32 sums never reach
  * memory and no scratch is used. Replaces the Multiply (554-639) + Finish (649-682) pair; each output byte equals what

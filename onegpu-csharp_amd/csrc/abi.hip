@@ -455,13 +455,25 @@ struct RequantOut {
     bool is_signed;
 };
 
+// The activation scale of og_int8_gemm_float_scaled.
+struct ActScale {
+    og_buffer buf;
+    uint32_t offset;
+};
+
 // og_int8_gemm and og_int8_gemm_requantized: validation, then the kernel choice and launch. With `rq`, C is the 8-bit
 // output Y (OffC and StrideC in bytes) and `scale` the multiplier.
 static int run_gemm(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_buffer A, og_buffer B, og_buffer C,
-                    og_buffer ZA, og_buffer ZB, og_buffer bias, og_buffer scale, og_buffer fbias, const RequantOut *rq)
+                    og_buffer ZA, og_buffer ZB, og_buffer bias, og_buffer scale, og_buffer fbias, const RequantOut *rq,
+                    const ActScale *act = nullptr)
 {
     int st = check_gemm_params(ctx, p, batch, rq != nullptr);
     if (st != OG_OK) return st;
+    if (act) {
+        if (!(p->Epi & OG_EPI_FLOAT)) return fail(ctx, OG_ERR_INVALID_ARG, "Epi", "a scaled product needs the float result bit");
+        if (!act->buf.ptr || ((uintptr_t)act->buf.ptr & 3)) return fail(ctx, OG_ERR_INVALID_ARG, "activationScale", "the activation scale is missing or misaligned");
+        if (!fits((uint64_t)act->offset * 4, 4, act->buf)) return fail(ctx, OG_ERR_INVALID_ARG, "activationScale", "element %u reaches past the buffer of %llu", act->offset, (unsigned long long)(act->buf.bytes / 4));
+    }
     const bool trans_b = p->Flags & OG_GEMM_TRANSPOSE_B;
     const uint64_t M = p->M, N = p->N, K = p->K;
     const uint64_t lda = p->Lda ? p->Lda : (K ? K : 1);
@@ -538,7 +550,9 @@ static int run_gemm(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, o
     g.lda = (int32_t)lda;
     g.ldb = (int32_t)ldb;
     g.flags = p->Flags;
-    g.epi = p->Epi | (rq ? (og::EPI_REQUANT | (rq->is_signed ? 0u : og::EPI_REQUANT_U8)) : 0u);
+    g.epi = p->Epi | (rq ? (og::EPI_REQUANT | (rq->is_signed ? 0u : og::EPI_REQUANT_U8)) : 0u) |
+            (act ? og::EPI_SCALE_PRODUCT : 0u);
+    g.act_scale = act ? static_cast<const float *>(act->buf.ptr) + act->offset : nullptr;
     g.zp_y = rq ? rq->zero_point : 0;
 
     (void)hipSetDevice(ctx->device);
@@ -584,6 +598,14 @@ int og_int8_gemm(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_b
                  og_buffer ZA, og_buffer ZB, og_buffer bias, og_buffer scale, og_buffer fbias)
 {
     return run_gemm(ctx, p, batch, A, B, C, ZA, ZB, bias, scale, fbias, nullptr);
+}
+
+int og_int8_gemm_float_scaled(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_buffer A, og_buffer B,
+                              og_buffer C, og_buffer ZA, og_buffer ZB, og_buffer bias, og_buffer act_scale,
+                              uint32_t act_offset, og_buffer scale, og_buffer fbias)
+{
+    const ActScale act{act_scale, act_offset};
+    return run_gemm(ctx, p, batch, A, B, C, ZA, ZB, bias, scale, fbias, nullptr, &act);
 }
 
 int og_int8_gemm_requantized(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_buffer A, og_buffer B,

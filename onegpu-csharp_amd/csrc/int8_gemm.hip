@@ -420,6 +420,9 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_tiled(GemmArgs g, int32_t
         if (n >= g.N) continue;                                                                                        \
         const uint32_t wz = (uint32_t)signed_zero(g.ZB, n, zb_col, b_signed);                                          \
         const uint32_t st = SUM_B ? (uint32_t)ColSum[nl] : 0u;                                                         \
+        const uint32_t cib = (g.epi & OG_EPI_INT_BIAS) ? (uint32_t)g.bias[n] : 0u;                                     \
+        const float csc = (g.epi & (OG_EPI_FLOAT | EPI_REQUANT)) ? column_scale(g, n) : 0.0f;                          \
+        const float cfb = (g.epi & OG_EPI_FLOAT_BIAS) ? g.fbias[n] : 0.0f;                                             \
         _Pragma("unroll") for (int i = 0; i < T::FM; i++) {                                                            \
             _Pragma("unroll") for (int r = 0; r < 4; r++) {                                                            \
                 const int ml = wm * (BM / WM) + 16 * i + 4 * g4 + r;                                                   \
@@ -428,16 +431,16 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_tiled(GemmArgs g, int32_t
                 const uint32_t zz = (uint32_t)signed_zero(g.ZA, m, za_row, a_signed);                                  \
                 const uint32_t ss = SUM_A ? (uint32_t)RowSum[ml] : 0u;                                                 \
                 const uint32_t v = (uint32_t)acc[i][j][r] - wz * ss - zz * st + Ku * zz * wz;                          \
-                STORE(g, batch * g.strideC + (int64_t)m * g.N + n, n, v);                                              \
+                STORE(g, batch * g.strideC + (int64_t)m * g.N + n, v + cib, csc, cfb);                                 \
             }                                                                                                          \
         }                                                                                                              \
     }
     if (g.epi & EPI_REQUANT) {
 #pragma unroll
-        OG_TILED_STORE_LOOP(store_requantized)
+        OG_TILED_STORE_LOOP(store_requantized_col)
     } else {
 #pragma unroll
-        OG_TILED_STORE_LOOP(store_sum)
+        OG_TILED_STORE_LOOP(store_sum_col)
     }
 #undef OG_TILED_STORE_LOOP
 }

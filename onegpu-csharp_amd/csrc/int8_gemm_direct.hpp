@@ -206,7 +206,7 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
     const uint32_t za_raw = (SUM_B && g.ZA) ? g.ZA[(g.flags & OG_GEMM_ZA_PER_ROW) ? my_m : 0] : 0u;
     const uint32_t zb_raw = (SUM_A && g.ZB) ? g.ZB[(g.flags & OG_GEMM_ZB_PER_COL) ? my_n : 0] : 0u;
     const int32_t my_ib = (epi & OG_EPI_INT_BIAS) ? g.bias[my_n] : 0;
-    const float my_sc = (epi & (OG_EPI_FLOAT | EPI_REQUANT)) ? g.scale[(epi & OG_EPI_SCALE_PER_COL) ? my_n : 0] : 0.0f;
+    const float my_sc = (epi & (OG_EPI_FLOAT | EPI_REQUANT)) ? column_scale(g, my_n) : 0.0f;
     const float my_fb = (epi & OG_EPI_FLOAT_BIAS) ? g.fbias[my_n] : 0.0f;
 
     // This tile's operand ranges (under 2^31 bytes, as the launcher checks): loads past the last valid byte return

@@ -21,6 +21,7 @@ struct GemmArgs {
     const int32_t *bias;
     const float *scale;
     const float *fbias;
+    const float *act_scale;   // EPI_SCALE_PRODUCT: the column scale is fl(*act_scale * scale[n or 0])
     int64_t strideA, strideB, strideC;
     int32_t M, N, K, batch;
     int32_t lda, ldb;
@@ -32,6 +33,8 @@ struct GemmArgs {
 // Library-internal epilogue bits (above the public OG_EPI_* ones): C is 8-bit and each sum is requantized with the
 // multiplier at `scale` and the zero point zp_y; uint8 output when EPI_REQUANT_U8, else int8.
 constexpr uint32_t EPI_REQUANT = 0x100u, EPI_REQUANT_U8 = 0x200u;
+// Library-internal: the float result's column scale is the product fl(*act_scale * scale[n or 0]).
+constexpr uint32_t EPI_SCALE_PRODUCT = 0x400u;
 
 // Device workspace owned by a context: the partial sums of the few-rows kernels and the dynamic quantizer's
 // per-workgroup ranges. Sized once at og_init; the partial sums grow (outside any launch) when a larger few-rows product
@@ -142,6 +145,13 @@ __device__ __forceinline__ void transpose4x4(uint32_t r0, uint32_t r1, uint32_t 
 
 __device__ __forceinline__ int32_t sext8(uint32_t b) { return (int32_t)(int8_t)(uint8_t)b; }
 
+// The column scale of a float result: scale[n or 0], or its product with the activation scale.
+__device__ __forceinline__ float column_scale(const GemmArgs &g, int32_t col)
+{
+    const float s = g.scale[(g.epi & OG_EPI_SCALE_PER_COL) ? col : 0];
+    return (g.epi & EPI_SCALE_PRODUCT) ? __fmul_rn(*g.act_scale, s) : s;
+}
+
 // QLinearMatMul's requantization of one sum (bias already added; Int8Epilogue.hlsl:54-68): v = fl(float(sum) * mult);
 // NaN to the lowest value; else round half to even, clamp to [lo - zp, hi - zp], add zp. Returns the byte.
 __device__ __forceinline__ uint32_t requantize_byte(uint32_t sum, float mult, int32_t zp, bool u8)
@@ -163,7 +173,7 @@ __device__ __forceinline__ void store_sum(const GemmArgs &g, int64_t ci, int32_t
         static_cast<int32_t *>(g.C)[ci] = (int32_t)sum;
         return;
     }
-    float s = g.scale[(epi & OG_EPI_SCALE_PER_COL) ? col : 0];
+    const float s = column_scale(g, col);
     float f = __fmul_rn((float)(int32_t)sum, s);
     if (epi & OG_EPI_FLOAT_BIAS) f = __fadd_rn(f, g.fbias[col]);
     static_cast<float *>(g.C)[ci] = f;
@@ -176,6 +186,24 @@ __device__ __forceinline__ void store_requantized(const GemmArgs &g, int64_t ci,
     if (epi & OG_EPI_INT_BIAS) sum += (uint32_t)g.bias[col];
     const float mult = g.scale[(epi & OG_EPI_SCALE_PER_COL) ? col : 0];
     static_cast<uint8_t *>(g.C)[ci] = (uint8_t)requantize_byte(sum, mult, g.zp_y, (epi & EPI_REQUANT_U8) != 0);
+}
+
+// store_sum and store_requantized with the column's int bias already added to `sum` and its scale (multiplier) and
+// float bias fetched, for kernels that store many values of one column.
+__device__ __forceinline__ void store_sum_col(const GemmArgs &g, int64_t ci, uint32_t sum, float sc, float fb)
+{
+    if (!(g.epi & OG_EPI_FLOAT)) {
+        static_cast<int32_t *>(g.C)[ci] = (int32_t)sum;
+        return;
+    }
+    float f = __fmul_rn((float)(int32_t)sum, sc);
+    if (g.epi & OG_EPI_FLOAT_BIAS) f = __fadd_rn(f, fb);
+    static_cast<float *>(g.C)[ci] = f;
+}
+
+__device__ __forceinline__ void store_requantized_col(const GemmArgs &g, int64_t ci, uint32_t sum, float mult, float)
+{
+    static_cast<uint8_t *>(g.C)[ci] = (uint8_t)requantize_byte(sum, mult, g.zp_y, (g.epi & EPI_REQUANT_U8) != 0);
 }
 
 // Either of the two, as the product's epilogue bits say (for kernels that store few values a thread).

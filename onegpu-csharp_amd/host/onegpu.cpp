@@ -419,6 +419,25 @@ void Int8Gemm::EncodeFloat(GpuCommandEncoder &encoder, const Int8GemmProblem &pr
                            const std::optional<Int8Operand> &zeroPointA, const std::optional<Int8Operand> &zeroPointB,
                            const std::optional<Int8Operand> &floatBias, const std::optional<Int8Operand> &intBias)
 {
+    FloatProduct(encoder, problem, a, b, c, nullptr, scale, zeroPointA, zeroPointB, floatBias, intBias);
+}
+
+void Int8Gemm::EncodeFloatScaled(GpuCommandEncoder &encoder, const Int8GemmProblem &problem, const GpuBuffer &a,
+                                 const GpuBuffer &b, const GpuBuffer &c, const Int8Operand &activationScale,
+                                 const Int8Operand &weightScale, const std::optional<Int8Operand> &zeroPointA,
+                                 const std::optional<Int8Operand> &zeroPointB,
+                                 const std::optional<Int8Operand> &floatBias, const std::optional<Int8Operand> &intBias)
+{
+    FloatProduct(encoder, problem, a, b, c, &activationScale, weightScale, zeroPointA, zeroPointB, floatBias, intBias);
+}
+
+// EncodeFloat's checks and recording (Int8Gemm.cs:270-314), with the activation scale when there is one.
+void Int8Gemm::FloatProduct(GpuCommandEncoder &encoder, const Int8GemmProblem &problem, const GpuBuffer &a,
+                            const GpuBuffer &b, const GpuBuffer &c, const Int8Operand *activationScale,
+                            const Int8Operand &scale, const std::optional<Int8Operand> &zeroPointA,
+                            const std::optional<Int8Operand> &zeroPointB, const std::optional<Int8Operand> &floatBias,
+                            const std::optional<Int8Operand> &intBias)
+{
     if (!c.Valid()) throw GpuKernelShapeException(kGemm, "c", "buffer is null");
     auto prep = Prepare(problem, a, b, zeroPointA, zeroPointB);
     RequireType(kGemm, c, ElementType::Float32, "c");
@@ -427,6 +446,10 @@ void Int8Gemm::EncodeFloat(GpuCommandEncoder &encoder, const Int8GemmProblem &pr
     CheckBindable("C", c);
     if (scale.Buffer.Valid()) RequireType(kGemm, scale.Buffer, ElementType::Float32, "scale");
     CheckVector("scale", scale.Buffer, scale.Offset, scale.IsVector, problem.N);
+    if (activationScale) {
+        if (activationScale->Buffer.Valid()) RequireType(kGemm, activationScale->Buffer, ElementType::Float32, "activationScale");
+        CheckVector("activationScale", activationScale->Buffer, activationScale->Offset, false, problem.N);
+    }
     if (floatBias) {
         if (floatBias->Buffer.Valid()) RequireType(kGemm, floatBias->Buffer, ElementType::Float32, "floatBias");
         CheckVector("floatBias", floatBias->Buffer, floatBias->Offset, true, problem.N);
@@ -451,6 +474,10 @@ void Int8Gemm::EncodeFloat(GpuCommandEncoder &encoder, const Int8GemmProblem &pr
     CheckBindable("scale", scale.Buffer);
     epi.Scale = scale.Buffer;
     epi.OffScale = (uint32_t)scale.Offset;
+    if (activationScale) {
+        epi.ActScale = activationScale->Buffer;
+        epi.OffActScale = (uint32_t)activationScale->Offset;
+    }
     Multiply(encoder, problem, a, a.Type() == ElementType::Int8, b, b.Type() == ElementType::Int8, c, problem.OffsetC,
              zeroPointA, zeroPointB, epi);
 }
@@ -613,6 +640,16 @@ void Int8Gemm::Multiply(GpuCommandEncoder &encoder, const Int8GemmProblem &p, co
                 ThrowIfFailed(ctx, og_int8_gemm_requantized(ctx, &w, batch, bind(A), bind(B), bind(C), bind(zaBuf), bind(zbBuf), bind(ib), bind(sc), zy, ys), kGemm);
             },
             keep_of({&A, &B, &C, &zaBuf, &zbBuf, &ib, &sc}));
+        return;
+    }
+    if (epi.ActScale.Valid()) {
+        GpuBuffer as = epi.ActScale;
+        const uint32_t aoff = epi.OffActScale;
+        encoder.Record(
+            [w, batch, A, B, C, zaBuf, zbBuf, ib, as, aoff, sc, fb](og_ctx *ctx) {
+                ThrowIfFailed(ctx, og_int8_gemm_float_scaled(ctx, &w, batch, bind(A), bind(B), bind(C), bind(zaBuf), bind(zbBuf), bind(ib), bind(as), aoff, bind(sc), bind(fb)), kGemm);
+            },
+            keep_of({&A, &B, &C, &zaBuf, &zbBuf, &ib, &as, &sc, &fb}));
         return;
     }
     encoder.Record(

@@ -214,6 +214,15 @@ public:
                      const std::optional<Int8Operand> &zeroPointB = std::nullopt,
                      const std::optional<Int8Operand> &floatBias = std::nullopt,
                      const std::optional<Int8Operand> &intBias = std::nullopt);
+    // This library's own: EncodeFloat whose column scale is fl(activationScale * weightScale[n or 0]), the product
+    // the reference computes with an elementwise Mul before EncodeFloat (Int8Tests.cs:738-745); one launch, the same
+    // bits. activationScale is one float32 (e.g. DynamicQuantizeLinear's scale output).
+    void EncodeFloatScaled(GpuCommandEncoder &encoder, const Int8GemmProblem &problem, const GpuBuffer &a,
+                           const GpuBuffer &b, const GpuBuffer &c, const Int8Operand &activationScale,
+                           const Int8Operand &weightScale, const std::optional<Int8Operand> &zeroPointA = std::nullopt,
+                           const std::optional<Int8Operand> &zeroPointB = std::nullopt,
+                           const std::optional<Int8Operand> &floatBias = std::nullopt,
+                           const std::optional<Int8Operand> &intBias = std::nullopt);
     // Int8Gemm.cs:316-363: QLinearMatMul, the sums in scratch, then the requantizing pass.
     void EncodeRequantized(GpuCommandEncoder &encoder, const Int8GemmProblem &problem, const GpuBuffer &a,
                            const GpuBuffer &b, const GpuBuffer &y, const Int8Operand &multiplier, int zeroPointY,
@@ -237,6 +246,8 @@ private:
     struct Epilogue {
         uint32_t Flags = 0;
         bool Requantized = false;   // C is the 8-bit output; Scale holds the multiplier (og_int8_gemm_requantized)
+        GpuBuffer ActScale;         // when valid: the column scale is fl(ActScale[OffActScale] * Scale[..])
+        uint32_t OffActScale = 0;
         int ZeroPointY = 0;
         bool SignedY = false;
         GpuBuffer IntBias;
@@ -249,6 +260,11 @@ private:
     Prepared Prepare(const Int8GemmProblem &p, const GpuBuffer &a, const GpuBuffer &b,
                      const std::optional<Int8Operand> &zpA, const std::optional<Int8Operand> &zpB);
     void CheckBindable(const std::string &operand, const GpuBuffer &buffer) const;
+    void FloatProduct(GpuCommandEncoder &encoder, const Int8GemmProblem &problem, const GpuBuffer &a,
+                      const GpuBuffer &b, const GpuBuffer &c, const Int8Operand *activationScale,
+                      const Int8Operand &scale, const std::optional<Int8Operand> &zeroPointA,
+                      const std::optional<Int8Operand> &zeroPointB, const std::optional<Int8Operand> &floatBias,
+                      const std::optional<Int8Operand> &intBias);
     void Multiply(GpuCommandEncoder &encoder, const Int8GemmProblem &p, const GpuBuffer &a, bool aSigned,
                   const GpuBuffer &b, bool bSigned, const GpuBuffer &c, int offsetC,
                   const std::optional<Int8Operand> &za, const std::optional<Int8Operand> &zb, const Epilogue &epi);

@@ -131,7 +131,19 @@ PYBIND11_MODULE(_onegpu_host, m)
     py::class_<GpuCommandEncoder>(m, "GpuCommandEncoder")
         .def_property_readonly("DispatchCount", &GpuCommandEncoder::DispatchCount)
         .def("BeginPassTiming", &GpuCommandEncoder::BeginPassTiming, py::arg("max_passes"))
-        .def("EndPassTiming", &GpuCommandEncoder::EndPassTiming);
+        .def("EndPassTiming", &GpuCommandEncoder::EndPassTiming)
+        // Benchmark utility (no counterpart in the reference's kernel families): records out[i] = fl(a[0] * b[i]) for
+        // i < n, the elementwise Mul of the reference's MatMulIntegerToFloat chain, as one dispatch of this encoder.
+        .def("RecordScaleProduct", [](GpuCommandEncoder &e, const GpuBuffer &a, const GpuBuffer &b, uint32_t n,
+                                      const GpuBuffer &out) {
+            og_buffer ba = a.Binding(), bb = b.Binding(), bo = out.Binding();
+            e.Record(
+                [ba, bb, n, bo](og_ctx *ctx) {
+                    if (og_util_scale_product(ctx, ba, bb, n, bo) != OG_OK)
+                        throw std::runtime_error(std::string("scale product: ") + og_last_error(ctx));
+                },
+                {a.impl(), b.impl(), out.impl()});
+        }, py::arg("a"), py::arg("b"), py::arg("n"), py::arg("out"));
 
     py::class_<GpuDevice, std::shared_ptr<GpuDevice>>(m, "GpuDevice")
         .def_static("Create", [](int ordinal, uint64_t max_binding) { GpuDeviceOptions o; o.MaxStorageBufferBindingBytes = max_binding; return GpuDevice::Create(ordinal, o); },
@@ -203,6 +215,10 @@ PYBIND11_MODULE(_onegpu_host, m)
         .def("EncodeFloat", &Int8Gemm::EncodeFloat, py::arg("encoder"), py::arg("problem"), py::arg("a"), py::arg("b"),
              py::arg("c"), py::arg("scale"), py::arg("zeroPointA") = py::none(), py::arg("zeroPointB") = py::none(),
              py::arg("floatBias") = py::none(), py::arg("intBias") = py::none())
+        .def("EncodeFloatScaled", &Int8Gemm::EncodeFloatScaled, py::arg("encoder"), py::arg("problem"), py::arg("a"),
+             py::arg("b"), py::arg("c"), py::arg("activationScale"), py::arg("weightScale"),
+             py::arg("zeroPointA") = py::none(), py::arg("zeroPointB") = py::none(), py::arg("floatBias") = py::none(),
+             py::arg("intBias") = py::none())
         .def("EncodeRequantized", &Int8Gemm::EncodeRequantized, py::arg("encoder"), py::arg("problem"), py::arg("a"),
              py::arg("b"), py::arg("y"), py::arg("multiplier"), py::arg("zeroPointY"), py::arg("zeroPointA") = py::none(),
              py::arg("zeroPointB") = py::none(), py::arg("intBias") = py::none(), py::arg("scratch") = py::none())

@@ -53,6 +53,17 @@ def test_int8_gemm_bad_arguments_are_rejected(d):
     shape_error(lambda: gemm.EncodeInt32(enc, P(2, 2, 2), a, b, c, og.Int8Operand(a, 63, True)), "zpA")
     shape_error(lambda: gemm.EncodeInt32(enc, P(2, 2, 2), f, b, c), "a")
     shape_error(lambda: gemm.EncodeFloat(enc, P(2, 8, 2), a, b, f, og.Int8Operand(fl, 0, True)), "scale")
+    # EncodeFloatScaled (this library's one-launch MatMulIntegerToFloat): EncodeFloat's checks plus a float32
+    # activation scale of one element.
+    shape_error(lambda: gemm.EncodeFloatScaled(enc, P(2, 8, 2), a, b, f, og.Int8Operand(fl, 0), og.Int8Operand(fl, 0, True)),
+                "scale")
+    shape_error(lambda: gemm.EncodeFloatScaled(enc, P(2, 8, 2), a, b, f, og.Int8Operand(fl, 1), og.Int8Operand(fl, 0)),
+                "activationScale")
+    shape_error(lambda: gemm.EncodeFloatScaled(enc, P(2, 8, 2), a, b, f, og.Int8Operand(c, 0), og.Int8Operand(fl, 0)),
+                "activationScale")
+    ok_enc = d.BeginCommands()
+    gemm.EncodeFloatScaled(ok_enc, P(2, 8, 2), a, b, f, og.Int8Operand(fl, 0), og.Int8Operand(f, 0, True))
+    assert ok_enc.DispatchCount == 1
     shape_error(lambda: gemm.EncodeRequantized(enc, P(2, 2, 2), a, b, a, og.Int8Operand(fl, 0), 300), "zeroPointY")
     shape_error(lambda: gemm.EncodeRequantized(enc, P(2, 2, 2), a, b, b, og.Int8Operand(fl, 0), 128), "zeroPointY")
     # Further checks of Prepare (Int8Gemm.cs:419-484).
@@ -231,6 +242,24 @@ def test_abi_validates_before_touching_a_device():
     assert rq(p, zero=-128, signed=1) == (6, "ctx")
     assert rq(p, zero=128, signed=1) == (1, "zeroPointY")
     assert rq(GemmParams(M=4, N=4, K=4, Epi=0x2))[1] == "bias"
+
+    # The one-launch MatMulIntegerToFloat: a float result whose column scale takes the activation scale.
+    lib.og_int8_gemm_float_scaled.argtypes = ([ctypes.c_void_p, ctypes.POINTER(GemmParams), ctypes.c_uint32] + [Buf] * 7
+                                              + [ctypes.c_uint32, Buf, Buf])
+
+    def fs(p, act=4, act_off=0, **kw):
+        bufs = dict(A=Buf(addr, 64), B=Buf(addr, 64), C=Buf(addr, 64), ZA=none, ZB=none, bias=none)
+        st = lib.og_int8_gemm_float_scaled(None, ctypes.byref(p), 1, *bufs.values(), Buf(addr, act), act_off,
+                                           kw.get("scale", Buf(addr, 16)), none)
+        return st, lib.og_last_error_argument(None).decode()
+
+    pf = GemmParams(M=4, N=4, K=4, Epi=0x1 | 0x4)
+    assert fs(pf) == (6, "ctx")
+    assert fs(GemmParams(M=4, N=4, K=4)) == (1, "Epi")           # an int32 result has no scale
+    assert fs(pf, act=0) == (1, "activationScale")
+    assert fs(pf, act=8, act_off=2) == (1, "activationScale")
+    assert fs(pf, act=8, act_off=1) == (6, "ctx")
+    assert fs(pf, scale=Buf(addr, 12)) == (1, "scale")
 
 
 def test_kernel_choice_is_reported():

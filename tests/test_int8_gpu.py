@@ -173,6 +173,49 @@ def test_requantized_product_on_every_kernel(config, fused):
         assert kernels == {"int8-epilogue"}, kernels
 
 
+# Activation scales for the scaled float product: ordinary, tiny (products in the denormal range, kept), huge
+# (products that overflow to infinity) and NaN.
+ACT_SCALES = [0.0123, 3.7e-3, 1e-30, 3e36, float("nan")]
+
+
+@pytest.mark.parametrize("config", list(CONFIG_OPTIONS))
+def test_scaled_float_product_on_every_kernel(config):
+    # EncodeFloatScaled: MatMulIntegerToFloat with the column scale fl(actScale * wScale[n]) made in the product's
+    # epilogue. Expected: numpy's float32 product (IEEE, round to nearest even) as the scale vector, then the oracle's
+    # float steps (Int8Tests.cs:356-373), i.e. the reference's Mul + EncodeFloat chain.
+    d = device()
+    gemm = og.Int8Gemm(d, og.Int8GemmOptions(**CONFIG_OPTIONS[config]))
+    bad, seed, kernels = 0, 700, set()
+    for (m, n, k) in REQUANT_KERNEL_SHAPES:
+        for i, vec in enumerate((True, False)):
+            act = np.float32(ACT_SCALES[(seed + i) % len(ACT_SCALES)])
+            with_ib, with_fb = (seed & 1) == 0, (seed & 2) == 0
+            a, b, za, zb, wscale, ib, fb = cases.float_case_data(m, n, k, vec, seed)
+            p = cases.problem(m, n, k)
+            sums = oracle.int8_gemm(p, a, False, b, True, (za, False, 0), (zb, True, 0))
+            with np.errstate(all="ignore"):
+                colscale = (act * wscale.astype(np.float32)).astype(np.float32)
+            expected = oracle.float_epilogue(sums, n, colscale, vec, ib if with_ib else None, fb if with_fb else None)
+            say(f"scaled float [{config}] {m}x{n}x{k} vec {vec} act {act} ib {with_ib} fb {with_fb}")
+            ba, bb = d.CreateBuffer(as_u8(a)), d.CreateBuffer(as_i8(b))
+            bza, bzb = d.CreateBuffer(as_u8(za)), d.CreateBuffer(as_i8(zb))
+            bs, bib, bfb = d.CreateBuffer(wscale), d.CreateBuffer(ib), d.CreateBuffer(fb)
+            bact = d.CreateBuffer(np.array([0.0, act], np.float32))
+            bc = d.CreateBufferOf(og.ElementType.Float32, m * n)
+            run(d, lambda e: gemm.EncodeFloatScaled(e, to_problem(p), ba, bb, bc, og.Int8Operand(bact, 1),
+                                                    og.Int8Operand(bs, 0, vec), og.Int8Operand(bza, 0),
+                                                    og.Int8Operand(bzb, 0, True),
+                                                    og.Int8Operand(bfb, 0, True) if with_fb else None,
+                                                    og.Int8Operand(bib, 0, True) if with_ib else None))
+            got = bc.Read()
+            same = np.where(np.isnan(expected), np.isnan(got), got.view(np.uint32) == expected.view(np.uint32))
+            bad += int(np.count_nonzero(~same))
+            kernels.add(d.LastKernel)
+            seed += 1
+    say(f"ROW scaled float [{config}] wrong values {bad}; kernels {sorted(kernels)}")
+    assert bad == 0
+
+
 @pytest.mark.parametrize("fused", [True, False], ids=["one launch", "two passes"])
 @pytest.mark.parametrize("shape", [(1, 1, 1), (4, 256, 64), (128, 128, 64)])
 def test_requantization_rounds_half_to_even_and_saturates(shape, fused):
