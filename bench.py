@@ -411,6 +411,27 @@ def qlinear_c2(d, steps, warmup, fused, check=True):
     return res
 
 
+def embedding_gather(d, steps, warmup, tokens, check=True, vocab=250002, hidden=768):
+    """The int8 embedding lookup in front of the first int8 product: Gather on axis 0 of an int8 table
+    [vocab, hidden] (the largest vocabulary of the reference's embedding tests) with `tokens` int64 token ids.
+    Bytes per step: the rows read and written once each, and the ids."""
+    table = synth(d, og.ElementType.Int8, vocab * hidden, 6, 60, -128, 127, 0)
+    ids_host = (np.random.default_rng(tokens).integers(0, vocab, tokens)).astype(np.int64)
+    ids = d.CreateBuffer(ids_host)
+    out = d.CreateBufferOf(og.ElementType.Int8, tokens * hidden)
+    k = og.GatherKernels(d)
+    wall, region, times = timed(d, lambda e, i: k.EncodeGather(e, table, 0, [vocab, hidden], 0, ids, 0, tokens, out, 0),
+                                steps, warmup)
+    res = {"tokens": tokens, "bytes": 2 * tokens * hidden + 8 * tokens, "wall_s": wall, "step_mean_ms": region / steps * 1e3,
+           "kernel": times[0][1] if times else ""}
+    if check:
+        rows = np.array([0, 1, tokens // 2, tokens - 1])
+        T = table.Read().reshape(vocab, hidden)
+        got = out.Read().reshape(tokens, hidden)[rows]
+        res["check"] = "bit-exact" if np.array_equal(got, T[ids_host[rows]]) else "MISMATCH"
+    return res
+
+
 def only(d, name, steps, warmup):
     """One workload alone (for rocprofv3 runs of committed files); prints a one-line summary."""
     if name == "c4":
@@ -424,6 +445,8 @@ def only(d, name, steps, warmup):
         r = c5_batched(d, steps, warmup, check=False)
     elif name in ("c2q", "c2q2"):
         r = qlinear_c2(d, steps, warmup, fused=name == "c2q", check=False)
+    elif name.startswith("gather"):
+        r = embedding_gather(d, steps, warmup, int(name[6:] or 4096), check=False)
     elif name == "copy":
         r = copy_workload(d, steps, warmup)
     elif name in ("c4const", "c4nt", "c4plain", "c4plainnt"):
@@ -443,7 +466,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline configuration only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["c4", "c4const", "c4nt", "c4plain", "c4plainnt", "gemv1", "gemv4", "gemv16", "c2", "c2q", "c2q2", "c5", "copy", "vendor"],
+    ap.add_argument("--only", choices=["c4", "c4const", "c4nt", "c4plain", "c4plainnt", "gemv1", "gemv4", "gemv16", "c2", "c2q", "c2q2", "c5", "gather4096", "gather65536", "copy", "vendor"],
                     help="run one workload alone and print its summary (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -504,6 +527,14 @@ def main():
                             "dispatch_mean_us": {k: v * 1e3 for k, v in r["dispatch_mean_ms"].items()},
                             "check": r["check"]}
             log(json.dumps(configs[key]))
+        for tokens in (4096, 65536):
+            log(f"int8 embedding lookup: 250002 x 768 table, {tokens} token ids")
+            r = embedding_gather(d, args.steps, args.warmup, tokens)
+            gbs = r["bytes"] / (r["step_mean_ms"] * 1e-3) / 1e9
+            configs[f"embedding_gather_{tokens}"] = {"step_mean_us": r["step_mean_ms"] * 1e3, "gbs": gbs,
+                                                     "frac": gbs / PEAK_HBM_GBS, "kernel": r["kernel"],
+                                                     "check": r["check"]}
+            log(json.dumps(configs[f"embedding_gather_{tokens}"]))
         log("config 5: batched 32 x 512 x 4096 x 4096")
         r = c5_batched(d, max(3, args.steps // 5), 2)
         configs["c5_batched"] = {"tops_kernel": r["ops"] / (r["kernel_mean_ms"] * 1e-3) / 1e12,

@@ -226,6 +226,23 @@ int og_dequantize(og_ctx *ctx, int kind, int f16_out, const og_dequant_params *p
 int og_quantize(og_ctx *ctx, int is_signed, int f16_in, const og_dequant_params *params, og_buffer X, og_buffer scale,
                 og_buffer zero, og_buffer out);
 
+/* ------------------------------------------------------------------ Gather (the int8 embedding lookup) */
+
+/* GatherParams, 9 words (src/RecursiveAI.OneGpu.Kernels/Shaders/Gather.hlsl:6-17). The data tensor is seen as
+ * [outer, AxisLen, Inner] elements, the output as [outer, IdxCount, Inner]; Count = outer * IdxCount * Inner. Offsets
+ * count elements (indices: index elements). Flags bit 0: int64 indices (else int32). GridX is ignored. */
+typedef struct og_gather_params {
+    uint32_t Count, OffData, OffOut, OffIdx, GridX, Flags, Inner, IdxCount, AxisLen;
+} og_gather_params;
+
+/* out[o, i, n] = data[o, index[i], n] for elements of elem_bytes bytes (1: uint8/int8, 2: half, 4, 8); a negative
+ * index counts from the end of the axis. An index outside [-AxisLen, AxisLen) reads nothing: its output elements are
+ * zero and, when status is given (one uint32, initialised to 0xFFFFFFFF by the caller), the smallest such position is
+ * recorded there with an atomic minimum. Output bytes outside the gathered range are left as they are. The output
+ * must not overlap the data. Replaces GatherKernels.EncodeGather's dispatch (GatherKernels.cs:66-118, Gather.hlsl). */
+int og_gather(og_ctx *ctx, uint32_t elem_bytes, const og_gather_params *params, og_buffer data, og_buffer indices,
+              og_buffer out, og_buffer status);
+
 /* ------------------------------------------------------------------ diagnostics */
 
 const char *og_last_error(og_ctx *ctx);           /* text of the last failure (thread-local when ctx is NULL) */

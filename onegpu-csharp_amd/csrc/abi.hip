@@ -656,6 +656,53 @@ int og_int8_epilogue(og_ctx *ctx, const og_int8_epilogue_params *p, og_buffer ac
     return st == OG_OK ? ok(ctx) : st;
 }
 
+// ------------------------------------------------------------------ Gather
+
+int og_gather(og_ctx *ctx, uint32_t elem_bytes, const og_gather_params *p, og_buffer data, og_buffer indices,
+              og_buffer out, og_buffer status)
+{
+    if (!p) return fail(ctx, OG_ERR_INVALID_ARG, "params", "null parameter block");
+    if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8)
+        return fail(ctx, OG_ERR_INVALID_ARG, "T", "element size %u is not 1, 2, 4 or 8 bytes", elem_bytes);
+    if (p->Flags & ~1u) return fail(ctx, OG_ERR_INVALID_ARG, "Flags", "unknown flag bits 0x%x", p->Flags & ~1u);
+    if (p->Count > 0x7FFFFFFFu) return fail(ctx, OG_ERR_INVALID_ARG, "indexCount", "the output holds more elements than the kernels address");
+    const uint64_t per_outer = (uint64_t)p->IdxCount * p->Inner;
+    if (per_outer == 0 ? p->Count != 0 : p->Count % per_outer != 0)
+        return fail(ctx, OG_ERR_INVALID_ARG, "Count", "%u is not a multiple of IdxCount * Inner = %llu", p->Count, (unsigned long long)per_outer);
+    if (p->AxisLen > 0x7FFFFFFFu) return fail(ctx, OG_ERR_INVALID_ARG, "AxisLen", "the axis is longer than an index reaches");
+    const uint64_t outer = per_outer ? p->Count / per_outer : 0;
+    const bool wide = p->Flags & 1u;
+    const uint64_t eb = elem_bytes;
+    if (p->Count > 0) {
+        const uint64_t data_elems = outer * p->AxisLen * p->Inner;
+        if (data_elems > 0 && (!data.ptr || !fits((uint64_t)p->OffData * eb, data_elems * eb, data)))
+            return fail(ctx, OG_ERR_INVALID_ARG, "data", "elements %u..%llu reach past the buffer", p->OffData, (unsigned long long)(p->OffData + data_elems));
+        const uint64_t ib = wide ? 8 : 4;
+        if (!indices.ptr || ((uintptr_t)indices.ptr & 3) || !fits((uint64_t)p->OffIdx * ib, (uint64_t)p->IdxCount * ib, indices))
+            return fail(ctx, OG_ERR_INVALID_ARG, "indices", "elements %u..%llu reach past the buffer", p->OffIdx, (unsigned long long)p->OffIdx + p->IdxCount);
+        if (!out.ptr || !fits((uint64_t)p->OffOut * eb, (uint64_t)p->Count * eb, out))
+            return fail(ctx, OG_ERR_INVALID_ARG, "output", "elements %u..%llu reach past the buffer", p->OffOut, (unsigned long long)p->OffOut + p->Count);
+        if (status.ptr && (((uintptr_t)status.ptr & 3) || status.bytes < 4))
+            return fail(ctx, OG_ERR_INVALID_ARG, "status", "the status word is misaligned or too small");
+        // With an empty axis every index is invalid and the data is never read (it may be absent).
+    }
+    if (!ctx) return fail(ctx, OG_ERR_NO_DEVICE, "ctx", "no context: the arguments are valid but there is no device to run on");
+    if (p->Count == 0) return ok(ctx);
+    og::GatherArgs a{};
+    a.data = static_cast<const uint8_t *>(data.ptr) + (uint64_t)p->OffData * eb;
+    a.idx = static_cast<const uint8_t *>(indices.ptr) + (uint64_t)p->OffIdx * (wide ? 8 : 4);
+    a.out = static_cast<uint8_t *>(out.ptr) + (uint64_t)p->OffOut * eb;
+    a.status = static_cast<uint32_t *>(status.ptr);
+    a.rows = (int64_t)(outer * p->IdxCount);
+    a.count = p->IdxCount;
+    a.axis_len = p->AxisLen;
+    a.row_bytes = (int64_t)p->Inner * (int64_t)eb;
+    a.wide = wide;
+    (void)hipSetDevice(ctx->device);
+    int st = launch(ctx, "og_gather", [&](const char **k) { return og::launch_gather(a, ctx->stream, k); });
+    return st == OG_OK ? ok(ctx) : st;
+}
+
 // ------------------------------------------------------------------ DynamicQuantizeLinear
 
 int og_dynamic_quantize(og_ctx *ctx, const og_dq_params *p, og_buffer X, og_buffer Y, og_buffer scale, og_buffer zero)

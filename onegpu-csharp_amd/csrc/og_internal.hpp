@@ -107,6 +107,20 @@ struct DequantArgs {
 hipError_t launch_dequantize(const DequantArgs &d, int kind, bool f16_out, hipStream_t s, const char **kernel);
 hipError_t launch_quantize(const DequantArgs &d, bool is_signed, bool f16_in, hipStream_t s, const char **kernel);
 
+// ONNX Gather along one axis as a copy of byte rows: output row (o, i) of row_bytes bytes is data row
+// (o, index[i]); rows = outer * count. An invalid index gives a zero row and its position in *status (atomic minimum).
+struct GatherArgs {
+    const uint8_t *data;
+    const void *idx;
+    uint8_t *out;
+    uint32_t *status;   // nullptr: invalid indices only give zeros
+    int64_t rows, count;
+    uint32_t axis_len;
+    int64_t row_bytes;
+    bool wide;          // int64 indices
+};
+hipError_t launch_gather(const GatherArgs &a, hipStream_t s, const char **kernel);
+
 hipError_t launch_fill_bytes(void *dst, uint8_t value, uint64_t bytes, hipStream_t s);
 hipError_t launch_synth(int kind, uint64_t seed, uint32_t tensor, void *out, uint64_t count, double lo, double hi,
                         hipStream_t s);

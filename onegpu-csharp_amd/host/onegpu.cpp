@@ -835,4 +835,107 @@ void DequantizeKernels::EncodeQuantize(GpuCommandEncoder &encoder, const GpuBuff
         keep_of({&X, &S, &Z, &O}));
 }
 
+// ------------------------------------------------------------------ Gather
+
+GpuIndexStatus::GpuIndexStatus(std::shared_ptr<GpuDevice> device) : device_(std::move(device))
+{
+    if (!device_) throw std::invalid_argument("device");
+    buffer_ = device_->CreateBuffer(ElementType::UInt32, 1);
+    Reset();
+}
+
+void GpuIndexStatus::Reset()
+{
+    const uint32_t none = 0xFFFFFFFFu;
+    buffer_.Write(&none, 4);
+}
+
+void GpuIndexStatus::ThrowIfFailed()
+{
+    uint32_t word = 0;
+    device_->WaitIdle();
+    buffer_.Read(&word, 4);
+    if (word != 0xFFFFFFFFu) throw GpuKernelIndexException(operation_.empty() ? "index operation" : operation_, word);
+}
+
+GatherKernels::GatherKernels(std::shared_ptr<GpuDevice> device, int maxCachedBindGroups) : device_(std::move(device))
+{
+    if (!device_) throw std::invalid_argument("device");
+    if (maxCachedBindGroups < 1) throw std::out_of_range("maxCachedBindGroups");
+}
+
+// IndexSupport.Width (IndexSupport.cs:7-28): 0 halves, 1 four-byte values, 2 eight-byte values, 3 bytes.
+static int PayloadWidth(const std::string &operation, ElementType t)
+{
+    switch (t) {
+    case ElementType::UInt8:
+    case ElementType::Int8: return 3;
+    case ElementType::Float16: return 0;
+    case ElementType::Int64: return 2;
+    case ElementType::Float32:
+    case ElementType::Int32:
+    case ElementType::UInt32: return 1;
+    default: throw GpuKernelShapeException(operation, "T", std::string("element type ") + ElementName(t) + " is not supported here");
+    }
+}
+
+// GatherKernels.cs:66-118.
+void GatherKernels::EncodeGather(GpuCommandEncoder &encoder, const GpuBuffer &data, int offsetData,
+                                 const std::vector<int> &dataShape, int axis, const GpuBuffer &indices, int offsetIndices,
+                                 int indexCount, const GpuBuffer &output, int offsetOutput, GpuIndexStatus *status)
+{
+    const std::string Name = "Gather";
+    if (!data.Valid()) throw GpuKernelShapeException(Name, "data", "buffer is null");
+    if (!indices.Valid()) throw GpuKernelShapeException(Name, "indices", "buffer is null");
+    if (!output.Valid()) throw GpuKernelShapeException(Name, "output", "buffer is null");
+    const int width = PayloadWidth(Name, data.Type());
+    if (output.Type() != data.Type()) throw GpuKernelShapeException(Name, "output", "the output's element type differs from the data's");
+    if (indices.Type() != ElementType::Int32 && indices.Type() != ElementType::Int64)
+        throw GpuKernelShapeException(Name, "TIndex", std::string("index type ") + ElementName(indices.Type()) + " is not supported; use int or long");
+    const bool wide = indices.Type() == ElementType::Int64;
+    const int rank = (int)dataShape.size();
+    if (rank == 0) throw GpuKernelShapeException(Name, "dataShape", "a scalar has no axis to gather along");
+    if (axis < -rank || axis >= rank)
+        throw GpuKernelShapeException(Name, "axis", "axis " + std::to_string(axis) + " is outside [" + std::to_string(-rank) + ", " + std::to_string(rank) + ")");
+    const int ax = axis < 0 ? axis + rank : axis;
+    const int64_t dataCount = Check::Product(Name, "dataShape", dataShape);
+    if (indexCount < 0) throw GpuKernelShapeException(Name, "indexCount", "count " + std::to_string(indexCount) + " is negative");
+    int64_t outer = 1, inner = 1;
+    for (int i = 0; i < ax; i++) outer *= dataShape[i];
+    for (int i = ax + 1; i < rank; i++) inner *= dataShape[i];
+    const int64_t axisLength = dataShape[ax];
+    const int64_t total = outer * indexCount * inner;
+    if (total > Check::MaxElements)
+        throw GpuKernelShapeException(Name, "indexCount", "the output holds " + std::to_string(total) + " elements, more than the " + std::to_string(Check::MaxElements) + " the kernels address");
+    const int64_t elemWidth = width == 2 ? 2 : 1;
+    auto range = [&](const char *name, const GpuBuffer &b, int offset, int64_t extent) {
+        if (width == 3) Check::RangeBytes(Name, name, b.Length(), offset, extent);
+        else Check::Range(Name, name, b.Length(), offset, extent, width == 0);
+    };
+    range("data", data, offsetData, dataCount);
+    Check::Range(Name, "indices", indices.Length(), offsetIndices, indexCount);
+    range("output", output, offsetOutput, total);
+    const int64_t limit = 0xFFFFFFFFll / 2;   // GatherKernels.CheckAddressable (GatherKernels.cs:393-400)
+    if (dataCount * elemWidth > limit || total * elemWidth > limit || (int64_t)indexCount * (wide ? 2 : 1) > limit)
+        throw GpuKernelShapeException(Name, "shape", "a tensor is too large for 32-bit word addressing");
+    if (total == 0) return;
+    if (status) status->Note(Name);
+    og_gather_params w{};
+    w.Count = (uint32_t)total;
+    w.OffData = (uint32_t)offsetData;
+    w.OffOut = (uint32_t)offsetOutput;
+    w.OffIdx = (uint32_t)offsetIndices;
+    w.Flags = wide ? 1u : 0u;
+    w.Inner = (uint32_t)inner;
+    w.IdxCount = (uint32_t)indexCount;
+    w.AxisLen = (uint32_t)axisLength;
+    const uint32_t eb = (uint32_t)ElementSize(data.Type());
+    GpuBuffer D = data, I = indices, O = output, S = status ? status->Buffer() : GpuBuffer();
+    encoder.Record(
+        [w, eb, D, I, O, S](og_ctx *ctx) {
+            ThrowIfFailed(ctx, og_gather(ctx, eb, &w, bind(D), bind(I), bind(O), bind(S)), "Gather");
+        },
+        keep_of({&D, &I, &O, &S}));
+}
+
 }  // namespace onegpu

@@ -60,6 +60,17 @@ public:
     using GpuException::GpuException;
 };
 
+// An index given to a gather was outside its axis (GpuIndexStatus.cs:66-80).
+class GpuKernelIndexException : public GpuException {
+public:
+    GpuKernelIndexException(std::string operation, int64_t position)
+        : GpuException(operation + ": the index at position " + std::to_string(position) +
+                       " of the indices is outside its axis"),
+          Operation(std::move(operation)), Position(position) {}
+    std::string Operation;
+    int64_t Position;
+};
+
 // ------------------------------------------------------------------ device layer
 
 // The element types the path uses; the C# names are what its messages print (typeof(T).Name).
@@ -306,6 +317,41 @@ public:
                         int axis, bool perAxis, const GpuBuffer &scale, int offsetScale,
                         const std::optional<GpuBuffer> &zeroPoint, int offsetZeroPoint, const GpuBuffer &output,
                         int offsetOutput);
+    int BindGroupsCreated() const { return 0; }
+    void ReleaseBindings() {}
+    void Dispose() {}
+
+private:
+    std::shared_ptr<GpuDevice> device_;
+};
+
+// Where a gather records the position of an invalid index (GpuIndexStatus.cs:13-63): one uint32 on the device, reset to
+// "none" (0xFFFFFFFF) before the work and read back after it.
+class GpuIndexStatus {
+public:
+    explicit GpuIndexStatus(std::shared_ptr<GpuDevice> device);
+    void Reset();            // the write happens before the next submitted commands
+    void ThrowIfFailed();    // waits for the device, reads the word, throws GpuKernelIndexException
+    void Dispose() { buffer_.Dispose(); }
+    const GpuBuffer &Buffer() const { return buffer_; }
+    void Note(const std::string &operation) { operation_ = operation; }
+
+private:
+    std::shared_ptr<GpuDevice> device_;
+    GpuBuffer buffer_;
+    std::string operation_;
+};
+
+// The ONNX Gather of GatherKernels (GatherKernels.cs:22-118): EncodeGather over every payload type the reference
+// takes (uint8/int8, half, int32/uint32/float32, int64), int32 or int64 indices. GatherElements and GatherND are not
+// part of this library.
+class GatherKernels {
+public:
+    explicit GatherKernels(std::shared_ptr<GpuDevice> device, int maxCachedBindGroups = 1024);
+    // GatherKernels.cs:66-118: output[o, i, n] = data[o, indices[i], n] around `axis`.
+    void EncodeGather(GpuCommandEncoder &encoder, const GpuBuffer &data, int offsetData, const std::vector<int> &dataShape,
+                      int axis, const GpuBuffer &indices, int offsetIndices, int indexCount, const GpuBuffer &output,
+                      int offsetOutput, GpuIndexStatus *status = nullptr);
     int BindGroupsCreated() const { return 0; }
     void ReleaseBindings() {}
     void Dispose() {}

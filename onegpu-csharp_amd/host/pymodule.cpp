@@ -80,6 +80,7 @@ PYBIND11_MODULE(_onegpu_host, m)
     static py::handle LostErr = py::object(errors.attr("GpuDeviceLostException")).release();
     static py::handle CmdErr = py::object(errors.attr("GpuCommandFailedException")).release();
     static py::handle BaseErr = py::object(errors.attr("GpuException")).release();
+    static py::handle IndexErr = py::object(errors.attr("GpuKernelIndexException")).release();
     py::register_exception_translator([](std::exception_ptr p) {
         try {
             if (p) std::rethrow_exception(p);
@@ -93,6 +94,9 @@ PYBIND11_MODULE(_onegpu_host, m)
             PyErr_SetString(OomErr.ptr(), e.what());
         } catch (const GpuDeviceLostException &e) {
             PyErr_SetString(LostErr.ptr(), e.what());
+        } catch (const GpuKernelIndexException &e) {
+            py::object ex = IndexErr(e.Operation, e.Position);
+            PyErr_SetObject(IndexErr.ptr(), ex.ptr());
         } catch (const GpuCommandFailedException &e) {
             PyErr_SetString(CmdErr.ptr(), e.what());
         } catch (const GpuException &e) {
@@ -241,6 +245,25 @@ PYBIND11_MODULE(_onegpu_host, m)
         .def("Dispose", &DynamicQuantizeKernels::Dispose)
         .def("__enter__", [](DynamicQuantizeKernels &g) -> DynamicQuantizeKernels & { return g; })
         .def("__exit__", [](DynamicQuantizeKernels &g, py::args) { g.Dispose(); });
+
+    py::class_<GpuIndexStatus>(m, "GpuIndexStatus")
+        .def(py::init<std::shared_ptr<GpuDevice>>(), py::arg("device"))
+        .def("Reset", &GpuIndexStatus::Reset)
+        .def("ThrowIfFailed", &GpuIndexStatus::ThrowIfFailed)
+        .def("Dispose", &GpuIndexStatus::Dispose)
+        .def("__enter__", [](GpuIndexStatus &g) -> GpuIndexStatus & { return g; })
+        .def("__exit__", [](GpuIndexStatus &g, py::args) { g.Dispose(); });
+
+    py::class_<GatherKernels>(m, "GatherKernels")
+        .def(py::init<std::shared_ptr<GpuDevice>, int>(), py::arg("device"), py::arg("maxCachedBindGroups") = 1024)
+        .def("EncodeGather", &GatherKernels::EncodeGather, py::arg("encoder"), py::arg("data"), py::arg("offsetData"),
+             py::arg("dataShape"), py::arg("axis"), py::arg("indices"), py::arg("offsetIndices"), py::arg("indexCount"),
+             py::arg("output"), py::arg("offsetOutput"), py::arg("status") = nullptr)
+        .def_property_readonly("BindGroupsCreated", &GatherKernels::BindGroupsCreated)
+        .def("ReleaseBindings", &GatherKernels::ReleaseBindings)
+        .def("Dispose", &GatherKernels::Dispose)
+        .def("__enter__", [](GatherKernels &g) -> GatherKernels & { return g; })
+        .def("__exit__", [](GatherKernels &g, py::args) { g.Dispose(); });
 
     py::class_<DequantizeKernels>(m, "DequantizeKernels")
         .def(py::init<std::shared_ptr<GpuDevice>, int>(), py::arg("device"), py::arg("maxCachedBindGroups") = 1024)

@@ -5,13 +5,13 @@ The compute runs only in the HIP library; importing fails loudly when the built 
 """
 import os
 
-from .errors import (GpuCommandFailedException, GpuDeviceLostException, GpuException, GpuKernelShapeException,
-                     GpuOutOfMemoryException, GpuUnsupportedException)
+from .errors import (GpuCommandFailedException, GpuDeviceLostException, GpuException, GpuKernelIndexException,
+                     GpuKernelShapeException, GpuOutOfMemoryException, GpuUnsupportedException)
 
 try:
-    from ._onegpu_host import (DequantizeKernels, DynamicQuantizeKernels, ElementType, GpuBuffer, GpuCommandEncoder,
-                               GpuComputeCapabilities, GpuDevice, Int8Gemm, Int8GemmOptions, Int8GemmProblem,
-                               Int8Operand, Int8Scratch, version)
+    from ._onegpu_host import (DequantizeKernels, DynamicQuantizeKernels, ElementType, GatherKernels, GpuBuffer,
+                               GpuCommandEncoder, GpuComputeCapabilities, GpuDevice, GpuIndexStatus, Int8Gemm,
+                               Int8GemmOptions, Int8GemmProblem, Int8Operand, Int8Scratch, version)
 except ImportError as e:  # pragma: no cover - a build problem, reported as such
     raise ImportError("onegpu_hip: the native extension is not built; run python onegpu-csharp_amd/build.py "
                       f"(or __graft_entry__.build()) first: {e}") from e
@@ -33,7 +33,8 @@ def padded_half_length(count: int) -> int:
     return (count + 1) & ~1
 
 
-__all__ = ["DequantizeKernels", "DynamicQuantizeKernels", "ElementType", "GpuBuffer", "GpuCommandEncoder",
+__all__ = ["DequantizeKernels", "DynamicQuantizeKernels", "ElementType", "GatherKernels", "GpuIndexStatus",
+           "GpuKernelIndexException", "GpuBuffer", "GpuCommandEncoder",
            "GpuComputeCapabilities", "GpuDevice", "Int8Gemm", "Int8GemmOptions", "Int8GemmProblem", "Int8Operand",
            "Int8Scratch", "GpuException", "GpuKernelShapeException", "GpuUnsupportedException", "GpuOutOfMemoryException",
            "GpuDeviceLostException", "GpuCommandFailedException", "padded_bool_length", "padded_half_length", "LIB_PATH",

@@ -33,3 +33,12 @@ class GpuDeviceLostException(GpuException):
 
 class GpuCommandFailedException(GpuException):
     pass
+
+
+class GpuKernelIndexException(GpuException):
+    """An index given to a gather was outside its axis (GpuIndexStatus.cs:66-80)."""
+
+    def __init__(self, operation: str, position: int):
+        super().__init__(f"{operation}: the index at position {position} of the indices is outside its axis")
+        self.Operation = operation
+        self.Position = position

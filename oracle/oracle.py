@@ -4,7 +4,7 @@ Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this
 the product (the HIP library and its host layer) never loads it.
 
 Each wrapper keeps the name and argument meaning of the C function it calls; oracle.c cites the reference file:line
-each one restates.
+each one restates. The gather (byte and element copies, no arithmetic) is restated here in numpy.
 """
 from __future__ import annotations
 
@@ -295,3 +295,30 @@ def quantize(x, scale, is_signed, per_axis=False, axis_len=1, inner=1, zero=None
     lib().ora_quantize(_ptr(x), x.size, int(per_axis), axis_len, inner, _ptr(scale), _ptr(zero), int(is_signed),
                        _ptr(out))
     return out
+
+
+# ------------------------------------------------------------------ gather
+
+def gather(data, shape, axis, indices, wide=False):
+    """ONNX Gather along one axis as Gather.hlsl:25-43 with IndexCommon.hlsli:12-43 computes it and GatherTests.cs:8-68
+    checks it. The data (any element dtype, dense row-major) is [outer, axisLen, inner] around `axis`;
+    out[o, i, n] = data[o, idx[i], n], a negative index counting from the end of the axis. An index outside
+    [-axisLen, axisLen), or, with int64 indices (`wide`), one that does not fit an int32, reads nothing: its output
+    elements are zero. Returns (the flat output [outer * count * inner], the smallest invalid position or None)."""
+    shape = [int(x) for x in shape]
+    rank = len(shape)
+    ax = axis + rank if axis < 0 else axis
+    outer = int(np.prod(shape[:ax], dtype=np.int64))
+    inner = int(np.prod(shape[ax + 1:], dtype=np.int64))
+    n_axis = shape[ax]
+    v = np.asarray(indices).astype(np.int64).ravel()
+    valid = (v >= -n_axis) & (v < n_axis)
+    if wide:
+        valid &= (v >= -(1 << 31)) & (v < (1 << 31))
+    norm = np.where(v < 0, v + n_axis, v)
+    d3 = np.asarray(data).reshape(outer, n_axis, inner)
+    out = np.zeros((outer, v.size, inner), d3.dtype)
+    if valid.any():
+        out[:, valid, :] = d3[:, norm[valid], :]
+    bad = np.flatnonzero(~valid)
+    return out.reshape(-1), (int(bad[0]) if bad.size else None)

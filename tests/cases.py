@@ -184,3 +184,49 @@ def requant_case_data(m, n, k, mult_vec, seed):
     cols = np.arange(n)
     ib = (((cols * 6007) % 4001) - 2000).astype(np.int32)
     return a, b, za, mult, ib
+
+
+# ------------------------------------------------------------------ gather (GatherTests.cs, IndexRig.cs)
+
+# GatherIsExact's shapes (GatherTests.cs:78-82): (data shape, axis, index count).
+GATHER_CASES = [([10], 0, 7), ([10], -1, 1), ([5, 6], 0, 9), ([5, 6], 1, 4), ([5, 6], -1, 11), ([2, 3, 4, 5], 2, 6),
+                ([2, 3, 4, 5], -4, 3), ([1, 7], 1, 5), ([4, 1, 9], 0, 8), ([3, 257], 1, 300), ([1031, 3], 0, 1500),
+                ([2, 3, 4, 5, 6], 3, 2)]
+
+_M32 = 0xFFFFFFFF
+
+
+def index_rig_make(dtype, i: np.ndarray) -> np.ndarray:
+    """IndexRig.Make<T>(i) (IndexRig.cs:17-57): a hashed payload of every bit pattern (finite floats and halves)."""
+    i = np.asarray(i, np.int64)
+    h = ((i.astype(np.uint64) * np.uint64(2654435761) + np.uint64(0x9E3779B9)) & np.uint64(_M32))
+    h ^= h >> np.uint64(15)
+    h = (h * np.uint64(0x85EBCA6B)) & np.uint64(_M32)
+    h ^= h >> np.uint64(13)
+    dt = np.dtype(dtype)
+    if dt == np.float32:
+        return (((h & np.uint64(0xFFFFF)).astype(np.int64) - 0x80000).astype(np.float32) / np.float32(1024)).astype(np.float32)
+    if dt == np.float16:
+        return (((h & np.uint64(0xFFF)).astype(np.int64) - 0x800).astype(np.float32) / np.float32(16)).astype(np.float16)
+    if dt in (np.int32, np.uint32):
+        return h.astype(np.uint32).view(np.int32).astype(dt) if dt == np.int32 else h.astype(np.uint32)
+    if dt in (np.uint8, np.int8):
+        return (h >> np.uint64(8)).astype(np.uint8).view(dt)
+    if dt == np.int64:
+        lo = ((i * 40503 + 17) & _M32).astype(np.uint64)
+        return ((h << np.uint64(32)) ^ lo).view(np.int64)
+    raise ValueError(dt)
+
+
+def index_rig_fill(dtype, length: int, seed: int) -> np.ndarray:
+    """IndexRig.Fill<T> (IndexRig.cs:62-72), without the padding (the tests pad their buffers themselves)."""
+    return index_rig_make(dtype, np.arange(length) + seed * 7919)
+
+
+def index_rig_random_index(i, n_axis: int, seed: int) -> np.ndarray:
+    """IndexRig.RandomIndex (IndexRig.cs:109-117): deterministic indices in [-len, len), some negative."""
+    i = np.asarray(i, np.int64)
+    h = (((i + seed * 104729) & _M32).astype(np.uint64) * np.uint64(2246822519)) & np.uint64(_M32)
+    h ^= h >> np.uint64(13)
+    h = (h * np.uint64(3266489917)) & np.uint64(_M32)
+    return (h % np.uint64(2 * n_axis)).astype(np.int64) - n_axis

@@ -158,6 +158,36 @@ def test_quantize_bad_arguments(d):
     shape_error(lambda: k.EncodeQuantize(enc, xi, 0, [4], 0, False, s, 0, None, 0, o, 0), "T")
 
 
+def test_gather_bad_arguments_are_rejected(d):
+    # GatherTests.cs:228-258: the rejections EncodeGather makes before recording, with the argument each names.
+    k = og.GatherKernels(d)
+    data, idx = buf(d, og.ElementType.Float32, 12), buf(d, og.ElementType.Int32, 4)
+    outp = buf(d, og.ElementType.Float32, 12)
+    enc = d.BeginCommands()
+    k.EncodeGather(enc, data, 0, [3, 4], 0, idx, 0, 0, outp, 0)       # no indices: nothing to record
+    k.EncodeGather(enc, data, 0, [0, 4], 0, idx, 0, 2, outp, 0)       # an empty axis: valid, every index fails
+    assert enc.DispatchCount == 1
+    shape_error(lambda: k.EncodeGather(enc, data, 0, [3, 4], 2, idx, 0, 2, outp, 0), "axis")
+    shape_error(lambda: k.EncodeGather(enc, data, 0, [3, 4], 0, idx, 3, 2, outp, 0), "indices")
+    shape_error(lambda: k.EncodeGather(enc, data, 0, [3, 4], 0, idx, 0, 4, outp, 1), "output")
+    shape_error(lambda: k.EncodeGather(enc, data, 0, [3, 4], 0, idx, 0, -1, outp, 0), "indexCount")
+    shape_error(lambda: k.EncodeGather(enc, data, 0, [], 0, idx, 0, 1, outp, 0), "dataShape")
+    shape_error(lambda: k.EncodeGather(enc, data, 0, [3, 5], 0, idx, 0, 1, outp, 0), "data")
+    shape_error(lambda: k.EncodeGather(enc, data, 0, [2147483647, 2], 0, idx, 0, 1, outp, 0))
+    shorts = buf(d, og.ElementType.UInt16, 16)
+    shape_error(lambda: k.EncodeGather(enc, shorts, 0, [16], 0, idx, 0, 1, shorts, 0), "T")
+    # Byte payloads are packed four to a word: a buffer that ends inside a word is refused.
+    b18, b20 = buf(d, og.ElementType.UInt8, 18), buf(d, og.ElementType.UInt8, 20)
+    assert b18.Size == 20   # CreateBuffer pads bytes to a whole word, but the element count is what is checked
+    shape_error(lambda: k.EncodeGather(enc, b18, 0, [1, 18], 0, idx, 0, 1, b20, 0), "data")
+    shape_error(lambda: k.EncodeGather(enc, b20, 0, [1, 18], 0, idx, 0, 1, b18, 0), "output")
+    floats = buf(d, og.ElementType.Float32, 4)
+    shape_error(lambda: k.EncodeGather(enc, data, 0, [3, 4], 0, floats, 0, 1, outp, 0), "TIndex")
+    i8 = buf(d, og.ElementType.Int8, 20)
+    shape_error(lambda: k.EncodeGather(enc, b20, 0, [20], 0, idx, 0, 1, i8, 0), "output")   # element types differ
+    assert enc.DispatchCount == 1
+
+
 # ------------------------------------------------------------------ the C ABI
 
 
@@ -260,6 +290,38 @@ def test_abi_validates_before_touching_a_device():
     assert fs(pf, act=8, act_off=2) == (1, "activationScale")
     assert fs(pf, act=8, act_off=1) == (6, "ctx")
     assert fs(pf, scale=Buf(addr, 12)) == (1, "scale")
+
+
+class GatherParams(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in ("Count", "OffData", "OffOut", "OffIdx", "GridX", "Flags", "Inner",
+                                               "IdxCount", "AxisLen")]
+
+
+def test_gather_abi_validates_before_touching_a_device():
+    lib = ctypes.CDLL(og.LIB_PATH)
+    lib.og_gather.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.POINTER(GatherParams), Buf, Buf, Buf, Buf]
+    lib.og_last_error_argument.restype = ctypes.c_char_p
+    lib.og_last_error_argument.argtypes = [ctypes.c_void_p]
+    host = (ctypes.c_uint8 * 4096)()
+    addr = ctypes.addressof(host)
+
+    def call(p, eb=1, data=64, idx=64, out=64, status=Buf(None, 0)):
+        st = lib.og_gather(None, eb, ctypes.byref(p), Buf(addr, data), Buf(addr, idx), Buf(addr, out), status)
+        return st, lib.og_last_error_argument(None).decode()
+
+    # data [2, 8, 3] bytes gathered on axis 1 with 4 int32 indices: output [2, 4, 3] = 24 bytes.
+    p = GatherParams(Count=24, Inner=3, IdxCount=4, AxisLen=8)
+    assert call(p) == (6, "ctx")
+    assert call(p, data=47) == (1, "data")          # 2 * 8 * 3 = 48 bytes
+    assert call(p, idx=15) == (1, "indices")
+    assert call(p, out=23) == (1, "output")
+    assert call(p, eb=4, data=192, out=95) == (1, "output")
+    assert call(p, eb=3) == (1, "T")
+    assert call(GatherParams(Count=25, Inner=3, IdxCount=4, AxisLen=8)) == (1, "Count")
+    assert call(GatherParams(Count=24, Inner=3, IdxCount=4, AxisLen=8, Flags=1), idx=31) == (1, "indices")
+    assert call(GatherParams(Count=24, Inner=3, IdxCount=4, AxisLen=8, Flags=2)) == (1, "Flags")
+    assert call(p, status=Buf(addr + 1, 4)) == (1, "status")
+    assert call(GatherParams(Count=0, Inner=3, IdxCount=0, AxisLen=8), data=0, idx=0, out=0) == (6, "ctx")
 
 
 def test_kernel_choice_is_reported():

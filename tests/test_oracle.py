@@ -287,3 +287,57 @@ def test_generators_are_deterministic_and_in_range():
     assert u.min() == 100 and u.max() == 156
     g = oracle.synth_normal_f32(200000, 1, 0, 0.0, 1.0)
     assert abs(float(g.mean())) < 0.01 and abs(float(g.std()) - 1.0) < 0.01
+
+
+# ------------------------------------------------------------------ gather
+
+def _gather_loops(data, shape, axis, idx, wide):
+    """The index map GatherTests.cs:45-57 walks, in plain loops (tiny shapes only)."""
+    rank = len(shape)
+    ax = axis + rank if axis < 0 else axis
+    outer = int(np.prod(shape[:ax])) if ax else 1
+    inner = int(np.prod(shape[ax + 1:])) if ax + 1 < rank else 1
+    n_axis = shape[ax]
+    out, bad = [], None
+    for o in range(outer):
+        for i, v in enumerate(idx):
+            ok = -n_axis <= v < n_axis and (not wide or -(1 << 31) <= v < (1 << 31))
+            if not ok and bad is None:
+                bad = i
+            for m in range(inner):
+                out.append(data[(o * n_axis + (v + n_axis if v < 0 else v)) * inner + m] if ok else 0)
+    return np.array(out, dtype=np.asarray(data).dtype), bad
+
+
+def test_gather_onnx_examples():
+    # The two examples of the ONNX Gather operator's specification (axis 0 and axis 1).
+    d0 = np.array([[1.0, 1.2], [2.3, 3.4], [4.5, 5.7]], np.float32)
+    out, bad = oracle.gather(d0, d0.shape, 0, [0, 1, 1, 2])
+    assert bad is None and out.reshape(2, 2, 2).tolist() == np.array(
+        [[[1.0, 1.2], [2.3, 3.4]], [[2.3, 3.4], [4.5, 5.7]]], np.float32).tolist()
+    d1 = np.array([[1.0, 1.2, 1.9], [2.3, 3.4, 3.9], [4.5, 5.7, 5.9]], np.float32)
+    out, bad = oracle.gather(d1, d1.shape, 1, [0, 2])
+    assert bad is None and out.reshape(3, 1, 2).tolist() == np.array(
+        [[[1.0, 1.9]], [[2.3, 3.9]], [[4.5, 5.9]]], np.float32).tolist()
+
+
+def test_gather_against_loops_and_numpy_take():
+    rng = np.random.default_rng(5)
+    for shape, axis in (([10], 0), ([5, 6], 1), ([5, 6], -1), ([2, 3, 4, 5], 2), ([4, 1, 9], 0), ([3, 0, 2], 1)):
+        data = rng.integers(-128, 128, int(np.prod(shape)), dtype=np.int8)
+        n_axis = shape[axis]
+        for wide in (False, True):
+            idx = [int(x) for x in rng.integers(-2 * n_axis - 1, 2 * n_axis + 2, 7)]
+            if wide:
+                idx += [(1 << 31) + 1, -(1 << 31) - 3]
+            got, bad = oracle.gather(data, shape, axis, idx, wide)
+            want, want_bad = _gather_loops(data, shape, axis, idx, wide)
+            assert np.array_equal(got, want) and bad == want_bad, (shape, axis, idx)
+            ok = [v for v in idx if -n_axis <= v < n_axis]
+            if ok:   # valid indices only: numpy's take along the axis
+                got, bad = oracle.gather(data, shape, axis, ok, wide)
+                assert bad is None
+                assert np.array_equal(got, np.take(data.reshape(shape), ok, axis=axis).ravel())
+    # A plausible slip (a negative index taken modulo the axis twice, or positions counted from 1) changes these.
+    out, bad = oracle.gather(np.arange(4, dtype=np.uint8), [4], 0, [-1, -4, 4, 0, -5])
+    assert out.tolist() == [3, 0, 0, 0, 0] and bad == 2
