@@ -226,6 +226,42 @@ int og_dequantize(og_ctx *ctx, int kind, int f16_out, const og_dequant_params *p
 int og_quantize(og_ctx *ctx, int is_signed, int f16_in, const og_dequant_params *params, og_buffer X, og_buffer scale,
                 og_buffer zero, og_buffer out);
 
+/* ------------------------------------------------------------------ ConvInteger */
+
+/* ConvProblem's fields (src/RecursiveAI.OneGpu.Kernels/ConvProblem.cs:107-235) and the operands' types: NCHW input,
+ * OIHW weights, strides, dilations, asymmetric padding, groups. Offsets count elements (bytes of x and w, int32 of y);
+ * the output extent is floor((in + padBegin + padEnd - dilation * (kernel - 1) - 1) / stride) + 1 per axis. */
+typedef struct og_conv_params {
+    uint32_t Batch, InChannels, Height, Width, OutChannels, KernelHeight, KernelWidth;
+    uint32_t StrideHeight, StrideWidth, DilationHeight, DilationWidth;
+    uint32_t PadTop, PadLeft, PadBottom, PadRight, Groups;
+    uint32_t OffsetX, OffsetW, OffsetY;
+    uint32_t Flags;       /* OG_CONV_* */
+    uint32_t OffXZero;    /* element offset of x's zero point (one value) */
+    uint32_t OffWZero;    /* element offset of w's zero point (one value, or one per output channel) */
+    uint32_t GemmFlags;   /* OG_GEMM_PORTABLE / NO_SKINNY / NO_DIRECT / LARGE_TILE / NO_STREAM for the products */
+} og_conv_params;
+
+#define OG_CONV_X_INT8          0x1u  /* x is int8 (else uint8) */
+#define OG_CONV_W_INT8          0x2u  /* w is int8 (else uint8) */
+#define OG_CONV_XZ              0x4u  /* x has a zero point */
+#define OG_CONV_WZ              0x8u  /* w has a zero point */
+#define OG_CONV_WZ_PER_CHANNEL  0x10u /* ... one per output channel */
+#define OG_CONV_NO_DEPTHWISE    0x20u /* convolutions with one input channel a group through the column matrix too */
+
+/* Bytes of column scratch one image needs: Groups * K * ldb with K = InChannels / Groups * KernelHeight * KernelWidth
+ * and ldb = OutHeight * OutWidth rounded up to 16 (ConvIntegerKernels.ScratchBytesPerImage, ConvIntegerKernels.cs:78-89,
+ * which rounds to 4). 0 when the geometry is invalid. */
+uint64_t og_conv_integer_scratch_bytes(const og_conv_params *params);
+
+/* ONNX ConvInteger: y[n, m, oh, ow] = sum over c, kh, kw of (x - xz) * (w - wz[m]) in 32-bit wrap-around; taps in the
+ * padding add nothing. Replaces ConvIntegerKernels.Encode's dispatches (ConvIntegerKernels.cs:97-253): per chunk of
+ * images that fits the scratch (bytes from scratch_offset, a multiple of 4), the column matrix is packed and then
+ * multiplied, one batched product per group (the reference records one product per image and group). With one input
+ * channel a group (depthwise) the library convolves directly and the scratch is not used (may be absent). */
+int og_conv_integer(og_ctx *ctx, const og_conv_params *params, og_buffer x, og_buffer w, og_buffer y, og_buffer xz,
+                    og_buffer wz, og_buffer scratch, uint64_t scratch_offset);
+
 /* ------------------------------------------------------------------ Gather (the int8 embedding lookup) */
 
 /* GatherParams, 9 words (src/RecursiveAI.OneGpu.Kernels/Shaders/Gather.hlsl:6-17). The data tensor is seen as

@@ -4,6 +4,7 @@
 // skipped them still cannot make a kernel read or write outside its buffers.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -434,6 +435,8 @@ int og_int8_gemm_kernel_name(const og_int8_gemm_params *p, uint32_t batch, char 
     g.strideA = p->StrideA;
     g.strideB = p->StrideB;
     g.flags = p->Flags;
+    // B as og_alloc leaves it: padded to a whole 32-bit word.
+    g.b_bytes = (int64_t)(b - 1) * g.strideB + (int64_t)(g.K > 0 ? g.K - 1 : 0) * g.ldb + ((cols_b + 3) & ~3u);
     // The tiled family's name also says the kernel and tile (the same choice as launch_gemm_tiled).
     if (k == og::GemmKernel::Tiled) {
         const bool large = (p->Flags & OG_GEMM_LARGE_TILE) || og::tiled_uses_large(g.M, g.N, b);
@@ -447,6 +450,49 @@ int og_int8_gemm_kernel_name(const og_int8_gemm_params *p, uint32_t batch, char 
         name = og::gemm_kernel_name(og::GemmKernel::RowTiles);
     snprintf(buf, len, "%s", name);
     return OG_OK;
+}
+
+// Chooses the kernel for a validated product and launches it (two launches for the split few-rows forms), on ctx's
+// stream with its device current. og_int8_gemm and the convolution's products come through here.
+static int launch_product(og_ctx *ctx, const og::GemmArgs &g)
+{
+    int st = OG_OK;
+    og::GemmKernel k = og::choose_gemm_kernel(g.M, g.N, g.K, g.batch, g.flags);
+    if ((k == og::GemmKernel::Skinny || k == og::GemmKernel::SkinnyDirect) && !(g.flags & OG_GEMM_NO_STREAM) &&
+        og::gemv_tiles_ok(g))
+        k = og::GemmKernel::RowTiles;
+    switch (k) {
+    case og::GemmKernel::Portable:
+        st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_portable(g, ctx->stream, n); });
+        break;
+    case og::GemmKernel::Tiled:
+        st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_tiled(g, ctx->stream, n); });
+        break;
+    case og::GemmKernel::RowTiles:
+        st = ensure_partials(ctx, og::gemv_tiles_workspace_bytes(g));
+        if (st != OG_OK) return st;
+        st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemv_tiles(g, ctx->ws, ctx->stream, n, 0); });
+        if (st == OG_OK) {
+            const char *product = ctx->last_kernel;   // the product is named for its tile kernel, not the summing pass
+            st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemv_tiles(g, ctx->ws, ctx->stream, n, 1); });
+            ctx->last_kernel = product;
+        }
+        break;
+    case og::GemmKernel::SkinnyDirect:
+        st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_skinny(g, ctx->ws, ctx->stream, n, 0); });
+        break;
+    case og::GemmKernel::Skinny:
+        st = ensure_partials(ctx, og::skinny_workspace_bytes(g.M, g.N, g.K, g.batch));
+        if (st != OG_OK) return st;
+        st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_skinny(g, ctx->ws, ctx->stream, n, 0); });
+        if (st == OG_OK) {
+            const char *product = ctx->last_kernel;   // named for the split-k kernel, not the reduction pass
+            st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_skinny(g, ctx->ws, ctx->stream, n, 1); });
+            ctx->last_kernel = product;
+        }
+        break;
+    }
+    return st;
 }
 
 // The output side of a requantized product (og_int8_gemm_requantized); absent for og_int8_gemm.
@@ -543,6 +589,7 @@ static int run_gemm(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, o
     g.strideA = p->StrideA;
     g.strideB = p->StrideB;
     g.strideC = (int64_t)stride_c;
+    g.b_bytes = B.ptr && B.bytes > p->OffB ? (int64_t)(B.bytes - p->OffB) : 0;
     g.M = (int32_t)M;
     g.N = (int32_t)N;
     g.K = (int32_t)K;
@@ -556,41 +603,7 @@ static int run_gemm(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, o
     g.zp_y = rq ? rq->zero_point : 0;
 
     (void)hipSetDevice(ctx->device);
-    og::GemmKernel k = og::choose_gemm_kernel(g.M, g.N, g.K, g.batch, g.flags);
-    if ((k == og::GemmKernel::Skinny || k == og::GemmKernel::SkinnyDirect) && !(g.flags & OG_GEMM_NO_STREAM) &&
-        og::gemv_tiles_ok(g))
-        k = og::GemmKernel::RowTiles;
-    switch (k) {
-    case og::GemmKernel::Portable:
-        st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_portable(g, ctx->stream, n); });
-        break;
-    case og::GemmKernel::Tiled:
-        st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_tiled(g, ctx->stream, n); });
-        break;
-    case og::GemmKernel::RowTiles:
-        st = ensure_partials(ctx, og::gemv_tiles_workspace_bytes(g));
-        if (st != OG_OK) return st;
-        st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemv_tiles(g, ctx->ws, ctx->stream, n, 0); });
-        if (st == OG_OK) {
-            const char *product = ctx->last_kernel;   // the product is named for its tile kernel, not the summing pass
-            st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemv_tiles(g, ctx->ws, ctx->stream, n, 1); });
-            ctx->last_kernel = product;
-        }
-        break;
-    case og::GemmKernel::SkinnyDirect:
-        st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_skinny(g, ctx->ws, ctx->stream, n, 0); });
-        break;
-    case og::GemmKernel::Skinny:
-        st = ensure_partials(ctx, og::skinny_workspace_bytes(g.M, g.N, g.K, g.batch));
-        if (st != OG_OK) return st;
-        st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_skinny(g, ctx->ws, ctx->stream, n, 0); });
-        if (st == OG_OK) {
-            const char *product = ctx->last_kernel;   // named for the split-k kernel, not the reduction pass
-            st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_skinny(g, ctx->ws, ctx->stream, n, 1); });
-            ctx->last_kernel = product;
-        }
-        break;
-    }
+    st = launch_product(ctx, g);
     return st == OG_OK ? ok(ctx) : st;
 }
 
@@ -653,6 +666,192 @@ int og_int8_epilogue(og_ctx *ctx, const og_int8_epilogue_params *p, og_buffer ac
     e.out_byte_offset = byte_out ? p->OffOut : 0;
     (void)hipSetDevice(ctx->device);
     int st = launch(ctx, "og_int8_epilogue", [&](const char **k) { return og::launch_int8_epilogue(e, ctx->stream, k); });
+    return st == OG_OK ? ok(ctx) : st;
+}
+
+// ------------------------------------------------------------------ ConvInteger
+
+namespace {
+
+// The geometry of a convolution after ConvKernels.CheckConv (ConvKernels.cs:895-956) and ConvIntegerKernels.Geometry
+// (ConvIntegerKernels.cs:296-318); `arg` names what failed.
+struct ConvGeometry {
+    int64_t oh, ow, cin_g, cout_g, k, ldb, per_image, x_image, y_image;
+    const char *arg;
+    const char *msg;
+};
+
+int64_t conv_extent(int64_t in, int64_t kernel, int64_t stride, int64_t dilation, int64_t pb, int64_t pe)
+{
+    const int64_t span = in + pb + pe - (dilation * (kernel - 1) + 1);
+    return span < 0 ? 0 : span / stride + 1;
+}
+
+bool conv_geometry(const og_conv_params *p, ConvGeometry &g)
+{
+    const int64_t imax = 0x7FFFFFFF;
+    g.arg = nullptr;
+    auto bad = [&](const char *arg, const char *msg) { g.arg = arg; g.msg = msg; return false; };
+    if (p->Batch < 1 || p->Batch > imax) return bad("Batch", "batch must be at least 1");
+    if (p->InChannels < 1 || p->InChannels > imax) return bad("InChannels", "channel counts must be at least 1");
+    if (p->OutChannels < 1 || p->OutChannels > imax) return bad("OutChannels", "channel counts must be at least 1");
+    if (p->Groups < 1 || p->Groups > imax || p->InChannels % p->Groups || p->OutChannels % p->Groups)
+        return bad("Groups", "the groups do not divide the input and output channels");
+    const uint32_t in[2] = {p->Height, p->Width}, ker[2] = {p->KernelHeight, p->KernelWidth};
+    const uint32_t str[2] = {p->StrideHeight, p->StrideWidth}, dil[2] = {p->DilationHeight, p->DilationWidth};
+    const uint32_t pb[2] = {p->PadTop, p->PadLeft}, pe[2] = {p->PadBottom, p->PadRight};
+    int64_t out[2];
+    for (int a = 0; a < 2; a++) {
+        const char *axis = a ? "width" : "height";
+        if (in[a] < 1 || in[a] > imax) return bad(axis, "the input extent must be at least 1");
+        if (ker[a] < 1 || ker[a] > imax) return bad(axis, "the kernel extent must be at least 1");
+        if (str[a] < 1 || str[a] > imax) return bad(axis, "the stride must be at least 1");
+        if (dil[a] < 1 || dil[a] > imax) return bad(axis, "the dilation must be at least 1");
+        if (pb[a] > imax || pe[a] > imax) return bad(axis, "the padding must not be negative");
+        if ((int64_t)ker[a] * dil[a] > imax || (int64_t)pb[a] + pe[a] + in[a] > imax)
+            return bad(axis, "the window or padding is larger than the supported sizes");
+        out[a] = conv_extent(in[a], ker[a], str[a], dil[a], pb[a], pe[a]);
+        if (out[a] < 1) return bad(axis, "the kernel does not fit the padded input");
+    }
+    g.oh = out[0];
+    g.ow = out[1];
+    g.cin_g = p->InChannels / p->Groups;
+    g.cout_g = p->OutChannels / p->Groups;
+    g.k = g.cin_g * p->KernelHeight * p->KernelWidth;
+    g.ldb = (g.oh * g.ow + 15) / 16 * 16;
+    g.x_image = (int64_t)p->InChannels * p->Height * p->Width;
+    g.y_image = (int64_t)p->OutChannels * g.oh * g.ow;
+    if (g.k > imax || g.ldb > imax || g.x_image * p->Batch > imax) return bad("shape", "the convolution is larger than the supported sizes");
+    g.per_image = (int64_t)p->Groups * g.k * g.ldb;
+    if (g.per_image > imax) return bad("InChannels", "the column matrix of one image is larger than the supported sizes");
+    return true;
+}
+
+}  // namespace
+
+uint64_t og_conv_integer_scratch_bytes(const og_conv_params *p)
+{
+    ConvGeometry g;
+    return p && conv_geometry(p, g) ? (uint64_t)g.per_image : 0;
+}
+
+int og_conv_integer(og_ctx *ctx, const og_conv_params *p, og_buffer x, og_buffer w, og_buffer y, og_buffer xz,
+                    og_buffer wz, og_buffer scratch, uint64_t scratch_offset)
+{
+    if (!p) return fail(ctx, OG_ERR_INVALID_ARG, "params", "null parameter block");
+    ConvGeometry geo;
+    if (!conv_geometry(p, geo)) return fail(ctx, OG_ERR_INVALID_ARG, geo.arg, "%s", geo.msg);
+    const uint32_t known = OG_CONV_X_INT8 | OG_CONV_W_INT8 | OG_CONV_XZ | OG_CONV_WZ | OG_CONV_WZ_PER_CHANNEL | OG_CONV_NO_DEPTHWISE;
+    if (p->Flags & ~known) return fail(ctx, OG_ERR_INVALID_ARG, "Flags", "unknown flag bits 0x%x", p->Flags & ~known);
+    const uint32_t gemm_known = OG_GEMM_PORTABLE | OG_GEMM_NO_SKINNY | OG_GEMM_NO_DIRECT | OG_GEMM_LARGE_TILE | OG_GEMM_NO_STREAM;
+    if (p->GemmFlags & ~gemm_known) return fail(ctx, OG_ERR_INVALID_ARG, "GemmFlags", "flag bits 0x%x are not product options", p->GemmFlags & ~gemm_known);
+    if ((p->Flags & OG_CONV_WZ_PER_CHANNEL) && !(p->Flags & OG_CONV_WZ)) return fail(ctx, OG_ERR_INVALID_ARG, "Flags", "a per-channel zero point without a zero point");
+    const int64_t B = p->Batch;
+    if (!x.ptr || !fits(p->OffsetX, (uint64_t)(geo.x_image * B), x)) return fail(ctx, OG_ERR_INVALID_ARG, "x", "elements %u..%lld reach past the buffer", p->OffsetX, (long long)(p->OffsetX + geo.x_image * B));
+    if (!w.ptr || !fits(p->OffsetW, (uint64_t)(p->OutChannels * geo.k), w)) return fail(ctx, OG_ERR_INVALID_ARG, "w", "elements %u..%lld reach past the buffer", p->OffsetW, (long long)(p->OffsetW + p->OutChannels * geo.k));
+    if ((int64_t)p->OffsetY + geo.y_image * B > 0x7FFFFFFF) return fail(ctx, OG_ERR_INVALID_ARG, "y", "the result is larger than the supported sizes");
+    if (!y.ptr || ((uintptr_t)y.ptr & 3) || !fits((uint64_t)p->OffsetY * 4, (uint64_t)(geo.y_image * B) * 4, y)) return fail(ctx, OG_ERR_INVALID_ARG, "y", "elements %u..%lld reach past the buffer (or it is misaligned)", p->OffsetY, (long long)(p->OffsetY + geo.y_image * B));
+    if ((p->Flags & OG_CONV_XZ) && (!xz.ptr || !fits(p->OffXZero, 1, xz))) return fail(ctx, OG_ERR_INVALID_ARG, "xZeroPoint", "element %u reaches past the buffer", p->OffXZero);
+    const uint64_t nwz = (p->Flags & OG_CONV_WZ_PER_CHANNEL) ? p->OutChannels : 1;
+    if ((p->Flags & OG_CONV_WZ) && (!wz.ptr || !fits(p->OffWZero, nwz, wz))) return fail(ctx, OG_ERR_INVALID_ARG, "wZeroPoint", "elements %u..%llu reach past the buffer", p->OffWZero, (unsigned long long)(p->OffWZero + nwz));
+    const bool depthwise = geo.cin_g == 1 && !(p->Flags & OG_CONV_NO_DEPTHWISE);
+    int64_t per_chunk = B;
+    if (!depthwise) {
+        if (scratch_offset & 3) return fail(ctx, OG_ERR_INVALID_ARG, "scratchOffset", "offset %llu must be a multiple of 4", (unsigned long long)scratch_offset);
+        if (!scratch.ptr || !fits(scratch_offset, (uint64_t)geo.per_image, scratch)) return fail(ctx, OG_ERR_INVALID_ARG, "scratch", "one image's columns (%lld bytes from %llu) reach past the buffer", (long long)geo.per_image, (unsigned long long)scratch_offset);
+        per_chunk = std::min<int64_t>(B, (int64_t)((scratch.bytes - scratch_offset) / (uint64_t)geo.per_image));
+        per_chunk = std::min<int64_t>(per_chunk, 0x7FFFFFFF / geo.per_image);   // one chunk's columns stay under 2 GiB
+    }
+    if (!ctx) return fail(ctx, OG_ERR_NO_DEVICE, "ctx", "no context: the arguments are valid but there is no device to run on");
+    (void)hipSetDevice(ctx->device);
+
+    const uint8_t *xb = static_cast<const uint8_t *>(x.ptr) + p->OffsetX;
+    const uint8_t *wb = static_cast<const uint8_t *>(w.ptr) + p->OffsetW;
+    int32_t *yb = static_cast<int32_t *>(y.ptr) + p->OffsetY;
+    const uint8_t *xzp = (p->Flags & OG_CONV_XZ) ? static_cast<const uint8_t *>(xz.ptr) + p->OffXZero : nullptr;
+    const uint8_t *wzp = (p->Flags & OG_CONV_WZ) ? static_cast<const uint8_t *>(wz.ptr) + p->OffWZero : nullptr;
+    int st = OG_OK;
+    if (depthwise) {
+        og::ConvDepthwiseArgs a{};
+        a.x = xb;
+        a.wt = wb;
+        a.xz = xzp;
+        a.wz = wzp;
+        a.y = yb;
+        a.batch = (int32_t)B;
+        a.cin = (int32_t)p->InChannels;
+        a.cout = (int32_t)p->OutChannels;
+        a.h = (int32_t)p->Height;
+        a.w = (int32_t)p->Width;
+        a.oh = (int32_t)geo.oh;
+        a.ow = (int32_t)geo.ow;
+        a.kh = (int32_t)p->KernelHeight;
+        a.kw = (int32_t)p->KernelWidth;
+        a.sh = (int32_t)p->StrideHeight;
+        a.sw = (int32_t)p->StrideWidth;
+        a.dh = (int32_t)p->DilationHeight;
+        a.dw = (int32_t)p->DilationWidth;
+        a.ph = (int32_t)p->PadTop;
+        a.pw = (int32_t)p->PadLeft;
+        a.x_signed = p->Flags & OG_CONV_X_INT8;
+        a.w_signed = p->Flags & OG_CONV_W_INT8;
+        a.wz_per_channel = p->Flags & OG_CONV_WZ_PER_CHANNEL;
+        st = launch(ctx, "og_conv_integer", [&](const char **k) { return og::launch_conv_depthwise(a, ctx->stream, k); });
+        return st == OG_OK ? ok(ctx) : st;
+    }
+    uint8_t *cols = static_cast<uint8_t *>(scratch.ptr) + scratch_offset;
+    const int64_t ncols = geo.oh * geo.ow;
+    for (int64_t first = 0; first < B && st == OG_OK; first += per_chunk) {
+        const int32_t images = (int32_t)std::min<int64_t>(per_chunk, B - first);
+        og::ConvPackArgs pa{};
+        pa.x = xb + first * geo.x_image;
+        pa.xz = xzp;
+        pa.cols = cols;
+        pa.images = images;
+        pa.groups = (int32_t)p->Groups;
+        pa.k = (int32_t)geo.k;
+        pa.cin = (int32_t)p->InChannels;
+        pa.cin_g = (int32_t)geo.cin_g;
+        pa.h = (int32_t)p->Height;
+        pa.w = (int32_t)p->Width;
+        pa.oh = (int32_t)geo.oh;
+        pa.ow = (int32_t)geo.ow;
+        pa.kh = (int32_t)p->KernelHeight;
+        pa.kw = (int32_t)p->KernelWidth;
+        pa.sh = (int32_t)p->StrideHeight;
+        pa.sw = (int32_t)p->StrideWidth;
+        pa.dh = (int32_t)p->DilationHeight;
+        pa.dw = (int32_t)p->DilationWidth;
+        pa.ph = (int32_t)p->PadTop;
+        pa.pw = (int32_t)p->PadLeft;
+        pa.ldb = geo.ldb;
+        st = launch(ctx, "og_conv_integer", [&](const char **k) { return og::launch_conv_pack(pa, ctx->stream, k); });
+        // The products: A = the group's weights [cout_g x k] (zero point per row = per output channel), B = its
+        // column matrix [k x ncols] (x's zero point), one batch entry per image of the chunk.
+        for (int64_t g = 0; g < p->Groups && st == OG_OK; g++) {
+            og::GemmArgs ga{};
+            ga.A = wb + g * geo.cout_g * geo.k;
+            ga.B = cols + g * geo.k * geo.ldb;
+            ga.C = yb + first * geo.y_image + g * geo.cout_g * ncols;
+            ga.ZA = wzp ? wzp + ((p->Flags & OG_CONV_WZ_PER_CHANNEL) ? g * geo.cout_g : 0) : nullptr;
+            ga.ZB = xzp;
+            ga.strideA = 0;
+            ga.strideB = p->Groups * geo.k * geo.ldb;
+            ga.strideC = geo.y_image;
+            ga.b_bytes = (int64_t)(scratch.bytes - scratch_offset) - g * geo.k * geo.ldb;
+            ga.M = (int32_t)geo.cout_g;
+            ga.N = (int32_t)ncols;
+            ga.K = (int32_t)geo.k;
+            ga.batch = images;
+            ga.lda = (int32_t)geo.k;
+            ga.ldb = (int32_t)geo.ldb;
+            ga.flags = p->GemmFlags | ((p->Flags & OG_CONV_W_INT8) ? OG_GEMM_A_INT8 : 0u) |
+                       ((p->Flags & OG_CONV_X_INT8) ? OG_GEMM_B_INT8 : 0u) | (wzp ? OG_GEMM_ZA : 0u) |
+                       ((p->Flags & OG_CONV_WZ_PER_CHANNEL) ? OG_GEMM_ZA_PER_ROW : 0u) | (xzp ? OG_GEMM_ZB : 0u);
+            ga.epi = 0;
+            st = launch_product(ctx, ga);
+        }
+    }
     return st == OG_OK ? ok(ctx) : st;
 }
 

@@ -224,7 +224,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_tiled(GemmArgs g, int32_t
         b_valid = (int64_t)(min(g.N - n0, BN) - 1) * ldb + K;
     } else {
         b_base = g.B + batch * g.strideB + n0;
-        b_valid = (int64_t)(K - 1) * ldb + min(g.N - n0, BN);
+        b_valid = (int64_t)(K - 1) * ldb + ((min(g.N - n0, BN) + 3) & ~3);   // whole dwords (b_dwords_ok)
     }
 
     if (SUM_A) for (int i = tid; i < BM; i += T::THREADS) RowSum[i] = 0;
@@ -474,7 +474,7 @@ bool tiled_fast_ok(const GemmArgs &g)
     if (((g.ldb | g.strideB | (int64_t)(uintptr_t)g.B) & (trans_b ? 15 : 3)) != 0) return false;
     if ((int64_t)g.M * g.lda > lim) return false;
     if ((int64_t)(trans_b ? g.N : g.K) * g.ldb > lim) return false;
-    return true;
+    return b_dwords_ok(g);
 }
 
 // The large tile when it still gives (nearly) every CU a tile of its own; the small one otherwise.

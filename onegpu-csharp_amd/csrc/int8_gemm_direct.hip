@@ -16,7 +16,7 @@ bool direct_ok(const GemmArgs &g)
     if (((g.ldb | g.strideB | (int64_t)(uintptr_t)g.B) & 15) != 0) return false;
     if ((int64_t)g.M * g.lda > lim) return false;
     if ((int64_t)(trans_b ? g.N : g.K) * g.ldb > lim) return false;
-    return true;
+    return b_dwords_ok(g);
 }
 
 hipError_t launch_gemm_direct(const GemmArgs &g, hipStream_t s, const char **kernel, bool large)

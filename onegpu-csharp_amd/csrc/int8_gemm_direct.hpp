@@ -222,7 +222,7 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
         b_step = 1;
     } else {
         b_base = g.B + batch * g.strideB + n0;
-        b_valid = K > 0 ? (K - 1) * ldb + min(g.N - n0, DBN) : 0;
+        b_valid = K > 0 ? (K - 1) * ldb + ((min(g.N - n0, DBN) + 3) & ~3) : 0;   // whole dwords (b_dwords_ok)
         b_step = ldb;
     }
 

@@ -23,6 +23,9 @@ struct GemmArgs {
     const float *fbias;
     const float *act_scale;   // EPI_SCALE_PRODUCT: the column scale is fl(*act_scale * scale[n or 0])
     int64_t strideA, strideB, strideC;
+    // Bytes readable from B (all batches). The aligned K x N kernels load B's rows a dword at a time, so with N not a
+    // multiple of 4 they read up to round4(N) in the last row: they run only when that stays inside this extent.
+    int64_t b_bytes;
     int32_t M, N, K, batch;
     int32_t lda, ldb;
     uint32_t flags;  // OG_GEMM_*
@@ -62,6 +65,12 @@ hipError_t launch_gemm_generic(const GemmArgs &g, hipStream_t s, const char **ke
 // 128 x 128; launch_gemm_tiled picks it when it applies.
 hipError_t launch_gemm_direct(const GemmArgs &g, hipStream_t s, const char **kernel, bool large);
 bool direct_ok(const GemmArgs &g);
+// Whether B's last row can be read in whole dwords up to round4(N) (K x N layout; always true for N % 4 == 0).
+inline bool b_dwords_ok(const GemmArgs &g)
+{
+    if ((g.flags & OG_GEMM_TRANSPOSE_B) || g.N % 4 == 0 || g.K == 0) return true;
+    return (int64_t)(g.batch - 1) * g.strideB + (int64_t)(g.K - 1) * g.ldb + ((g.N + 3) & ~3) <= g.b_bytes;
+}
 bool tiled_fast_ok(const GemmArgs &g);
 bool tiled_uses_large(int32_t M, int32_t N, int32_t batch);
 // Few rows (M <= 16), B stored K x N: split-k partial sums into ws.partials, then a pass that adds them up, corrects for
@@ -120,6 +129,27 @@ struct GatherArgs {
     bool wide;          // int64 indices
 };
 hipError_t launch_gather(const GatherArgs &a, hipStream_t s, const char **kernel);
+
+// ConvInteger's column matrix for `images` images from x (image 0 of the chunk): per image and group K rows of ldb
+// bytes (ldb a multiple of 16, at least oh * ow), image-major then group; padding and padding columns hold *xz (0 when
+// absent).
+struct ConvPackArgs {
+    const uint8_t *x;
+    const uint8_t *xz;
+    uint8_t *cols;
+    int32_t images, groups, k, cin, cin_g, h, w, oh, ow, kh, kw, sh, sw, dh, dw, ph, pw;
+    int64_t ldb;
+};
+hipError_t launch_conv_pack(const ConvPackArgs &a, hipStream_t s, const char **kernel);
+
+// ConvInteger with one input channel a group: y[n, m, i, j] from input channel m / (cout / cin) directly.
+struct ConvDepthwiseArgs {
+    const uint8_t *x, *wt, *xz, *wz;
+    int32_t *y;
+    int32_t batch, cin, cout, h, w, oh, ow, kh, kw, sh, sw, dh, dw, ph, pw;
+    bool x_signed, w_signed, wz_per_channel;
+};
+hipError_t launch_conv_depthwise(const ConvDepthwiseArgs &a, hipStream_t s, const char **kernel);
 
 hipError_t launch_fill_bytes(void *dst, uint8_t value, uint64_t bytes, hipStream_t s);
 hipError_t launch_synth(int kind, uint64_t seed, uint32_t tensor, void *out, uint64_t count, double lo, double hi,

@@ -582,6 +582,17 @@ std::pair<GpuBuffer, int> Int8Gemm::Scratch(int64_t count, const std::optional<I
     return {scratch_.back(), 0};
 }
 
+// The library's product flags for Int8GemmOptions: the portable kernel, and the test hooks that pin a kernel.
+static uint32_t OptionFlags(const Int8GemmOptions &o)
+{
+    uint32_t flags = 0;
+    if (!o.AllowPackedDot) flags |= OG_GEMM_PORTABLE;
+    if (o.Tile == 64) flags |= OG_GEMM_NO_SKINNY;
+    if (o.Tile == 256) flags |= OG_GEMM_NO_SKINNY | OG_GEMM_LARGE_TILE;
+    if (o.Tile == 32) flags |= OG_GEMM_NO_DIRECT | OG_GEMM_NO_STREAM;
+    return flags;
+}
+
 // Int8Gemm.cs:554-639: the 19 parameter words, then one og_int8_gemm call when the encoder is submitted.
 void Int8Gemm::Multiply(GpuCommandEncoder &encoder, const Int8GemmProblem &p, const GpuBuffer &a, bool aSigned,
                         const GpuBuffer &b, bool bSigned, const GpuBuffer &c, int offsetC,
@@ -605,10 +616,7 @@ void Int8Gemm::Multiply(GpuCommandEncoder &encoder, const Int8GemmProblem &p, co
     // The reference's word-alignment bits (informational here: the library checks the addresses itself).
     if (((p.OffsetA | p.StrideA | lda) & 3) == 0) flags |= 128u;
     if (((p.OffsetB | p.StrideB | ldb) & 3) == 0) flags |= 256u;
-    if (!options_.AllowPackedDot) flags |= OG_GEMM_PORTABLE;
-    if (options_.Tile == 64) flags |= OG_GEMM_NO_SKINNY;
-    if (options_.Tile == 256) flags |= OG_GEMM_NO_SKINNY | OG_GEMM_LARGE_TILE;
-    if (options_.Tile == 32) flags |= OG_GEMM_NO_DIRECT | OG_GEMM_NO_STREAM;
+    flags |= OptionFlags(options_);
 
     og_int8_gemm_params w{};
     w.M = (uint32_t)p.M;
@@ -936,6 +944,202 @@ void GatherKernels::EncodeGather(GpuCommandEncoder &encoder, const GpuBuffer &da
             ThrowIfFailed(ctx, og_gather(ctx, eb, &w, bind(D), bind(I), bind(O), bind(S)), "Gather");
         },
         keep_of({&D, &I, &O, &S}));
+}
+
+// ------------------------------------------------------------------ ConvInteger
+
+ConvProblem ConvProblem::Conv1D(int batch, int inChannels, int length, int outChannels, int kernel, int stride,
+                                int dilation, int padBegin, int padEnd, int groups)
+{
+    ConvProblem p(batch, inChannels, 1, length, outChannels, 1, kernel);
+    p.StrideWidth = stride;
+    p.DilationWidth = dilation;
+    p.PadLeft = padBegin;
+    p.PadRight = padEnd;
+    p.Groups = groups;
+    return p;
+}
+
+static int OutputExtent(int input, int kernel, int stride, int dilation, int padBegin, int padEnd)
+{
+    if (input < 1 || kernel < 1 || stride < 1 || dilation < 1) return 0;
+    const int64_t effective = (int64_t)dilation * (kernel - 1) + 1;
+    const int64_t span = (int64_t)input + padBegin + padEnd - effective;
+    if (span < 0) return 0;
+    const int64_t extent = span / stride + 1;
+    return extent > INT32_MAX ? 0 : (int)extent;
+}
+
+int ConvProblem::OutHeight() const { return OutputExtent(Height, KernelHeight, StrideHeight, DilationHeight, PadTop, PadBottom); }
+int ConvProblem::OutWidth() const { return OutputExtent(Width, KernelWidth, StrideWidth, DilationWidth, PadLeft, PadRight); }
+
+static const char *kConv = "ConvInteger";
+
+// ConvKernels.CheckWindow / CheckConv (ConvKernels.cs:895-956).
+static void CheckWindow(const std::string &axis, int input, int kernel, int stride, int dilation, int padBegin, int padEnd)
+{
+    if (input < 1) throw GpuKernelShapeException(kConv, axis + " input", "extent " + std::to_string(input) + " must be at least 1");
+    if (kernel < 1) throw GpuKernelShapeException(kConv, axis + " kernel", "extent " + std::to_string(kernel) + " must be at least 1");
+    if (stride < 1) throw GpuKernelShapeException(kConv, axis + " stride", "stride " + std::to_string(stride) + " must be at least 1");
+    if (dilation < 1) throw GpuKernelShapeException(kConv, axis + " dilation", "dilation " + std::to_string(dilation) + " must be at least 1");
+    if (padBegin < 0 || padEnd < 0) throw GpuKernelShapeException(kConv, axis + " padding", "padding must not be negative");
+    if ((int64_t)kernel * dilation > Check::MaxElements || (int64_t)padBegin + padEnd + input > Check::MaxElements)
+        throw GpuKernelShapeException(kConv, axis, "the window or padding is larger than the supported sizes");
+}
+
+// ConvIntegerKernels.Geometry (ConvIntegerKernels.cs:296-318), with the column rows padded to 16 bytes.
+static void ConvGeometry(const ConvProblem &p, int &oh, int &ow, int64_t &k, int64_t &ldb)
+{
+    oh = p.OutHeight();
+    ow = p.OutWidth();
+    if (p.Batch < 1) throw GpuKernelShapeException(kConv, "Batch", "batch " + std::to_string(p.Batch) + " must be at least 1");
+    if (p.InChannels < 1 || p.OutChannels < 1)
+        throw GpuKernelShapeException(kConv, p.InChannels < 1 ? "InChannels" : "OutChannels", "channel counts must be at least 1");
+    if (p.Groups < 1 || p.InChannels % p.Groups != 0 || p.OutChannels % p.Groups != 0)
+        throw GpuKernelShapeException(kConv, "Groups", std::to_string(p.Groups) + " groups do not divide " + std::to_string(p.InChannels) +
+                                                          " input and " + std::to_string(p.OutChannels) + " output channels");
+    CheckWindow("height", p.Height, p.KernelHeight, p.StrideHeight, p.DilationHeight, p.PadTop, p.PadBottom);
+    CheckWindow("width", p.Width, p.KernelWidth, p.StrideWidth, p.DilationWidth, p.PadLeft, p.PadRight);
+    if (oh < 1) throw GpuKernelShapeException(kConv, "height", "the kernel does not fit the padded input");
+    if (ow < 1) throw GpuKernelShapeException(kConv, "width", "the kernel does not fit the padded input");
+    k = (int64_t)(p.InChannels / p.Groups) * p.KernelHeight * p.KernelWidth;
+    ldb = ((int64_t)oh * ow + 15) / 16 * 16;
+    if (k > Check::MaxElements || ldb > Check::MaxElements || (int64_t)p.Batch * p.InChannels * p.Height * p.Width > Check::MaxElements)
+        throw GpuKernelShapeException(kConv, "shape", "the convolution is larger than the supported sizes");
+}
+
+ConvIntegerKernels::ConvIntegerKernels(std::shared_ptr<GpuDevice> device, Int8GemmOptions options, int maxCachedBindGroups)
+    : device_(device), options_(options), gemm_(device, options, maxCachedBindGroups)
+{
+    if (!device_) throw std::invalid_argument("device");
+}
+
+int64_t ConvIntegerKernels::ScratchBytesPerImage(const ConvProblem &problem)
+{
+    int oh, ow;
+    int64_t k, ldb;
+    ConvGeometry(problem, oh, ow, k, ldb);
+    return (int64_t)problem.Groups * k * ldb;
+}
+
+GpuBuffer ConvIntegerKernels::Own(ElementType t, int64_t bytes)
+{
+    GpuBuffer &own = t == ElementType::Int8 ? own_i8_ : own_u8_;
+    int64_t want = std::min<int64_t>(Check::MaxElements, std::max<int64_t>(bytes, 4096));
+    if (!own.Valid() || own.Length() < want) {
+        if (own.Valid()) {
+            retired_.push_back(own);
+            want = std::min<int64_t>(Check::MaxElements, std::max<int64_t>(want, (int64_t)own.Length() * 2));
+        }
+        own = device_->CreateBuffer(t, (int)want);
+    }
+    return own;
+}
+
+void ConvIntegerKernels::Encode(GpuCommandEncoder &encoder, const ConvProblem &problem, const GpuBuffer &x,
+                                const GpuBuffer &w, const GpuBuffer &y, const std::optional<Int8Operand> &xZeroPoint,
+                                const std::optional<Int8Operand> &wZeroPoint, const std::optional<GpuBuffer> &scratch,
+                                int scratchOffset)
+{
+    if (!x.Valid()) throw GpuKernelShapeException(kConv, "x", "buffer is null");
+    if (!w.Valid()) throw GpuKernelShapeException(kConv, "w", "buffer is null");
+    if (!y.Valid()) throw GpuKernelShapeException(kConv, "y", "buffer is null");
+    auto requireInt8 = [](const GpuBuffer &b, const char *arg) {
+        if (b.Type() != ElementType::UInt8 && b.Type() != ElementType::Int8)
+            throw GpuKernelShapeException(kConv, arg, std::string("element type ") + ElementName(b.Type()) +
+                                                          " is not supported; use byte (uint8) or sbyte (int8)");
+    };
+    requireInt8(x, "x");
+    requireInt8(w, "w");
+    RequireType(kConv, y, ElementType::Int32, "y");
+    const ConvProblem &p = problem;
+    int oh, ow;
+    int64_t k, ldb;
+    ConvGeometry(p, oh, ow, k, ldb);
+    const int64_t nCols = (int64_t)oh * ow;
+    if (p.Activation != 0) throw GpuKernelShapeException(kConv, "Activation", "an integer convolution has no fused activation");
+    const int64_t xImage = (int64_t)p.InChannels * p.Height * p.Width;
+    const int64_t yImage = (int64_t)p.OutChannels * nCols;
+    Check::Range(kConv, "x", x.Length(), p.OffsetX, xImage * p.Batch);
+    Check::Range(kConv, "w", w.Length(), p.OffsetW, (int64_t)p.OutChannels * k);
+    Check::Range(kConv, "y", y.Length(), p.OffsetY, yImage * p.Batch);
+    if (p.OffsetY < 0 || (int64_t)p.OffsetY + yImage * p.Batch > Check::MaxElements)
+        throw GpuKernelShapeException(kConv, "y", "the result is larger than the supported sizes");
+    if (xZeroPoint) {
+        if (!xZeroPoint->Buffer.Valid()) throw GpuKernelShapeException(kConv, "xZeroPoint", "buffer is null");
+        if (xZeroPoint->Buffer.Type() != x.Type()) throw GpuKernelShapeException(kConv, "xZeroPoint", "the zero point has a different type than x");
+        Check::Range(kConv, "xZeroPoint", xZeroPoint->Buffer.Length(), xZeroPoint->Offset, 1);
+        if (xZeroPoint->IsVector) throw GpuKernelShapeException(kConv, "xZeroPoint", "the zero point of x is a single value");
+    }
+    if (wZeroPoint) {
+        if (!wZeroPoint->Buffer.Valid()) throw GpuKernelShapeException(kConv, "wZeroPoint", "buffer is null");
+        if (wZeroPoint->Buffer.Type() != w.Type()) throw GpuKernelShapeException(kConv, "wZeroPoint", "the zero point has a different type than w");
+        Check::Range(kConv, "wZeroPoint", wZeroPoint->Buffer.Length(), wZeroPoint->Offset, wZeroPoint->IsVector ? p.OutChannels : 1);
+    }
+    const int64_t perImage = (int64_t)p.Groups * k * ldb;
+    if (perImage > Check::MaxElements)
+        throw GpuKernelShapeException(kConv, "InChannels", "the column matrix of one image needs " + std::to_string(perImage) + " bytes, more than the supported sizes");
+    const bool depthwise = DirectDepthwise && p.InChannels == p.Groups;   // one input channel a group: convolved directly
+    GpuBuffer columns;
+    int64_t columnBase = 0;
+    if (scratch) {
+        if (!scratch->Valid()) throw GpuKernelShapeException(kConv, "scratch", "buffer is null");
+        if (scratch->Type() != x.Type()) throw GpuKernelShapeException(kConv, "scratch", "the scratch has a different type than x");
+        if (scratchOffset < 0 || (scratchOffset & 3) != 0)
+            throw GpuKernelShapeException(kConv, "scratchOffset", "offset " + std::to_string(scratchOffset) + " must be a non-negative multiple of 4");
+        if ((int64_t)scratchOffset + perImage > scratch->Length())
+            throw GpuKernelShapeException(kConv, "scratch", "bytes " + std::to_string(scratchOffset) + ".." + std::to_string(scratchOffset + perImage) +
+                                                                " (one image's columns) reach past the buffer of " + std::to_string(scratch->Length()));
+        columns = *scratch;
+        columnBase = scratchOffset;
+    } else if (!depthwise) {
+        const int64_t ownScratchBytes = int64_t(64) << 20;   // ConvIntegerKernels.cs:33
+        const int64_t imagesPerChunk = std::clamp<int64_t>(ownScratchBytes / perImage, 1, p.Batch);
+        columns = Own(x.Type(), imagesPerChunk * perImage);
+    }
+    og_conv_params c{};
+    c.Batch = (uint32_t)p.Batch;
+    c.InChannels = (uint32_t)p.InChannels;
+    c.Height = (uint32_t)p.Height;
+    c.Width = (uint32_t)p.Width;
+    c.OutChannels = (uint32_t)p.OutChannels;
+    c.KernelHeight = (uint32_t)p.KernelHeight;
+    c.KernelWidth = (uint32_t)p.KernelWidth;
+    c.StrideHeight = (uint32_t)p.StrideHeight;
+    c.StrideWidth = (uint32_t)p.StrideWidth;
+    c.DilationHeight = (uint32_t)p.DilationHeight;
+    c.DilationWidth = (uint32_t)p.DilationWidth;
+    c.PadTop = (uint32_t)p.PadTop;
+    c.PadLeft = (uint32_t)p.PadLeft;
+    c.PadBottom = (uint32_t)p.PadBottom;
+    c.PadRight = (uint32_t)p.PadRight;
+    c.Groups = (uint32_t)p.Groups;
+    c.OffsetX = (uint32_t)p.OffsetX;
+    c.OffsetW = (uint32_t)p.OffsetW;
+    c.OffsetY = (uint32_t)p.OffsetY;
+    c.Flags = (x.Type() == ElementType::Int8 ? OG_CONV_X_INT8 : 0u) | (w.Type() == ElementType::Int8 ? OG_CONV_W_INT8 : 0u) |
+              (xZeroPoint ? OG_CONV_XZ : 0u) | (wZeroPoint ? OG_CONV_WZ : 0u) |
+              (wZeroPoint && wZeroPoint->IsVector ? OG_CONV_WZ_PER_CHANNEL : 0u) | (DirectDepthwise ? 0u : OG_CONV_NO_DEPTHWISE);
+    c.OffXZero = xZeroPoint ? (uint32_t)xZeroPoint->Offset : 0u;
+    c.OffWZero = wZeroPoint ? (uint32_t)wZeroPoint->Offset : 0u;
+    c.GemmFlags = OptionFlags(options_);
+    GpuBuffer X = x, W = w, Y = y, XZ = xZeroPoint ? xZeroPoint->Buffer : GpuBuffer(),
+              WZ = wZeroPoint ? wZeroPoint->Buffer : GpuBuffer(), S = columns;
+    const uint64_t off = (uint64_t)columnBase;
+    encoder.Record(
+        [c, X, W, Y, XZ, WZ, S, off](og_ctx *ctx) {
+            ThrowIfFailed(ctx, og_conv_integer(ctx, &c, bind(X), bind(W), bind(Y), bind(XZ), bind(WZ), bind(S), off), kConv);
+        },
+        keep_of({&X, &W, &Y, &XZ, &WZ, &S}));
+}
+
+void ConvIntegerKernels::Dispose()
+{
+    gemm_.Dispose();
+    own_u8_.Dispose();
+    own_i8_.Dispose();
+    for (auto &b : retired_) b.Dispose();
+    retired_.clear();
 }
 
 }  // namespace onegpu

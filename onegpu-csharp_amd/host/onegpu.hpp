@@ -325,6 +325,55 @@ private:
     std::shared_ptr<GpuDevice> device_;
 };
 
+// The geometry of a convolution (src/RecursiveAI.OneGpu.Kernels/ConvProblem.cs:107-235): NCHW input, OIHW weights,
+// strides, dilations, asymmetric padding, groups; offsets in elements. Activation must stay 0 for ConvInteger.
+struct ConvProblem {
+    int Batch = 1, InChannels = 1, Height = 1, Width = 1, OutChannels = 1, KernelHeight = 1, KernelWidth = 1;
+    int StrideHeight = 1, StrideWidth = 1, DilationHeight = 1, DilationWidth = 1;
+    int PadTop = 0, PadLeft = 0, PadBottom = 0, PadRight = 0, Groups = 1;
+    int Activation = 0;
+    int OffsetX = 0, OffsetW = 0, OffsetBias = 0, OffsetResidual = 0, OffsetY = 0;
+    ConvProblem() = default;
+    ConvProblem(int batch, int inChannels, int height, int width, int outChannels, int kernelHeight, int kernelWidth)
+        : Batch(batch), InChannels(inChannels), Height(height), Width(width), OutChannels(outChannels),
+          KernelHeight(kernelHeight), KernelWidth(kernelWidth) {}
+    // ConvProblem.Conv1D (ConvProblem.cs:127-136): height 1.
+    static ConvProblem Conv1D(int batch, int inChannels, int length, int outChannels, int kernel, int stride = 1,
+                              int dilation = 1, int padBegin = 0, int padEnd = 0, int groups = 1);
+    int OutHeight() const;   // GpuWindow.OutputExtent without auto padding or ceil mode (ConvProblem.cs:36-73)
+    int OutWidth() const;
+};
+
+// ONNX ConvInteger (ConvIntegerKernels.cs:6-351): the column matrix and the int8 products, or a direct kernel when
+// every group has one input channel. Same checks, exceptions and scratch rules as the reference; the column rows are
+// padded to 16 bytes here, so ScratchBytesPerImage is Groups * K * round16(OutHeight * OutWidth).
+class ConvIntegerKernels {
+public:
+    explicit ConvIntegerKernels(std::shared_ptr<GpuDevice> device, Int8GemmOptions options = {},
+                                int maxCachedBindGroups = 1024);
+    std::string Variant() const { return gemm_.Variant(); }
+    int BindGroupsCreated() const { return 0; }
+    static int64_t ScratchBytesPerImage(const ConvProblem &problem);
+    // ConvIntegerKernels.cs:97-253.
+    void Encode(GpuCommandEncoder &encoder, const ConvProblem &problem, const GpuBuffer &x, const GpuBuffer &w,
+                const GpuBuffer &y, const std::optional<Int8Operand> &xZeroPoint = std::nullopt,
+                const std::optional<Int8Operand> &wZeroPoint = std::nullopt,
+                const std::optional<GpuBuffer> &scratch = std::nullopt, int scratchOffset = 0);
+    void ReleaseBindings() {}
+    void Dispose();
+    // This library's own: convolutions with one input channel a group run on the direct kernel (true, the default)
+    // or through the column matrix and the products like the others (false; a test hook).
+    bool DirectDepthwise = true;
+
+private:
+    GpuBuffer Own(ElementType t, int64_t bytes);
+    std::shared_ptr<GpuDevice> device_;
+    Int8GemmOptions options_;
+    Int8Gemm gemm_;
+    GpuBuffer own_u8_, own_i8_;
+    std::vector<GpuBuffer> retired_;   // smaller columns buffers that recorded commands may still name
+};
+
 // Where a gather records the position of an invalid index (GpuIndexStatus.cs:13-63): one uint32 on the device, reset to
 // "none" (0xFFFFFFFF) before the work and read back after it.
 class GpuIndexStatus {

@@ -246,6 +246,53 @@ PYBIND11_MODULE(_onegpu_host, m)
         .def("__enter__", [](DynamicQuantizeKernels &g) -> DynamicQuantizeKernels & { return g; })
         .def("__exit__", [](DynamicQuantizeKernels &g, py::args) { g.Dispose(); });
 
+    py::class_<ConvProblem>(m, "ConvProblem")
+        .def(py::init<>())
+        .def(py::init<int, int, int, int, int, int, int>(), py::arg("batch"), py::arg("inChannels"), py::arg("height"),
+             py::arg("width"), py::arg("outChannels"), py::arg("kernelHeight"), py::arg("kernelWidth"))
+        .def_static("Conv1D", &ConvProblem::Conv1D, py::arg("batch"), py::arg("inChannels"), py::arg("length"),
+                    py::arg("outChannels"), py::arg("kernel"), py::arg("stride") = 1, py::arg("dilation") = 1,
+                    py::arg("padBegin") = 0, py::arg("padEnd") = 0, py::arg("groups") = 1)
+        .def_readwrite("Batch", &ConvProblem::Batch)
+        .def_readwrite("InChannels", &ConvProblem::InChannels)
+        .def_readwrite("Height", &ConvProblem::Height)
+        .def_readwrite("Width", &ConvProblem::Width)
+        .def_readwrite("OutChannels", &ConvProblem::OutChannels)
+        .def_readwrite("KernelHeight", &ConvProblem::KernelHeight)
+        .def_readwrite("KernelWidth", &ConvProblem::KernelWidth)
+        .def_readwrite("StrideHeight", &ConvProblem::StrideHeight)
+        .def_readwrite("StrideWidth", &ConvProblem::StrideWidth)
+        .def_readwrite("DilationHeight", &ConvProblem::DilationHeight)
+        .def_readwrite("DilationWidth", &ConvProblem::DilationWidth)
+        .def_readwrite("PadTop", &ConvProblem::PadTop)
+        .def_readwrite("PadLeft", &ConvProblem::PadLeft)
+        .def_readwrite("PadBottom", &ConvProblem::PadBottom)
+        .def_readwrite("PadRight", &ConvProblem::PadRight)
+        .def_readwrite("Groups", &ConvProblem::Groups)
+        .def_readwrite("Activation", &ConvProblem::Activation)
+        .def_readwrite("OffsetX", &ConvProblem::OffsetX)
+        .def_readwrite("OffsetW", &ConvProblem::OffsetW)
+        .def_readwrite("OffsetY", &ConvProblem::OffsetY)
+        .def_property_readonly("OutHeight", &ConvProblem::OutHeight)
+        .def_property_readonly("OutWidth", &ConvProblem::OutWidth);
+
+    py::class_<ConvIntegerKernels>(m, "ConvIntegerKernels")
+        .def(py::init([](std::shared_ptr<GpuDevice> d, std::optional<Int8GemmOptions> o, int maxGroups) {
+                 return new ConvIntegerKernels(std::move(d), o.value_or(Int8GemmOptions{}), maxGroups);
+             }),
+             py::arg("device"), py::arg("options") = py::none(), py::arg("maxCachedBindGroups") = 1024)
+        .def_static("ScratchBytesPerImage", &ConvIntegerKernels::ScratchBytesPerImage, py::arg("problem"))
+        .def("Encode", &ConvIntegerKernels::Encode, py::arg("encoder"), py::arg("problem"), py::arg("x"), py::arg("w"),
+             py::arg("y"), py::arg("xZeroPoint") = py::none(), py::arg("wZeroPoint") = py::none(),
+             py::arg("scratch") = py::none(), py::arg("scratchOffset") = 0)
+        .def_readwrite("DirectDepthwise", &ConvIntegerKernels::DirectDepthwise)
+        .def_property_readonly("Variant", &ConvIntegerKernels::Variant)
+        .def_property_readonly("BindGroupsCreated", &ConvIntegerKernels::BindGroupsCreated)
+        .def("ReleaseBindings", &ConvIntegerKernels::ReleaseBindings)
+        .def("Dispose", &ConvIntegerKernels::Dispose)
+        .def("__enter__", [](ConvIntegerKernels &g) -> ConvIntegerKernels & { return g; })
+        .def("__exit__", [](ConvIntegerKernels &g, py::args) { g.Dispose(); });
+
     py::class_<GpuIndexStatus>(m, "GpuIndexStatus")
         .def(py::init<std::shared_ptr<GpuDevice>>(), py::arg("device"))
         .def("Reset", &GpuIndexStatus::Reset)

@@ -9,7 +9,8 @@ from .errors import (GpuCommandFailedException, GpuDeviceLostException, GpuExcep
                      GpuKernelShapeException, GpuOutOfMemoryException, GpuUnsupportedException)
 
 try:
-    from ._onegpu_host import (DequantizeKernels, DynamicQuantizeKernels, ElementType, GatherKernels, GpuBuffer,
+    from ._onegpu_host import (ConvIntegerKernels, ConvProblem, DequantizeKernels, DynamicQuantizeKernels, ElementType,
+                               GatherKernels, GpuBuffer,
                                GpuCommandEncoder, GpuComputeCapabilities, GpuDevice, GpuIndexStatus, Int8Gemm,
                                Int8GemmOptions, Int8GemmProblem, Int8Operand, Int8Scratch, version)
 except ImportError as e:  # pragma: no cover - a build problem, reported as such
@@ -33,7 +34,7 @@ def padded_half_length(count: int) -> int:
     return (count + 1) & ~1
 
 
-__all__ = ["DequantizeKernels", "DynamicQuantizeKernels", "ElementType", "GatherKernels", "GpuIndexStatus",
+__all__ = ["ConvIntegerKernels", "ConvProblem", "DequantizeKernels", "DynamicQuantizeKernels", "ElementType", "GatherKernels", "GpuIndexStatus",
            "GpuKernelIndexException", "GpuBuffer", "GpuCommandEncoder",
            "GpuComputeCapabilities", "GpuDevice", "Int8Gemm", "Int8GemmOptions", "Int8GemmProblem", "Int8Operand",
            "Int8Scratch", "GpuException", "GpuKernelShapeException", "GpuUnsupportedException", "GpuOutOfMemoryException",

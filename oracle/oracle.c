@@ -483,3 +483,72 @@ void ora_quantize(const float *x, int64_t count, int32_t per_axis, int64_t axis_
         out[j] = (uint8_t)ora_quantize_one(x[j], scale[a], zp, lo, hi);
     }
 }
+
+
+/* ------------------------------------------------------------------ ConvInteger */
+
+typedef struct conv_job {
+    const ora_conv *p;
+    const uint8_t *x, *w, *xz, *wz;
+    int32_t x_signed, w_signed, wz_vec;
+    int32_t *y;
+    int64_t row_begin, row_end;   /* rows are (n, m) pairs */
+} conv_job;
+
+/* tests/K/ConvIntegerTests.cs:42-89: one output plane per (image, output channel). */
+static void *conv_worker(void *arg)
+{
+    const conv_job *j = (const conv_job *)arg;
+    const ora_conv *p = j->p;
+    const int32_t oh = p->OutHeight, ow = p->OutWidth;
+    const int32_t cin_g = p->InChannels / p->Groups, cout_g = p->OutChannels / p->Groups;
+    const int32_t xzv = j->xz ? val(j->xz[0], j->x_signed) : 0;
+    for (int64_t row = j->row_begin; row < j->row_end; row++) {
+        const int64_t n = row / p->OutChannels, m = row % p->OutChannels, g = m / cout_g;
+        const int32_t wzv = j->wz ? val(j->wz[j->wz_vec ? m : 0], j->w_signed) : 0;
+        for (int32_t i = 0; i < oh; i++) {
+            for (int32_t jj = 0; jj < ow; jj++) {
+                uint32_t acc = 0;
+                for (int32_t c = 0; c < cin_g; c++) {
+                    for (int32_t kh = 0; kh < p->KernelHeight; kh++) {
+                        const int64_t ih = (int64_t)i * p->StrideHeight + (int64_t)kh * p->DilationHeight - p->PadTop;
+                        if (ih < 0 || ih >= p->Height) continue;
+                        for (int32_t kw = 0; kw < p->KernelWidth; kw++) {
+                            const int64_t iw = (int64_t)jj * p->StrideWidth + (int64_t)kw * p->DilationWidth - p->PadLeft;
+                            if (iw < 0 || iw >= p->Width) continue;
+                            const int64_t xi = ((n * p->InChannels + g * cin_g + c) * p->Height + ih) * p->Width + iw;
+                            const int64_t wi = ((m * cin_g + c) * p->KernelHeight + kh) * p->KernelWidth + kw;
+                            const int32_t xv = val(j->x[xi], j->x_signed) - xzv;
+                            const int32_t wv = val(j->w[wi], j->w_signed) - wzv;
+                            acc += (uint32_t)xv * (uint32_t)wv;
+                        }
+                    }
+                }
+                j->y[((n * p->OutChannels + m) * oh + i) * ow + jj] = (int32_t)acc;
+            }
+        }
+    }
+    return NULL;
+}
+
+void ora_conv_integer(const ora_conv *p, const uint8_t *x, int32_t x_signed, const uint8_t *w, int32_t w_signed,
+                      const uint8_t *xz, const uint8_t *wz, int32_t wz_vec, int32_t *y, int32_t threads)
+{
+    const int64_t rows = (int64_t)p->Batch * p->OutChannels;
+    if (threads < 1) threads = 1;
+    if (threads > 64) threads = 64;
+    if (rows < threads) threads = (int32_t)(rows > 0 ? rows : 1);
+    pthread_t tid[64];
+    conv_job jobs[64];
+    int started[64] = {0};
+    const int64_t per = (rows + threads - 1) / threads;
+    for (int32_t t = 0; t < threads; t++) {
+        jobs[t] = (conv_job){p, x, w, xz, wz, x_signed, w_signed, wz_vec, y, (int64_t)t * per, 0};
+        jobs[t].row_end = jobs[t].row_begin + per < rows ? jobs[t].row_begin + per : rows;
+        if (jobs[t].row_begin >= jobs[t].row_end) continue;
+        if (threads > 1 && pthread_create(&tid[t], NULL, conv_worker, &jobs[t]) == 0) started[t] = 1;
+        else conv_worker(&jobs[t]);
+    }
+    for (int32_t t = 0; t < threads; t++)
+        if (started[t]) pthread_join(tid[t], NULL);
+}

@@ -83,6 +83,18 @@ int32_t ora_quantize_one(float x, float scale, int32_t zero, int32_t lo, int32_t
 void ora_quantize(const float *x, int64_t count, int32_t per_axis, int64_t axis_len, int64_t inner, const float *scale,
                   const uint8_t *zero, int32_t is_signed, uint8_t *out);
 
+/* --- ConvInteger (tests/K/ConvIntegerTests.cs:42-89, Reference) --- */
+/* NCHW input, OIHW weights, strides, dilations, asymmetric padding (top/left given; the output extent oh x ow is the
+ * caller's), groups. y[n, m, i, j] = sum over c, kh, kw of (x - xz) * (w - wz[m]) in 32-bit wrap-around; taps in the
+ * padding add nothing. xz: one byte or NULL; wz: one byte, or one per output channel (wz_vec), or NULL. */
+typedef struct ora_conv {
+    int32_t Batch, InChannels, Height, Width, OutChannels, KernelHeight, KernelWidth;
+    int32_t StrideHeight, StrideWidth, DilationHeight, DilationWidth, PadTop, PadLeft, Groups;
+    int32_t OutHeight, OutWidth;
+} ora_conv;
+void ora_conv_integer(const ora_conv *p, const uint8_t *x, int32_t x_signed, const uint8_t *w, int32_t w_signed,
+                      const uint8_t *xz, const uint8_t *wz, int32_t wz_vec, int32_t *y, int32_t threads);
+
 #ifdef __cplusplus
 }
 #endif

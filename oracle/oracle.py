@@ -66,6 +66,7 @@ def _declare(L):
     L.ora_int8_gemm_identity.argtypes = gemm_args + [_P]
     L.ora_int8_gemm_rows.argtypes = gemm_args + [_P, _I64, _P, _I32]
     L.ora_float_epilogue.argtypes = [_P, _I64, _I32, _P, _P, _I32, _P, _P]
+    L.ora_conv_integer.argtypes = [_P, _P, _I32, _P, _I32, _P, _P, _I32, _P, _I32]
     L.ora_requant.argtypes = [_I32, _F, _I32, _I32]
     L.ora_requant.restype = _I32
     L.ora_requant_array.argtypes = [_P, _I64, _I32, _P, _P, _I32, _I32, _I32, _P]
@@ -322,3 +323,41 @@ def gather(data, shape, axis, indices, wide=False):
         out[:, valid, :] = d3[:, norm[valid], :]
     bad = np.flatnonzero(~valid)
     return out.reshape(-1), (int(bad[0]) if bad.size else None)
+
+
+# ------------------------------------------------------------------ ConvInteger
+
+class _Conv(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in
+                ("Batch", "InChannels", "Height", "Width", "OutChannels", "KernelHeight", "KernelWidth", "StrideHeight",
+                 "StrideWidth", "DilationHeight", "DilationWidth", "PadTop", "PadLeft", "Groups", "OutHeight",
+                 "OutWidth")]
+
+
+def conv_out_extent(inp: int, kernel: int, stride: int, dilation: int, pad_begin: int, pad_end: int) -> int:
+    """GpuWindow.OutputExtent without auto padding or ceil mode (ConvProblem.cs:36-73): floor of the padded span
+    over the stride, plus one; 0 when the dilated kernel does not fit."""
+    effective = dilation * (kernel - 1) + 1
+    span = inp + pad_begin + pad_end - effective
+    return 0 if span < 0 else span // stride + 1
+
+
+def conv_integer(conv: dict, x, x_signed, w, w_signed, xz=None, wz=None, wz_vec=False, threads: int = 8) -> np.ndarray:
+    """ConvIntegerTests.Reference (ConvIntegerTests.cs:42-89): int32 [Batch, OutChannels, OutHeight, OutWidth], flat.
+    `conv` holds the ConvProblem fields (PadBottom / PadRight only enter the output extent); x and w start at their
+    first element (the caller applies OffsetX / OffsetW)."""
+    c = dict(StrideHeight=1, StrideWidth=1, DilationHeight=1, DilationWidth=1, PadTop=0, PadLeft=0, PadBottom=0,
+             PadRight=0, Groups=1)
+    c.update(conv)
+    oh = conv_out_extent(c["Height"], c["KernelHeight"], c["StrideHeight"], c["DilationHeight"], c["PadTop"], c["PadBottom"])
+    ow = conv_out_extent(c["Width"], c["KernelWidth"], c["StrideWidth"], c["DilationWidth"], c["PadLeft"], c["PadRight"])
+    fields = [f for f, _ in _Conv._fields_ if f not in ("OutHeight", "OutWidth")]
+    pr = _Conv(**{f: int(c[f]) for f in fields}, OutHeight=oh, OutWidth=ow)
+    x = _c(np.asarray(x).view(np.uint8), np.uint8)
+    w = _c(np.asarray(w).view(np.uint8), np.uint8)
+    xzb = None if xz is None else _c(np.asarray(xz).view(np.uint8), np.uint8)
+    wzb = None if wz is None else _c(np.asarray(wz).view(np.uint8), np.uint8)
+    y = np.zeros(c["Batch"] * c["OutChannels"] * oh * ow, np.int32)
+    lib().ora_conv_integer(ctypes.byref(pr), _ptr(x), int(x_signed), _ptr(w), int(w_signed), _ptr(xzb), _ptr(wzb),
+                           int(wz_vec), _ptr(y), threads)
+    return y

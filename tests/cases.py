@@ -230,3 +230,89 @@ def index_rig_random_index(i, n_axis: int, seed: int) -> np.ndarray:
     h ^= h >> np.uint64(13)
     h = (h * np.uint64(3266489917)) & np.uint64(_M32)
     return (h % np.uint64(2 * n_axis)).astype(np.int64) - n_axis
+
+
+# ------------------------------------------------------------------ ConvInteger (ConvIntegerTests.cs)
+
+def conv_bytes(length: int, seed: int) -> np.ndarray:
+    """ConvIntegerTests.Bytes (ConvIntegerTests.cs:19-29): a 32-bit LCG, the top byte of each state. Computed a block
+    at a time: the state j steps on is A_j * s + C_j (mod 2^32)."""
+    a, c, block = 1664525, 1013904223, 4096
+    A, C = np.empty(block, np.uint64), np.empty(block, np.uint64)
+    av, cv = 1, 0
+    for j in range(block):
+        av, cv = (av * a) & _M32, (cv * a + c) & _M32
+        A[j], C[j] = av, cv
+    out = np.empty(length, np.uint8)
+    s = (seed * 2654435761 + 7) & _M32
+    for start in range(0, length, block):
+        n = min(block, length - start)
+        states = (A[:n] * np.uint64(s) + C[:n]) & np.uint64(_M32)
+        out[start:start + n] = (states >> np.uint64(24)).astype(np.uint8)
+        s = int(states[n - 1])
+    return out
+
+
+def conv_problem(batch, cin, h, w, cout, kh, kw, stride=1, dilation=1, pad=0, groups=1) -> dict:
+    """ConvIntegerTests.P (ConvIntegerTests.cs:183-195) as a dict of ConvProblem fields."""
+    return dict(Batch=batch, InChannels=cin, Height=h, Width=w, OutChannels=cout, KernelHeight=kh, KernelWidth=kw,
+                StrideHeight=stride, StrideWidth=stride, DilationHeight=dilation, DilationWidth=dilation, PadTop=pad,
+                PadBottom=pad, PadLeft=pad, PadRight=pad, Groups=groups)
+
+
+def conv1d(batch, cin, length, cout, kernel, stride=1, dilation=1, pad_begin=0, pad_end=0, groups=1) -> dict:
+    """ConvProblem.Conv1D (ConvProblem.cs:127-136)."""
+    return dict(Batch=batch, InChannels=cin, Height=1, Width=length, OutChannels=cout, KernelHeight=1,
+                KernelWidth=kernel, StrideHeight=1, StrideWidth=stride, DilationHeight=1, DilationWidth=dilation,
+                PadTop=0, PadBottom=0, PadLeft=pad_begin, PadRight=pad_end, Groups=groups)
+
+
+def conv_spread(name: str, p: dict) -> list:
+    """ConvIntegerTests.Spread (ConvIntegerTests.cs:223-233): the four signedness combinations; zero points none /
+    one / per channel in turn."""
+    return [dict(name=f"{name} s{s}", p=p, xs=(s & 1) != 0, ws=(s & 2) != 0, xzm=1 - (s & 1), wzm=(s + 1) % 3,
+                 fill=-1, scratch_images=0) for s in range(4)]
+
+
+def conv_edge_cases() -> list:
+    """EdgeGeometriesAreBitExact's cases (ConvIntegerTests.cs:235-275)."""
+    cases = []
+    cases += conv_spread("1x1 pointwise", conv_problem(2, 5, 7, 9, 6, 1, 1))
+    cases += conv_spread("3x3 pad1", conv_problem(1, 3, 10, 13, 4, 3, 3, pad=1))
+    cases += conv_spread("3x3 stride2 pad1 odd", conv_problem(2, 4, 9, 11, 5, 3, 3, stride=2, pad=1))
+    cases += conv_spread("5x5 dilation2", conv_problem(1, 2, 14, 15, 3, 5, 5, dilation=2, pad=4))
+    cases += conv_spread("groups 2", conv_problem(2, 4, 8, 8, 6, 3, 3, pad=1, groups=2))
+    cases += conv_spread("depthwise", conv_problem(2, 6, 9, 10, 6, 3, 3, pad=1, groups=6))
+    cases += conv_spread("1d k3", conv1d(2, 5, 31, 7, 3, pad_begin=1, pad_end=1))
+    cases += conv_spread("1d stride2", conv1d(1, 4, 40, 6, 3, stride=2, pad_begin=1, pad_end=1))
+    cases += conv_spread("1x1 image", conv_problem(3, 8, 1, 1, 4, 1, 1))
+    cases += conv_spread("kernel = image", conv_problem(1, 3, 5, 5, 2, 5, 5))
+    asym = conv_problem(1, 3, 12, 9, 4, 3, 2)
+    asym.update(PadTop=2, PadBottom=0, PadLeft=0, PadRight=3, StrideHeight=2)
+    cases += conv_spread("asymmetric padding", asym)
+    off = conv_problem(2, 3, 6, 7, 5, 3, 3, pad=1)
+    off.update(OffsetX=3, OffsetW=5, OffsetY=7)
+    cases += conv_spread("offsets", off)
+    for s in range(4):
+        for fill in (0, 127, 128, 255):
+            cases.append(dict(name=f"extremes {fill} s{s}", p=conv_problem(1, 17, 6, 6, 3, 3, 3, pad=1),
+                              xs=(s & 1) != 0, ws=(s & 2) != 0, xzm=1, wzm=2, fill=fill, scratch_images=0))
+    cases.append(dict(name="chunked batch, scratch for 1 image", p=conv_problem(3, 3, 8, 8, 4, 3, 3, pad=1), xs=False,
+                      ws=False, xzm=1, wzm=1, fill=-1, scratch_images=1))
+    cases.append(dict(name="grouped, scratch for 2 images", p=conv_problem(3, 4, 8, 8, 6, 3, 3, pad=1, groups=2),
+                      xs=True, ws=True, xzm=1, wzm=2, fill=-1, scratch_images=2))
+    return cases
+
+
+def conv_model_cases() -> list:
+    """WhisperStemIsBitExact and ResNetShapesAreBitExact (ConvIntegerTests.cs:277-307)."""
+    c = lambda name, p, xs, ws, wzm: dict(name=name, p=p, xs=xs, ws=ws, xzm=1, wzm=wzm, fill=-1, scratch_images=0)  # noqa: E731
+    return [
+        c("whisper conv1 u8 x i8 w", conv1d(1, 80, 3000, 768, 3, pad_begin=1, pad_end=1), False, True, 1),
+        c("whisper conv1 u8 x u8 w, per channel", conv1d(1, 80, 3000, 768, 3, pad_begin=1, pad_end=1), False, False, 2),
+        c("whisper conv2 u8 x i8 w", conv1d(1, 768, 1500, 768, 3, stride=2, pad_begin=1, pad_end=1), False, True, 1),
+        c("resnet stem 7x7/2", conv_problem(1, 3, 224, 224, 64, 7, 7, stride=2, pad=3), False, True, 1),
+        c("resnet 3x3 56x56", conv_problem(1, 64, 56, 56, 64, 3, 3, pad=1), False, True, 2),
+        c("resnet 1x1 56x56 b2", conv_problem(2, 64, 56, 56, 256, 1, 1), True, True, 1),
+        c("mobilenet depthwise 3x3", conv_problem(1, 96, 28, 28, 96, 3, 3, pad=1, groups=96), False, True, 2),
+    ]

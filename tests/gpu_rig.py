@@ -130,6 +130,16 @@ def abi():
         L.og_util_col_absmax_scale.argtypes = [ctypes.c_void_p, Buf, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_float, Buf]
         L.og_last_error.argtypes = [ctypes.c_void_p]
         L.og_last_error.restype = ctypes.c_char_p
+        L.og_last_kernel.argtypes = [ctypes.c_void_p]
+        L.og_last_kernel.restype = ctypes.c_char_p
+
+        class GemmParams(ctypes.Structure):
+            _fields_ = [(n, ctypes.c_uint32) for n in (
+                "M", "N", "K", "OffA", "OffB", "OffC", "StrideA", "StrideB", "StrideC", "Lda", "Ldb", "Flags", "OffZA",
+                "OffZB", "Epi", "OffBias", "OffScale", "OffFBias", "GridX")]
+
+        L.GemmParams = GemmParams
+        L.og_int8_gemm.argtypes = [ctypes.c_void_p, ctypes.POINTER(GemmParams), ctypes.c_uint32] + [Buf] * 8
         _ABI = L
     return _ABI
 

@@ -188,6 +188,63 @@ def test_gather_bad_arguments_are_rejected(d):
     assert enc.DispatchCount == 1
 
 
+def _conv(batch, cin, h, w, cout, kh, kw, groups=1):
+    p = og.ConvProblem(batch, cin, h, w, cout, kh, kw)
+    p.Groups = groups
+    return p
+
+
+def test_conv_integer_bad_shapes_throw_typed_errors(d):
+    # BadShapesThrowTypedErrors (ConvIntegerTests.cs:309-329), with the argument each names, and the scratch rules of
+    # Encode (ConvIntegerKernels.cs:158-185).
+    conv = og.ConvIntegerKernels(d)
+    x, w = buf(d, og.ElementType.UInt8, 64), buf(d, og.ElementType.Int8, 64)
+    y, f = buf(d, og.ElementType.Int32, 64), buf(d, og.ElementType.Float32, 64)
+    enc = d.BeginCommands()
+    shape_error(lambda: conv.Encode(enc, _conv(1, 3, 4, 4, 4, 3, 3, groups=2), x, w, y), "Groups")
+    shape_error(lambda: conv.Encode(enc, _conv(1, 3, 2, 2, 4, 3, 3), x, w, y), "height")
+    shape_error(lambda: conv.Encode(enc, _conv(1, 3, 8, 8, 4, 3, 3), x, w, y), "x")          # 192 bytes of x
+    shape_error(lambda: conv.Encode(enc, _conv(1, 1, 4, 4, 1, 1, 1), x, w, y, None, og.Int8Operand(w, 64, True)),
+                "wZeroPoint")
+    shape_error(lambda: conv.Encode(enc, _conv(1, 1, 4, 4, 1, 1, 1), f, w, y), "x")
+    shape_error(lambda: conv.Encode(enc, _conv(1, 1, 4, 4, 1, 1, 1), x, w, y, None, None, x, 2), "scratchOffset")
+    shape_error(lambda: conv.Encode(enc, _conv(1, 1, 4, 4, 1, 1, 1), x, w, y, None, None, x, 60), "scratch")
+    shape_error(lambda: conv.Encode(enc, _conv(1, 1, 4, 4, 1, 1, 1), x, w, y, og.Int8Operand(x, 0, True)), "xZeroPoint")
+    shape_error(lambda: conv.Encode(enc, _conv(0, 1, 4, 4, 1, 1, 1), x, w, y), "Batch")
+    p = _conv(1, 1, 4, 4, 1, 1, 1)
+    p.StrideHeight = 0
+    shape_error(lambda: conv.Encode(enc, p, x, w, y), "height stride")
+    p = _conv(1, 1, 4, 4, 1, 1, 1)
+    p.PadLeft = -1
+    shape_error(lambda: conv.Encode(enc, p, x, w, y), "width padding")
+    p = _conv(1, 1, 4, 4, 1, 1, 1)
+    p.Activation = 1
+    shape_error(lambda: conv.Encode(enc, p, x, w, y), "Activation")
+    assert enc.DispatchCount == 0
+    conv.Encode(enc, _conv(1, 1, 4, 4, 1, 1, 1), x, w, y)
+    assert enc.DispatchCount == 1
+
+
+def test_conv_integer_geometry():
+    # ConvProblem.OutHeight / OutWidth (ConvProblem.cs:36-73, 190-206) and the column scratch per image: Groups * K *
+    # round16(OutHeight * OutWidth) here (the reference rounds to 4).
+    p = og.ConvProblem(2, 4, 9, 11, 5, 3, 3)
+    p.StrideHeight = p.StrideWidth = 2
+    p.PadTop = p.PadBottom = p.PadLeft = p.PadRight = 1
+    assert (p.OutHeight, p.OutWidth) == (5, 6)
+    assert og.ConvIntegerKernels.ScratchBytesPerImage(p) == 4 * 9 * 32
+    q = og.ConvProblem.Conv1D(1, 80, 3000, 768, 3, padBegin=1, padEnd=1)
+    assert (q.Height, q.OutHeight, q.OutWidth) == (1, 1, 3000)
+    assert og.ConvIntegerKernels.ScratchBytesPerImage(q) == 240 * 3008
+    r = og.ConvProblem(1, 2, 14, 15, 3, 5, 5)
+    r.DilationHeight = r.DilationWidth = 2
+    r.PadTop = r.PadBottom = r.PadLeft = r.PadRight = 4
+    assert (r.OutHeight, r.OutWidth) == (14, 15)
+    g = og.ConvProblem(2, 6, 9, 10, 6, 3, 3)
+    g.Groups = 6
+    assert og.ConvIntegerKernels.ScratchBytesPerImage(g) == 6 * 9 * 64
+
+
 # ------------------------------------------------------------------ the C ABI
 
 
@@ -322,6 +379,50 @@ def test_gather_abi_validates_before_touching_a_device():
     assert call(GatherParams(Count=24, Inner=3, IdxCount=4, AxisLen=8, Flags=2)) == (1, "Flags")
     assert call(p, status=Buf(addr + 1, 4)) == (1, "status")
     assert call(GatherParams(Count=0, Inner=3, IdxCount=0, AxisLen=8), data=0, idx=0, out=0) == (6, "ctx")
+
+
+class ConvParams(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in (
+        "Batch", "InChannels", "Height", "Width", "OutChannels", "KernelHeight", "KernelWidth", "StrideHeight",
+        "StrideWidth", "DilationHeight", "DilationWidth", "PadTop", "PadLeft", "PadBottom", "PadRight", "Groups",
+        "OffsetX", "OffsetW", "OffsetY", "Flags", "OffXZero", "OffWZero", "GemmFlags")]
+
+
+def test_conv_abi_validates_before_touching_a_device():
+    lib = ctypes.CDLL(og.LIB_PATH)
+    lib.og_conv_integer.argtypes = [ctypes.c_void_p, ctypes.POINTER(ConvParams)] + [Buf] * 6 + [ctypes.c_uint64]
+    lib.og_conv_integer_scratch_bytes.argtypes = [ctypes.POINTER(ConvParams)]
+    lib.og_conv_integer_scratch_bytes.restype = ctypes.c_uint64
+    lib.og_last_error_argument.restype = ctypes.c_char_p
+    lib.og_last_error_argument.argtypes = [ctypes.c_void_p]
+    host = (ctypes.c_uint8 * 65536)()
+    addr = ctypes.addressof(host)
+    none = Buf(None, 0)
+    base = dict(Batch=2, InChannels=4, Height=6, Width=6, OutChannels=8, KernelHeight=3, KernelWidth=3, StrideHeight=1,
+                StrideWidth=1, DilationHeight=1, DilationWidth=1, PadTop=1, PadLeft=1, PadBottom=1, PadRight=1, Groups=1)
+
+    def call(x=288, w=288, y=2304, xz=none, wz=none, scratch=4 * 9 * 48, off=0, **kw):
+        p = ConvParams(**{**base, **kw})
+        st = lib.og_conv_integer(None, ctypes.byref(p), Buf(addr, x), Buf(addr, w), Buf(addr, y), xz, wz,
+                                 Buf(addr, scratch) if scratch else none, off)
+        return st, lib.og_last_error_argument(None).decode()
+
+    assert lib.og_conv_integer_scratch_bytes(ctypes.byref(ConvParams(**base))) == 36 * 48   # K = 36, ldb = 48
+    assert call() == (6, "ctx")
+    assert call(x=287) == (1, "x")
+    assert call(w=287) == (1, "w")
+    assert call(y=2303) == (1, "y")
+    assert call(scratch=36 * 48 - 1) == (1, "scratch")
+    assert call(off=2, scratch=4096) == (1, "scratchOffset")
+    assert call(Groups=3) == (1, "Groups")
+    assert call(KernelHeight=9) == (1, "height")
+    assert call(Flags=0x4) == (1, "xZeroPoint")
+    assert call(Flags=0x8 | 0x10, wz=Buf(addr, 7)) == (1, "wZeroPoint")
+    assert call(Flags=0x10) == (1, "Flags")
+    assert call(GemmFlags=0x1) == (1, "GemmFlags")
+    # One input channel a group (depthwise): no scratch needed; through the column matrix it is.
+    assert call(InChannels=8, Groups=8, x=576, w=72, scratch=0) == (6, "ctx")
+    assert call(InChannels=8, Groups=8, x=576, w=72, scratch=0, Flags=0x20) == (1, "scratch")
 
 
 def test_kernel_choice_is_reported():

@@ -1,5 +1,7 @@
 """GPU parity of the int8 path against the CPU oracle, through the host layer and the C ABI: the reference's
 Int8Tests (tests/RecursiveAI.OneGpu.Kernels.Tests/Int8Tests.cs), case for case, bit-exact."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -364,6 +366,61 @@ def test_products_wider_than_one_grid_axis_are_bit_exact():
             got = bc.Read()
             assert np.count_nonzero(got != want) == 0, (m, n, d.LastKernel)
             bc.Dispose()
+
+
+@pytest.mark.parametrize("config, k, want_kernel", [
+    ("default", 128, "mfma-i8-direct128x128x64"), ("large tile", 128, "mfma-i8-direct256x256x64"),
+    ("default", 96, "mfma-i8-tile128x128x128"), ("large tile", 96, "mfma-i8-tile256x256x64")])
+def test_padded_rows_of_b_with_a_ragged_width(config, k, want_kernel):
+    # B stored K x N in rows of Ldb > N bytes with N not a multiple of 4 (ConvInteger's column matrices have this
+    # shape): the final dword of B's last row holds valid columns and padding, and every column must come through.
+    d = device()
+    gemm = dict(configs(d, True))[config]
+    m, n, ldb = 200, 750, 752
+    rng = np.random.default_rng(k)
+    a = rng.integers(0, 256, m * k, dtype=np.uint8)
+    b = rng.integers(0, 256, k * ldb, dtype=np.uint8)
+    za, zb = np.array([7], np.uint8), rng.integers(0, 256, n, dtype=np.uint8)
+    p = oracle.Gemm(m, n, k, Ldb=ldb)
+    want = oracle.int8_gemm(p, a, False, b, True, (za, False, 0), (zb, True, 0))
+    ba, bb = d.CreateBuffer(a), d.CreateBuffer(b.view(np.int8))
+    bza, bzb = d.CreateBuffer(za), d.CreateBuffer(zb.view(np.int8))
+    bc = d.CreateBufferOf(og.ElementType.Int32, m * n)
+    q = og.Int8GemmProblem(m, n, k)
+    q.Ldb = ldb
+    run(d, lambda e: gemm.EncodeInt32(e, q, ba, bb, bc, og.Int8Operand(bza, 0), og.Int8Operand(bzb, 0, True)))
+    assert d.LastKernel == want_kernel
+    bad = int(np.count_nonzero(bc.Read() != want))
+    say(f"ROW padded B rows, N = 750 in rows of 752 [{d.LastKernel}]: {bad} elements differ")
+    assert bad == 0
+
+
+def test_b_ending_at_its_last_valid_byte_takes_another_kernel():
+    # The same product through the C ABI with B's buffer declared to end at its last valid byte: the dword-wide reads
+    # of the aligned kernels would leave it, so a kernel with byte-exact reads runs instead, with the same sums.
+    d = device()
+    m, n, k, ldb = 200, 750, 128, 752
+    rng = np.random.default_rng(5)
+    a = rng.integers(0, 256, m * k, dtype=np.uint8)
+    b = rng.integers(0, 256, k * ldb, dtype=np.uint8)
+    want = oracle.int8_gemm(oracle.Gemm(m, n, k, Ldb=ldb), a, False, b, True)
+    ba, bb = d.CreateBuffer(a), d.CreateBuffer(b.view(np.int8))
+    bc = d.CreateBufferOf(og.ElementType.Int32, m * n)
+    L = abi()
+    prm = L.GemmParams(M=m, N=n, K=k, Lda=k, Ldb=ldb, Flags=0x002, StrideC=m * n)
+    none = L.Buf(None, 0)
+    exact = L.Buf(bb.DevicePointer, (k - 1) * ldb + n)
+    check(L.og_int8_gemm(d.Context, ctypes.byref(prm), 1, binding(ba), exact, binding(bc), none, none, none, none,
+                         none), d)
+    d.WaitIdle()
+    kernel = L.og_last_kernel(d.Context).decode()
+    assert "direct" not in kernel and "tile" not in kernel, kernel
+    assert np.array_equal(bc.Read(), want)
+    check(L.og_int8_gemm(d.Context, ctypes.byref(prm), 1, binding(ba), binding(bb), binding(bc), none, none, none,
+                         none, none), d)
+    d.WaitIdle()
+    assert L.og_last_kernel(d.Context).decode() == "mfma-i8-direct128x128x64"
+    assert np.array_equal(bc.Read(), want)
 
 
 def test_scratch_semantics():

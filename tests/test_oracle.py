@@ -341,3 +341,119 @@ def test_gather_against_loops_and_numpy_take():
     # A plausible slip (a negative index taken modulo the axis twice, or positions counted from 1) changes these.
     out, bad = oracle.gather(np.arange(4, dtype=np.uint8), [4], 0, [-1, -4, 4, 0, -5])
     assert out.tolist() == [3, 0, 0, 0, 0] and bad == 2
+
+
+# ------------------------------------------------------------------ ConvInteger
+
+def test_conv_integer_onnx_examples():
+    # The ONNX ConvInteger specification's two examples (without and with padding 1).
+    x = np.array([2, 3, 4, 5, 6, 7, 8, 9, 10], np.uint8)
+    c = dict(Batch=1, InChannels=1, Height=3, Width=3, OutChannels=1, KernelHeight=2, KernelWidth=2)
+    assert oracle.conv_integer(c, x, False, np.ones(4, np.uint8), False, np.array([1], np.uint8)).tolist() == \
+        [12, 16, 24, 28]
+    c.update(PadTop=1, PadLeft=1, PadBottom=1, PadRight=1)
+    assert oracle.conv_integer(c, x, False, np.ones(4, np.uint8), False, np.array([1], np.uint8)).tolist() == \
+        [1, 3, 5, 3, 5, 12, 16, 9, 11, 24, 28, 15, 7, 15, 17, 9]
+
+
+def _conv_loops(c, x, xs, w, ws, xz, wz, wz_vec):
+    """The ONNX definition in plain loops (tiny shapes): int64 sums wrapped to int32 at the end."""
+    B, C, H, W, M = c["Batch"], c["InChannels"], c["Height"], c["Width"], c["OutChannels"]
+    KH, KW, G = c["KernelHeight"], c["KernelWidth"], c.get("Groups", 1)
+    SH, SW, DH, DW = c.get("StrideHeight", 1), c.get("StrideWidth", 1), c.get("DilationHeight", 1), c.get("DilationWidth", 1)
+    PT, PL, PB, PR = c.get("PadTop", 0), c.get("PadLeft", 0), c.get("PadBottom", 0), c.get("PadRight", 0)
+    oh = (H + PT + PB - DH * (KH - 1) - 1) // SH + 1
+    ow = (W + PL + PR - DW * (KW - 1) - 1) // SW + 1
+    xv = (x.view(np.int8) if xs else x).astype(np.int64).reshape(B, C, H, W)
+    wv = (w.view(np.int8) if ws else w).astype(np.int64).reshape(M, C // G, KH, KW)
+    xzv = 0 if xz is None else int((xz.view(np.int8) if xs else xz)[0])
+    wzv = np.zeros(M, np.int64) if wz is None else (wz.view(np.int8) if ws else wz).astype(np.int64)
+    if wz is not None and not wz_vec:
+        wzv = np.full(M, wzv[0])
+    y = np.zeros((B, M, oh, ow), np.int64)
+    for n in range(B):
+        for m in range(M):
+            g = m // (M // G)
+            for i in range(oh):
+                for j in range(ow):
+                    acc = 0
+                    for cc in range(C // G):
+                        for kh in range(KH):
+                            for kw in range(KW):
+                                ih, iw = i * SH + kh * DH - PT, j * SW + kw * DW - PL
+                                if 0 <= ih < H and 0 <= iw < W:
+                                    acc += (xv[n, g * (C // G) + cc, ih, iw] - xzv) * (wv[m, cc, kh, kw] - wzv[m])
+                    y[n, m, i, j] = acc
+    return ((y & 0xFFFFFFFF).astype(np.uint32).view(np.int32)).ravel()
+
+
+def _conv_im2col(c, x, xs, w, ws, xz, wz, wz_vec):
+    """An independent lowering: padded input filled with the zero point, windows unfolded with numpy slicing, one
+    int64 matrix product per group (numpy), wrapped to int32."""
+    B, C, H, W, M = c["Batch"], c["InChannels"], c["Height"], c["Width"], c["OutChannels"]
+    KH, KW, G = c["KernelHeight"], c["KernelWidth"], c.get("Groups", 1)
+    SH, SW, DH, DW = c.get("StrideHeight", 1), c.get("StrideWidth", 1), c.get("DilationHeight", 1), c.get("DilationWidth", 1)
+    PT, PL, PB, PR = c.get("PadTop", 0), c.get("PadLeft", 0), c.get("PadBottom", 0), c.get("PadRight", 0)
+    xzv = 0 if xz is None else int((xz.view(np.int8) if xs else xz)[0])
+    xv = (x.view(np.int8) if xs else x).astype(np.int64).reshape(B, C, H, W) - xzv
+    xp = np.zeros((B, C, H + PT + PB, W + PL + PR), np.int64)
+    xp[:, :, PT:PT + H, PL:PL + W] = xv
+    oh = (H + PT + PB - DH * (KH - 1) - 1) // SH + 1
+    ow = (W + PL + PR - DW * (KW - 1) - 1) // SW + 1
+    cols = np.stack([xp[:, :, kh * DH:kh * DH + SH * (oh - 1) + 1:SH, kw * DW:kw * DW + SW * (ow - 1) + 1:SW]
+                     for kh in range(KH) for kw in range(KW)], axis=2)          # [B, C, KH*KW, oh, ow]
+    wzv = np.zeros(M, np.int64) if wz is None else (wz.view(np.int8) if ws else wz).astype(np.int64)
+    if wz is not None and not wz_vec:
+        wzv = np.full(M, wzv[0])
+    wv = (w.view(np.int8) if ws else w).astype(np.int64).reshape(M, -1) - wzv[:, None]
+    cg, mg = C // G, M // G
+    y = np.zeros((B, M, oh * ow), np.int64)
+    for g in range(G):
+        a = wv[g * mg:(g + 1) * mg]                                              # [mg, cg*KH*KW]
+        bcol = cols[:, g * cg:(g + 1) * cg].reshape(B, cg * KH * KW, oh * ow)
+        y[:, g * mg:(g + 1) * mg] = np.einsum("mk,bkn->bmn", a, bcol)
+    return ((y & 0xFFFFFFFF).astype(np.uint32).view(np.int32)).ravel()
+
+
+CONV_PIN_CASES = [
+    dict(Batch=2, InChannels=4, Height=5, Width=6, OutChannels=3, KernelHeight=3, KernelWidth=3, PadTop=1, PadLeft=1,
+         PadBottom=1, PadRight=1),
+    dict(Batch=1, InChannels=3, Height=7, Width=5, OutChannels=2, KernelHeight=3, KernelWidth=2, StrideHeight=2,
+         PadTop=2, PadRight=3),
+    dict(Batch=1, InChannels=2, Height=8, Width=9, OutChannels=2, KernelHeight=3, KernelWidth=3, DilationHeight=2,
+         DilationWidth=2, PadTop=2, PadLeft=2, PadBottom=2, PadRight=2),
+    dict(Batch=2, InChannels=4, Height=4, Width=4, OutChannels=6, KernelHeight=3, KernelWidth=3, PadTop=1, PadLeft=1,
+         PadBottom=1, PadRight=1, Groups=2),
+    dict(Batch=1, InChannels=3, Height=5, Width=5, OutChannels=3, KernelHeight=3, KernelWidth=3, Groups=3),
+]
+
+
+def test_conv_integer_against_loops_and_an_im2col_product():
+    rng = np.random.default_rng(11)
+    for i, c in enumerate(CONV_PIN_CASES):
+        for xs, ws, zmode in ((False, True, 2), (True, False, 1), (True, True, 0), (False, False, 2)):
+            x = rng.integers(0, 256, c["Batch"] * c["InChannels"] * c["Height"] * c["Width"], dtype=np.uint8)
+            w = rng.integers(0, 256, c["OutChannels"] * (c["InChannels"] // c.get("Groups", 1)) * c["KernelHeight"]
+                             * c["KernelWidth"], dtype=np.uint8)
+            xz = None if zmode == 0 else rng.integers(0, 256, 1, dtype=np.uint8)
+            wz = None if zmode == 0 else rng.integers(0, 256, c["OutChannels"] if zmode == 2 else 1, dtype=np.uint8)
+            got = oracle.conv_integer(c, x, xs, w, ws, xz, wz, zmode == 2)
+            assert np.array_equal(got, _conv_loops(c, x, xs, w, ws, xz, wz, zmode == 2)), (i, xs, ws, zmode)
+            assert np.array_equal(got, _conv_im2col(c, x, xs, w, ws, xz, wz, zmode == 2)), (i, xs, ws, zmode)
+
+
+def test_conv_integer_pointwise_is_a_matrix_product():
+    # A 1x1 convolution is W [Cout, Cin] times X [Cin, H*W] per image; with extreme bytes the int32 sums wrap.
+    rng = np.random.default_rng(3)
+    c = dict(Batch=2, InChannels=300, Height=3, Width=4, OutChannels=5, KernelHeight=1, KernelWidth=1)
+    x = np.full(2 * 300 * 12, 255, np.uint8)
+    w = rng.integers(0, 256, 5 * 300, dtype=np.uint8)
+    got = oracle.conv_integer(c, x, False, w, False).reshape(2, 5, 12)
+    want = w.astype(np.int64).reshape(5, 300) @ x.astype(np.int64).reshape(2, 300, 12)
+    assert np.array_equal(got, want.astype(np.int32))
+    x = np.full(2 * 300 * 12, 0x80, np.uint8)                         # int8 -128
+    w = np.full(5 * 300, 0x80, np.uint8)
+    xz, wz = np.array([0x7F], np.uint8), np.array([0x7F], np.uint8)   # int8 127: each term (-255)^2
+    got = oracle.conv_integer(c, x, True, w, True, xz, wz)
+    assert np.all(got == np.int32(((300 * 255 * 255) & 0xFFFFFFFF) - (1 << 32) if (300 * 255 * 255) >= (1 << 31)
+                                  else 300 * 255 * 255))
