@@ -432,6 +432,64 @@ def embedding_gather(d, steps, warmup, tokens, check=True, vocab=250002, hidden=
     return res
 
 
+def resnet50_convs() -> list:
+    """The 53 convolutions of ResNet-50 (v1.5: the stride of a stage's first block in its 3 x 3) at 224 x 224, as
+    (in channels, size, out channels, kernel, stride, pad)."""
+    layers = [(3, 224, 64, 7, 2, 3)]
+    cin, size = 64, 56
+    for blocks, mid, out, stride in ((3, 64, 256, 1), (4, 128, 512, 2), (6, 256, 1024, 2), (3, 512, 2048, 2)):
+        for b in range(blocks):
+            s = stride if b == 0 else 1
+            layers.append((cin, size, mid, 1, 1, 0))
+            layers.append((mid, size, mid, 3, s, 1))
+            osize = size // s
+            layers.append((mid, osize, out, 1, 1, 0))
+            if b == 0:
+                layers.append((cin, size, out, 1, s, 0))   # the projection shortcut
+            cin, size = out, osize
+    return layers
+
+
+def conv_workload(d, steps, warmup, which):
+    """ConvInteger layers at batch 1, u8 activations with a zero point, int8 weights with a zero point per output
+    channel, int32 out: 'resnet50' runs all 53 convolutions of ResNet-50 back to back as one step; 'whisper' the
+    two convolutions of the Whisper-small stem; 'depthwise' MobileNet's 96-channel 3 x 3 depthwise layer at 28 x 28."""
+    if which == "resnet50":
+        layers = [(1, c, h, h, o, k, k, s, p, 1) for (c, h, o, k, s, p) in resnet50_convs()]
+    elif which == "whisper":
+        layers = [(1, 80, 1, 3000, 768, 1, 3, 1, 1, 1), (1, 768, 1, 3000, 768, 1, 3, 2, 1, 1)]
+    else:
+        layers = [(1, 96, 28, 28, 96, 3, 3, 1, 1, 96)]
+    conv = og.ConvIntegerKernels(d)
+    items, ops = [], 0.0
+    for i, (b, c, h, w, o, kh, kw, st, pad, g) in enumerate(layers):
+        q = og.ConvProblem(b, c, h, w, o, kh, kw)
+        q.StrideWidth = st
+        q.StrideHeight = st if h > 1 else 1
+        q.PadLeft = q.PadRight = pad
+        q.PadTop = q.PadBottom = pad if h > 1 else 0
+        q.Groups = g
+        x = synth(d, og.ElementType.UInt8, b * c * h * w, 7, 100 + 3 * i, 0, 255, 0)
+        wt = synth(d, og.ElementType.Int8, o * (c // g) * kh * kw, 7, 101 + 3 * i, -127, 127, 0)
+        wz = synth(d, og.ElementType.Int8, o, 7, 102 + 3 * i, -8, 8, 0)
+        xz = d.CreateBuffer(np.array([128, 0, 0, 0], np.uint8))
+        y = d.CreateBufferOf(og.ElementType.Int32, b * o * q.OutHeight * q.OutWidth)
+        items.append((q, x, wt, y, xz, wz))
+        ops += 2.0 * b * o * q.OutHeight * q.OutWidth * (c // g) * kh * kw
+
+    def step(e, i):
+        for q, x, wt, y, xz, wz in items:
+            conv.Encode(e, q, x, wt, y, og.Int8Operand(xz, 0), og.Int8Operand(wz, 0, True))
+
+    wall, region, times = timed(d, step, steps, warmup)
+    per = {}
+    for t, k in times:
+        per.setdefault(k, []).append(t)
+    return {"layers": len(layers), "ops": ops, "wall_s": wall, "step_mean_ms": region / steps * 1e3,
+            "dispatches_per_step": len(times) // steps,
+            "kernel_ms_per_step": {k: sum(v) / steps for k, v in per.items()}}
+
+
 def only(d, name, steps, warmup):
     """One workload alone (for rocprofv3 runs of committed files); prints a one-line summary."""
     if name == "c4":
@@ -445,6 +503,8 @@ def only(d, name, steps, warmup):
         r = c5_batched(d, steps, warmup, check=False)
     elif name in ("c2q", "c2q2"):
         r = qlinear_c2(d, steps, warmup, fused=name == "c2q", check=False)
+    elif name in ("resnet50", "whisper", "depthwise"):
+        r = conv_workload(d, steps, warmup, name)
     elif name.startswith("gather"):
         r = embedding_gather(d, steps, warmup, int(name[6:] or 4096), check=False)
     elif name == "copy":
@@ -466,7 +526,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline configuration only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["c4", "c4const", "c4nt", "c4plain", "c4plainnt", "gemv1", "gemv4", "gemv16", "c2", "c2q", "c2q2", "c5", "gather4096", "gather65536", "copy", "vendor"],
+    ap.add_argument("--only", choices=["c4", "c4const", "c4nt", "c4plain", "c4plainnt", "gemv1", "gemv4", "gemv16", "c2", "c2q", "c2q2", "c5", "gather4096", "gather65536", "resnet50", "whisper", "depthwise", "copy", "vendor"],
                     help="run one workload alone and print its summary (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -535,6 +595,14 @@ def main():
                                                      "frac": gbs / PEAK_HBM_GBS, "kernel": r["kernel"],
                                                      "check": r["check"]}
             log(json.dumps(configs[f"embedding_gather_{tokens}"]))
+        for which in ("resnet50", "whisper", "depthwise"):
+            log(f"ConvInteger: {which} at batch 1")
+            r = conv_workload(d, args.steps, args.warmup, which)
+            configs[f"conv_{which}_b1"] = {"layers": r["layers"], "step_mean_us": r["step_mean_ms"] * 1e3,
+                                            "tops": r["ops"] / (r["step_mean_ms"] * 1e-3) / 1e12,
+                                            "dispatches_per_step": r["dispatches_per_step"],
+                                            "kernel_us_per_step": {k: v * 1e3 for k, v in r["kernel_ms_per_step"].items()}}
+            log(json.dumps(configs[f"conv_{which}_b1"]))
         log("config 5: batched 32 x 512 x 4096 x 4096")
         r = c5_batched(d, max(3, args.steps // 5), 2)
         configs["c5_batched"] = {"tops_kernel": r["ops"] / (r["kernel_mean_ms"] * 1e-3) / 1e12,

@@ -258,7 +258,9 @@ uint64_t og_conv_integer_scratch_bytes(const og_conv_params *params);
  * padding add nothing. Replaces ConvIntegerKernels.Encode's dispatches (ConvIntegerKernels.cs:97-253): per chunk of
  * images that fits the scratch (bytes from scratch_offset, a multiple of 4), the column matrix is packed and then
  * multiplied, one batched product per group (the reference records one product per image and group). With one input
- * channel a group (depthwise) the library convolves directly and the scratch is not used (may be absent). */
+ * channel a group (depthwise) the library convolves directly, and a 1 x 1 window with unit strides and no padding
+ * whose image rows are whole 16-byte multiples from a 16-byte aligned start multiplies the input as it lies; neither
+ * uses the scratch (it may be absent). */
 int og_conv_integer(og_ctx *ctx, const og_conv_params *params, og_buffer x, og_buffer w, og_buffer y, og_buffer xz,
                     og_buffer wz, og_buffer scratch, uint64_t scratch_offset);
 

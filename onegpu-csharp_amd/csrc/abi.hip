@@ -755,8 +755,17 @@ int og_conv_integer(og_ctx *ctx, const og_conv_params *p, og_buffer x, og_buffer
     const uint64_t nwz = (p->Flags & OG_CONV_WZ_PER_CHANNEL) ? p->OutChannels : 1;
     if ((p->Flags & OG_CONV_WZ) && (!wz.ptr || !fits(p->OffWZero, nwz, wz))) return fail(ctx, OG_ERR_INVALID_ARG, "wZeroPoint", "elements %u..%llu reach past the buffer", p->OffWZero, (unsigned long long)(p->OffWZero + nwz));
     const bool depthwise = geo.cin_g == 1 && !(p->Flags & OG_CONV_NO_DEPTHWISE);
+    // A 1 x 1 window with unit strides and no padding: image n's channels of group g already are the product's B
+    // operand, [cin_g x H*W] in rows of H*W bytes, so there is nothing to pack, as long as those rows suit the
+    // LDS-DMA kernel (whole 16-byte chunks from a 16-byte aligned start); otherwise the packed copy, whose rows are
+    // padded to 16 bytes, is the faster operand.
+    const int64_t plane = (int64_t)p->Height * p->Width;
+    const bool pointwise = !depthwise && p->KernelHeight == 1 && p->KernelWidth == 1 && p->StrideHeight == 1 &&
+                           p->StrideWidth == 1 && p->PadTop == 0 && p->PadLeft == 0 && p->PadBottom == 0 &&
+                           p->PadRight == 0 && plane % 16 == 0 &&
+                           ((uintptr_t)static_cast<const uint8_t *>(x.ptr) + p->OffsetX) % 16 == 0;
     int64_t per_chunk = B;
-    if (!depthwise) {
+    if (!depthwise && !pointwise) {
         if (scratch_offset & 3) return fail(ctx, OG_ERR_INVALID_ARG, "scratchOffset", "offset %llu must be a multiple of 4", (unsigned long long)scratch_offset);
         if (!scratch.ptr || !fits(scratch_offset, (uint64_t)geo.per_image, scratch)) return fail(ctx, OG_ERR_INVALID_ARG, "scratch", "one image's columns (%lld bytes from %llu) reach past the buffer", (long long)geo.per_image, (unsigned long long)scratch_offset);
         per_chunk = std::min<int64_t>(B, (int64_t)((scratch.bytes - scratch_offset) / (uint64_t)geo.per_image));
@@ -799,8 +808,40 @@ int og_conv_integer(og_ctx *ctx, const og_conv_params *p, og_buffer x, og_buffer
         st = launch(ctx, "og_conv_integer", [&](const char **k) { return og::launch_conv_depthwise(a, ctx->stream, k); });
         return st == OG_OK ? ok(ctx) : st;
     }
-    uint8_t *cols = static_cast<uint8_t *>(scratch.ptr) + scratch_offset;
     const int64_t ncols = geo.oh * geo.ow;
+    // The products: A = group g's weights [cout_g x k] (its zero point per row = per output channel), B = the group's
+    // column matrix [k x ncols] (x's zero point), one batch entry per image.
+    auto product = [&](const uint8_t *b, int64_t ldb, int64_t stride_b, int64_t b_bytes, int64_t first, int32_t images,
+                       int64_t g) {
+        og::GemmArgs ga{};
+        ga.A = wb + g * geo.cout_g * geo.k;
+        ga.B = b;
+        ga.C = yb + first * geo.y_image + g * geo.cout_g * ncols;
+        ga.ZA = wzp ? wzp + ((p->Flags & OG_CONV_WZ_PER_CHANNEL) ? g * geo.cout_g : 0) : nullptr;
+        ga.ZB = xzp;
+        ga.strideA = 0;
+        ga.strideB = stride_b;
+        ga.strideC = geo.y_image;
+        ga.b_bytes = b_bytes;
+        ga.M = (int32_t)geo.cout_g;
+        ga.N = (int32_t)ncols;
+        ga.K = (int32_t)geo.k;
+        ga.batch = images;
+        ga.lda = (int32_t)geo.k;
+        ga.ldb = (int32_t)ldb;
+        ga.flags = p->GemmFlags | ((p->Flags & OG_CONV_W_INT8) ? OG_GEMM_A_INT8 : 0u) |
+                   ((p->Flags & OG_CONV_X_INT8) ? OG_GEMM_B_INT8 : 0u) | (wzp ? OG_GEMM_ZA : 0u) |
+                   ((p->Flags & OG_CONV_WZ_PER_CHANNEL) ? OG_GEMM_ZA_PER_ROW : 0u) | (xzp ? OG_GEMM_ZB : 0u);
+        ga.epi = 0;
+        return launch_product(ctx, ga);
+    };
+    if (pointwise) {
+        for (int64_t g = 0; g < p->Groups && st == OG_OK; g++)
+            st = product(xb + g * geo.cin_g * plane, plane, geo.x_image,
+                         (int64_t)(x.bytes - p->OffsetX) - g * geo.cin_g * plane, 0, (int32_t)B, g);
+        return st == OG_OK ? ok(ctx) : st;
+    }
+    uint8_t *cols = static_cast<uint8_t *>(scratch.ptr) + scratch_offset;
     for (int64_t first = 0; first < B && st == OG_OK; first += per_chunk) {
         const int32_t images = (int32_t)std::min<int64_t>(per_chunk, B - first);
         og::ConvPackArgs pa{};
@@ -826,31 +867,9 @@ int og_conv_integer(og_ctx *ctx, const og_conv_params *p, og_buffer x, og_buffer
         pa.pw = (int32_t)p->PadLeft;
         pa.ldb = geo.ldb;
         st = launch(ctx, "og_conv_integer", [&](const char **k) { return og::launch_conv_pack(pa, ctx->stream, k); });
-        // The products: A = the group's weights [cout_g x k] (zero point per row = per output channel), B = its
-        // column matrix [k x ncols] (x's zero point), one batch entry per image of the chunk.
-        for (int64_t g = 0; g < p->Groups && st == OG_OK; g++) {
-            og::GemmArgs ga{};
-            ga.A = wb + g * geo.cout_g * geo.k;
-            ga.B = cols + g * geo.k * geo.ldb;
-            ga.C = yb + first * geo.y_image + g * geo.cout_g * ncols;
-            ga.ZA = wzp ? wzp + ((p->Flags & OG_CONV_WZ_PER_CHANNEL) ? g * geo.cout_g : 0) : nullptr;
-            ga.ZB = xzp;
-            ga.strideA = 0;
-            ga.strideB = p->Groups * geo.k * geo.ldb;
-            ga.strideC = geo.y_image;
-            ga.b_bytes = (int64_t)(scratch.bytes - scratch_offset) - g * geo.k * geo.ldb;
-            ga.M = (int32_t)geo.cout_g;
-            ga.N = (int32_t)ncols;
-            ga.K = (int32_t)geo.k;
-            ga.batch = images;
-            ga.lda = (int32_t)geo.k;
-            ga.ldb = (int32_t)geo.ldb;
-            ga.flags = p->GemmFlags | ((p->Flags & OG_CONV_W_INT8) ? OG_GEMM_A_INT8 : 0u) |
-                       ((p->Flags & OG_CONV_X_INT8) ? OG_GEMM_B_INT8 : 0u) | (wzp ? OG_GEMM_ZA : 0u) |
-                       ((p->Flags & OG_CONV_WZ_PER_CHANNEL) ? OG_GEMM_ZA_PER_ROW : 0u) | (xzp ? OG_GEMM_ZB : 0u);
-            ga.epi = 0;
-            st = launch_product(ctx, ga);
-        }
+        for (int64_t g = 0; g < p->Groups && st == OG_OK; g++)
+            st = product(cols + g * geo.k * geo.ldb, geo.ldb, p->Groups * geo.k * geo.ldb,
+                         (int64_t)(scratch.bytes - scratch_offset) - g * geo.k * geo.ldb, first, images, g);
     }
     return st == OG_OK ? ok(ctx) : st;
 }

@@ -1080,6 +1080,11 @@ void ConvIntegerKernels::Encode(GpuCommandEncoder &encoder, const ConvProblem &p
     if (perImage > Check::MaxElements)
         throw GpuKernelShapeException(kConv, "InChannels", "the column matrix of one image needs " + std::to_string(perImage) + " bytes, more than the supported sizes");
     const bool depthwise = DirectDepthwise && p.InChannels == p.Groups;   // one input channel a group: convolved directly
+    // x is the matrix as it lies (the library's rule: a 1 x 1 window, unit strides, no padding, 16-byte rows and start)
+    const bool pointwise = p.KernelHeight == 1 && p.KernelWidth == 1 && p.StrideHeight == 1 && p.StrideWidth == 1 &&
+                           p.PadTop == 0 && p.PadLeft == 0 && p.PadBottom == 0 && p.PadRight == 0 &&
+                           ((int64_t)p.Height * p.Width) % 16 == 0 &&
+                           ((uintptr_t)x.DevicePointer() + (uintptr_t)p.OffsetX) % 16 == 0;
     GpuBuffer columns;
     int64_t columnBase = 0;
     if (scratch) {
@@ -1092,7 +1097,7 @@ void ConvIntegerKernels::Encode(GpuCommandEncoder &encoder, const ConvProblem &p
                                                                 " (one image's columns) reach past the buffer of " + std::to_string(scratch->Length()));
         columns = *scratch;
         columnBase = scratchOffset;
-    } else if (!depthwise) {
+    } else if (!depthwise && !pointwise) {
         const int64_t ownScratchBytes = int64_t(64) << 20;   // ConvIntegerKernels.cs:33
         const int64_t imagesPerChunk = std::clamp<int64_t>(ownScratchBytes / perImage, 1, p.Batch);
         columns = Own(x.Type(), imagesPerChunk * perImage);

@@ -423,6 +423,14 @@ def test_conv_abi_validates_before_touching_a_device():
     # One input channel a group (depthwise): no scratch needed; through the column matrix it is.
     assert call(InChannels=8, Groups=8, x=576, w=72, scratch=0) == (6, "ctx")
     assert call(InChannels=8, Groups=8, x=576, w=72, scratch=0, Flags=0x20) == (1, "scratch")
+    # A 1 x 1 window with unit strides and no padding over rows of 16-byte multiples multiplies x as it lies: no
+    # scratch either (6 x 6 = 36-byte rows are packed; 8 x 8 = 64-byte rows are not).
+    pw = dict(KernelHeight=1, KernelWidth=1, PadTop=0, PadLeft=0, PadBottom=0, PadRight=0)
+    aligned = (addr + 15) & ~15
+    st = lib.og_conv_integer(None, ctypes.byref(ConvParams(**{**base, **pw, "Height": 8, "Width": 8})),
+                             Buf(aligned, 512), Buf(addr, 288), Buf(addr, 4096), none, none, none, 0)
+    assert (st, lib.og_last_error_argument(None).decode()) == (6, "ctx")
+    assert call(scratch=0, **pw)[1] == "scratch"
 
 
 def test_kernel_choice_is_reported():
