@@ -297,6 +297,12 @@ def conv_edge_cases() -> list:
         for fill in (0, 127, 128, 255):
             cases.append(dict(name=f"extremes {fill} s{s}", p=conv_problem(1, 17, 6, 6, 3, 3, 3, pad=1),
                               xs=(s & 1) != 0, ws=(s & 2) != 0, xzm=1, wzm=2, fill=fill, scratch_images=0))
+    # This library's own paths: 1 x 1 unit-stride convolutions over 16-byte image rows multiply x in place (grouped,
+    # and with a per-channel zero point), and the same shape with x at an odd offset goes through the pack.
+    cases += conv_spread("1x1 in place, groups 2", conv_problem(2, 8, 8, 8, 6, 1, 1, groups=2))
+    pw_off = conv_problem(2, 4, 4, 8, 5, 1, 1)
+    pw_off.update(OffsetX=3)
+    cases += conv_spread("1x1 at an odd offset", pw_off)
     cases.append(dict(name="chunked batch, scratch for 1 image", p=conv_problem(3, 3, 8, 8, 4, 3, 3, pad=1), xs=False,
                       ws=False, xzm=1, wzm=1, fill=-1, scratch_images=1))
     cases.append(dict(name="grouped, scratch for 2 images", p=conv_problem(3, 4, 8, 8, 6, 3, 3, pad=1, groups=2),
