@@ -441,7 +441,9 @@ int og_int8_gemm_kernel_name(const og_int8_gemm_params *p, uint32_t batch, char 
     if (k == og::GemmKernel::Tiled) {
         const bool large = (p->Flags & OG_GEMM_LARGE_TILE) || og::tiled_uses_large(g.M, g.N, b);
         if (!og::tiled_fast_ok(g)) name = "mfma-i8-generic128x128x64";
-        else if (og::direct_ok(g)) name = large ? "mfma-i8-direct256x256x64" : "mfma-i8-direct128x128x64";
+        else if (og::direct_ok(g))
+            name = large ? "mfma-i8-direct256x256x64"
+                         : (og::direct_split(g) > 1 ? "mfma-i8-direct128x128x64-splitk" : "mfma-i8-direct128x128x64");
         else name = large ? "mfma-i8-tile256x256x64" : "mfma-i8-tile128x128x128";
     }
     // The few-rows products take the tiled kernel when the operands' rows are aligned.
@@ -465,9 +467,24 @@ static int launch_product(og_ctx *ctx, const og::GemmArgs &g)
     case og::GemmKernel::Portable:
         st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_portable(g, ctx->stream, n); });
         break;
-    case og::GemmKernel::Tiled:
+    case og::GemmKernel::Tiled: {
+        // A grid that fills under half the chip splits along K when it takes the 128 x 128 direct kernel.
+        const int ks = og::tiled_fast_ok(g) && og::direct_ok(g) && !og::tiled_uses_large(g.M, g.N, g.batch)
+                           ? og::direct_split(g) : 1;
+        if (ks > 1) {
+            st = ensure_partials(ctx, og::direct_split_workspace_bytes(g, ks));
+            if (st != OG_OK) return st;
+            st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_direct_split(g, ctx->ws, ctx->stream, n, ks, 0); });
+            if (st == OG_OK) {
+                const char *product = ctx->last_kernel;   // named for the product, not the summing pass
+                st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_direct_split(g, ctx->ws, ctx->stream, n, ks, 1); });
+                ctx->last_kernel = product;
+            }
+            break;
+        }
         st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_tiled(g, ctx->stream, n); });
         break;
+    }
     case og::GemmKernel::RowTiles:
         st = ensure_partials(ctx, og::gemv_tiles_workspace_bytes(g));
         if (st != OG_OK) return st;

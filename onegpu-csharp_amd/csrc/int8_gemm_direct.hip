@@ -3,6 +3,8 @@
 // int8_gemm_direct128.hip).
 #include "int8_gemm_direct.hpp"
 
+#include <algorithm>
+
 namespace og {
 
 // The direct kernel's conditions: K a multiple of the stage depth (64), 16-byte aligned rows for both operands,
@@ -27,9 +29,102 @@ hipError_t launch_gemm_direct(const GemmArgs &g, hipStream_t s, const char **ker
     *kernel = large ? "mfma-i8-direct256x256x64" : "mfma-i8-direct128x128x64";
     if (blocks <= 0) return hipSuccess;
     const dim3 grid((uint32_t)blocks);
-    if (!large) launch_direct128(g, s, grid, tn, tm);
+    if (!large) launch_direct128(g, s, grid, tn, tm, 1, g.K);
     else if (g.flags & OG_GEMM_TRANSPOSE_B) launch_direct_nk256(g, s, grid, tn, tm);
-    else launch_direct_t<256, false>(g, s, grid, tn, tm);
+    else launch_direct_t<256, false>(g, s, grid, tn, tm, 1, g.K);
+    return hipGetLastError();
+}
+
+int direct_split(const GemmArgs &g)
+{
+    // Grids that fill under half the chip with 128 x 128 tiles, cut along K into slices of at least 4 stages, with
+    // no more workgroups than CUs (a second round would undo the gain). The split pays when the stages it takes off
+    // each workgroup's serial walk outweigh what the split adds: every slice's int32 result written and read back, and
+    // a launch. Conservative costs from MI355X measurements: 0.25 us per 64-deep stage of one 128 tile (C2's 12 stages
+    // take 13.2 us and Whisper's 36 stages 22 us, of which about 9 us are a workgroup's fixed cost), 3 us a launch,
+    // 4 TB/s for the partial sums.
+    if (g.K <= 0 || g.M <= 0 || g.N <= 0 || (g.flags & OG_GEMM_LARGE_TILE)) return 1;
+    const int64_t tiles = (int64_t)((g.M + 127) / 128) * ((g.N + 127) / 128) * g.batch;
+    const int64_t stages = g.K / DBK;
+    if (tiles * 2 > kSplitTargetTiles || stages < 8) return 1;
+    int64_t ks = std::min<int64_t>(kSplitTargetTiles / tiles, stages / 4);
+    // The partial sums (int32, every slice's whole result) stay within the workspace's budget and int32 indexing.
+    const int64_t per_slice = (int64_t)g.M * g.N * g.batch * 4;
+    ks = std::min<int64_t>(ks, kSplitMaxBytes / std::max<int64_t>(per_slice, 1));
+    if (ks < 2) return 1;
+    // As many slices as slices of that length need, so that none is empty.
+    const int64_t per = (stages + ks - 1) / ks;
+    ks = (stages + per - 1) / per;
+    const double saved_us = 0.25 * (double)(stages - per);
+    const double cost_us = 3.0 + (double)(2 * ks + 1) * (double)per_slice / 4e6;
+    return ks >= 2 && saved_us > 1.2 * cost_us ? (int)ks : 1;
+}
+
+uint64_t direct_split_workspace_bytes(const GemmArgs &g, int ks)
+{
+    return (uint64_t)ks * (uint64_t)g.M * (uint64_t)g.N * (uint64_t)g.batch * 4u;
+}
+
+namespace {
+
+// Slice kc's partial for (b, m, n) is parts[((b * ks + kc) * M + m) * N + n]; their sum gets the bias and the epilogue.
+// V4: four neighbouring columns a thread (N a multiple of 4), one 16-byte load per slice.
+template <bool V4>
+__global__ __launch_bounds__(256) void k_splitk_sum(GemmArgs g, int32_t ks, const int32_t *parts)
+{
+    const int64_t mn = (int64_t)g.M * g.N, per = V4 ? mn / 4 : mn, total = per * g.batch;
+    for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += (int64_t)gridDim.x * 256) {
+        const int64_t b = t / per, r = (t - b * per) * (V4 ? 4 : 1);
+        const int32_t n = (int32_t)(r % g.N);
+        const int32_t *p = parts + b * ks * mn + r;
+        if constexpr (V4) {
+            uint4 sum = make_uint4(0u, 0u, 0u, 0u);
+            for (int32_t kc = 0; kc < ks; kc++) {
+                const uint4 v = *reinterpret_cast<const uint4 *>(p + kc * mn);
+                sum.x += v.x;
+                sum.y += v.y;
+                sum.z += v.z;
+                sum.w += v.w;
+            }
+            const int64_t c = b * g.strideC + r;
+            store_value(g, c, n, sum.x);
+            store_value(g, c + 1, n + 1, sum.y);
+            store_value(g, c + 2, n + 2, sum.z);
+            store_value(g, c + 3, n + 3, sum.w);
+        } else {
+            uint32_t sum = 0;
+            for (int32_t kc = 0; kc < ks; kc++) sum += (uint32_t)p[kc * mn];
+            store_value(g, b * g.strideC + r, n, sum);
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_gemm_direct_split(const GemmArgs &g, const Workspace &ws, hipStream_t s, const char **kernel, int ks,
+                                    int step)
+{
+    const int32_t tn = (g.N + 127) / 128, tm = (g.M + 127) / 128;
+    if (step == 0) {
+        *kernel = "mfma-i8-direct128x128x64-splitk";
+        // Each slice: the whole k range's product machinery on its slice, int32 sums into the partials.
+        GemmArgs gs = g;
+        gs.C = ws.partials;
+        gs.strideC = (int64_t)g.M * g.N;
+        gs.batch = g.batch * ks;
+        gs.epi = 0;
+        const int64_t stages = g.K / DBK;
+        const int32_t kslice = (int32_t)((stages + ks - 1) / ks) * DBK;
+        const int64_t blocks = (int64_t)tn * tm * gs.batch;
+        launch_direct128(gs, s, dim3((uint32_t)blocks), tn, tm, ks, kslice);
+        return hipGetLastError();
+    }
+    *kernel = "splitk-sum";
+    const bool v4 = g.N % 4 == 0;   // the partials start 256-byte aligned, so each row of 4-column groups is aligned
+    const int64_t total = (int64_t)g.M * g.N * g.batch / (v4 ? 4 : 1);
+    const int64_t wgs = std::min<int64_t>((total + 255) / 256, int64_t(1) << 20);
+    if (v4) hipLaunchKernelGGL(k_splitk_sum<true>, dim3((uint32_t)wgs), dim3(256), 0, s, g, (int32_t)ks, ws.partials);
+    else hipLaunchKernelGGL(k_splitk_sum<false>, dim3((uint32_t)wgs), dim3(256), 0, s, g, (int32_t)ks, ws.partials);
     return hipGetLastError();
 }
 

@@ -162,7 +162,12 @@ __device__ __forceinline__ void sched_block()
 // FLIP_A / FLIP_B: the operand is unsigned (moved to the signed domain fragment by fragment). SUM_A / SUM_B: the row
 // sums of A / column sums of B are needed (the other operand's zero point in the signed domain can be non-zero).
 template <int BT, bool TRANS_B, bool SUM_A, bool SUM_B, bool FLIP_A, bool FLIP_B>
-__global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t tiles_n, int32_t tiles_m)
+// ksplit > 1: the product is cut along K into slices of kslice bytes (a multiple of 64); g.batch counts batch entries
+// times slices, and slice kc of batch entry b computes the int32 sums of its k range with the zero points applied
+// (every correction term is linear in the slice) into batch entry b * ksplit + kc of C, which is then a dense int32
+// partial buffer (the caller adds the slices and applies the epilogue). ksplit = 1: the whole product.
+__global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t tiles_n, int32_t tiles_m, int32_t ksplit,
+                                                          int32_t kslice)
 {
     using D = DCfg<BT>;
     constexpr int DBM = BT, DBN = BT, A_STAGE = D::A_STAGE, STAGE = D::STAGE, LOADS_A = D::LOADS_A;
@@ -182,7 +187,9 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
     const int64_t nblocks = tiles * g.batch;
     int64_t bid = blockIdx.x;
     if ((nblocks & 7) == 0) bid = (bid & 7) * (nblocks >> 3) + (bid >> 3);
-    const int32_t batch = (int32_t)(bid / tiles);
+    const int32_t bsplit = (int32_t)(bid / tiles);           // batch entry of C
+    const int32_t kc = bsplit % ksplit, batch = bsplit / ksplit;   // k slice; batch entry of A and B
+    const int32_t K0 = kc * kslice;
     const int64_t t = bid % tiles;
     int32_t tm, tn;
     {
@@ -195,7 +202,7 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
         tn = (int32_t)(in / gsize);
     }
     const int32_t m0 = tm * DBM, n0 = tn * DBN;
-    const int32_t lda = g.lda, ldb = g.ldb, K = g.K;
+    const int32_t lda = g.lda, ldb = g.ldb, K = max(0, min(kslice, g.K - K0));   // an empty slice adds zero
     constexpr bool a_signed = !FLIP_A, b_signed = !FLIP_B;
 
     // The epilogue's per-row and per-column parameters, fetched now so that their latency hides behind the loop:
@@ -212,16 +219,16 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
     // This tile's operand ranges (under 2^31 bytes, as the launcher checks): loads past the last valid byte return
     // zeros. With K = 0 the operands may be absent and nothing is read (the prologue still issues its loads, over
     // empty ranges).
-    const uint8_t *a_base = g.A + batch * g.strideA + (int64_t)m0 * lda;
+    const uint8_t *a_base = g.A + batch * g.strideA + (int64_t)m0 * lda + K0;
     const int32_t a_valid = K > 0 ? (min(g.M - m0, DBM) - 1) * lda + K : 0;
     const uint8_t *b_base;
     int32_t b_valid, b_step;
     if constexpr (TRANS_B) {
-        b_base = g.B + batch * g.strideB + (int64_t)n0 * ldb;
+        b_base = g.B + batch * g.strideB + (int64_t)n0 * ldb + K0;
         b_valid = K > 0 ? (min(g.N - n0, DBN) - 1) * ldb + K : 0;
         b_step = 1;
     } else {
-        b_base = g.B + batch * g.strideB + n0;
+        b_base = g.B + batch * g.strideB + n0 + (int64_t)K0 * ldb;
         b_valid = K > 0 ? (K - 1) * ldb + ((min(g.N - n0, DBN) + 3) & ~3) : 0;   // whole dwords (b_dwords_ok)
         b_step = ldb;
     }
@@ -437,8 +444,8 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
         fb[j] = ColFb[nl];
     }
     // int32 and float32 results are 4-byte elements, requantized ones bytes; strideC counts elements either way.
-    int32_t *const Cb = static_cast<int32_t *>(g.C) + batch * g.strideC;
-    uint8_t *const Yb = static_cast<uint8_t *>(g.C) + batch * g.strideC;
+    int32_t *const Cb = static_cast<int32_t *>(g.C) + bsplit * g.strideC;
+    uint8_t *const Yb = static_cast<uint8_t *>(g.C) + bsplit * g.strideC;
     const int32_t ncol0 = n0 + wn * WT + i32;
     const int32_t M = g.M, N = g.N, zp_y = g.zp_y;
     // MODE 0: int32 (+ bias); 1: float32, `opt` = float bias present; 2: requantized bytes, `opt` = uint8 output.
@@ -489,9 +496,11 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
 
 // One instantiation per operand signedness and needed byte sums (an unsigned operand always needs the other's sums).
 template <int BT, bool T, bool FA, bool FB>
-inline void launch_direct_flips(const GemmArgs &g, hipStream_t s, dim3 grid, int32_t tn, int32_t tm, bool sa, bool sb)
+inline void launch_direct_flips(const GemmArgs &g, hipStream_t s, dim3 grid, int32_t tn, int32_t tm, int32_t ks,
+                                int32_t kslice, bool sa, bool sb)
 {
-#define OG_D(SA, SB) hipLaunchKernelGGL((k_gemm_direct<BT, T, SA, SB, FA, FB>), grid, dim3(DTHREADS), 0, s, g, tn, tm)
+#define OG_D(SA, SB) \
+    hipLaunchKernelGGL((k_gemm_direct<BT, T, SA, SB, FA, FB>), grid, dim3(DTHREADS), 0, s, g, tn, tm, ks, kslice)
     if constexpr (FA && FB) {
         OG_D(true, true);
     } else if constexpr (FA) {
@@ -510,18 +519,19 @@ inline void launch_direct_flips(const GemmArgs &g, hipStream_t s, dim3 grid, int
 }
 
 template <int BT, bool T>
-inline void launch_direct_t(const GemmArgs &g, hipStream_t s, dim3 grid, int32_t tn, int32_t tm)
+inline void launch_direct_t(const GemmArgs &g, hipStream_t s, dim3 grid, int32_t tn, int32_t tm, int32_t ks,
+                            int32_t kslice)
 {
     const bool fa = !(g.flags & OG_GEMM_A_INT8), fb = !(g.flags & OG_GEMM_B_INT8);
     const bool sa = (g.flags & OG_GEMM_ZB) || fb, sb = (g.flags & OG_GEMM_ZA) || fa;
-    if (fa && fb) launch_direct_flips<BT, T, true, true>(g, s, grid, tn, tm, sa, sb);
-    else if (fa) launch_direct_flips<BT, T, true, false>(g, s, grid, tn, tm, sa, sb);
-    else if (fb) launch_direct_flips<BT, T, false, true>(g, s, grid, tn, tm, sa, sb);
-    else launch_direct_flips<BT, T, false, false>(g, s, grid, tn, tm, sa, sb);
+    if (fa && fb) launch_direct_flips<BT, T, true, true>(g, s, grid, tn, tm, ks, kslice, sa, sb);
+    else if (fa) launch_direct_flips<BT, T, true, false>(g, s, grid, tn, tm, ks, kslice, sa, sb);
+    else if (fb) launch_direct_flips<BT, T, false, true>(g, s, grid, tn, tm, ks, kslice, sa, sb);
+    else launch_direct_flips<BT, T, false, false>(g, s, grid, tn, tm, ks, kslice, sa, sb);
 }
 
 // Instantiated in translation units of their own (compiled in parallel): B stored N x K at 256, both layouts at 128.
 void launch_direct_nk256(const GemmArgs &g, hipStream_t s, dim3 grid, int32_t tn, int32_t tm);
-void launch_direct128(const GemmArgs &g, hipStream_t s, dim3 grid, int32_t tn, int32_t tm);
+void launch_direct128(const GemmArgs &g, hipStream_t s, dim3 grid, int32_t tn, int32_t tm, int32_t ks, int32_t kslice);
 
 }  // namespace og

@@ -65,6 +65,14 @@ hipError_t launch_gemm_generic(const GemmArgs &g, hipStream_t s, const char **ke
 // 128 x 128; launch_gemm_tiled picks it when it applies.
 hipError_t launch_gemm_direct(const GemmArgs &g, hipStream_t s, const char **kernel, bool large);
 bool direct_ok(const GemmArgs &g);
+// Split-k of the 128 x 128 direct kernel for grids that fill under half the chip: direct_split gives the number of k
+// slices (1: no split); the slices' int32 sums go to ws.partials (step 0), a second pass adds them and applies the
+// bias and the epilogue (step 1).
+constexpr int64_t kSplitTargetTiles = 256, kSplitMaxBytes = int64_t(256) << 20;
+int direct_split(const GemmArgs &g);
+uint64_t direct_split_workspace_bytes(const GemmArgs &g, int ks);
+hipError_t launch_gemm_direct_split(const GemmArgs &g, const Workspace &ws, hipStream_t s, const char **kernel, int ks,
+                                    int step);
 // Whether B's last row can be read in whole dwords up to round4(N) (K x N layout; always true for N % 4 == 0).
 inline bool b_dwords_ok(const GemmArgs &g)
 {

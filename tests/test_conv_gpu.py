@@ -78,6 +78,23 @@ def _configs(d):
     return out
 
 
+def test_onnx_specification_examples():
+    # The ONNX ConvInteger specification's two examples, as known answers: x = 2..10 (3 x 3, uint8, zero point 1),
+    # w = 2 x 2 ones; without padding [12, 16, 24, 28], with padding 1 the 4 x 4 result below. Run on the column
+    # matrix path and on the portable product.
+    d = device()
+    x = d.CreateBuffer(_bytes_of(np.array([2, 3, 4, 5, 6, 7, 8, 9, 10], np.uint8), False))
+    w = d.CreateBuffer(_bytes_of(np.ones(4, np.uint8), False))
+    xz = d.CreateBuffer(_bytes_of(np.array([1], np.uint8), False))
+    want = {0: [12, 16, 24, 28], 1: [1, 3, 5, 3, 5, 12, 16, 9, 11, 24, 28, 15, 7, 15, 17, 9]}
+    for name, conv in _configs(d)[:2]:
+        for pad, expected in want.items():
+            q = _problem(cases.conv_problem(1, 1, 3, 3, 1, 2, 2, pad=pad))
+            y = d.CreateBufferOf(og.ElementType.Int32, len(expected))
+            run(d, lambda e: conv.Encode(e, q, x, w, y, og.Int8Operand(xz, 0)))
+            assert y.Read().tolist() == expected, (name, pad)
+
+
 def test_edge_geometries_are_bit_exact():
     # EdgeGeometriesAreBitExact (ConvIntegerTests.cs:235-275).
     d = device()

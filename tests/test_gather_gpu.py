@@ -65,6 +65,22 @@ def _gather_case(d, k, dtype, itype, shape, axis, count, seed, idx_values=None, 
     return bad, pos, d.LastKernel
 
 
+def test_onnx_specification_examples():
+    # The ONNX Gather specification's two examples as known answers, with int8 payloads (the values times 10): axis 0
+    # with indices [[0, 1], [1, 2]], and axis 1 with indices [[0, 2]].
+    d = device()
+    k = og.GatherKernels(d)
+    d0 = np.array([10, 12, 23, 34, 45, 57, 0, 0], np.int8)           # [[1.0, 1.2], [2.3, 3.4], [4.5, 5.7]] x 10
+    out = d.CreateBufferOf(og.ElementType.Int8, 8)
+    i0 = d.CreateBuffer(np.array([0, 1, 1, 2], np.int32))
+    run(d, lambda e: k.EncodeGather(e, d.CreateBuffer(d0), 0, [3, 2], 0, i0, 0, 4, out, 0))
+    assert out.Read()[:8].tolist() == [10, 12, 23, 34, 23, 34, 45, 57]
+    d1 = np.array([10, 12, 19, 23, 34, 39, 45, 57, 59, 0, 0, 0], np.int8)   # the 3 x 3 example x 10
+    i1 = d.CreateBuffer(np.array([0, 2], np.int64))
+    run(d, lambda e: k.EncodeGather(e, d.CreateBuffer(d1), 0, [3, 3], 1, i1, 0, 2, out, 0))
+    assert out.Read()[:6].tolist() == [10, 19, 23, 39, 45, 59]
+
+
 def test_gather_is_exact():
     # GatherIsExact (GatherTests.cs:73-100): 12 shapes x 10 payload / index types, negative indices, odd offsets.
     d = device()

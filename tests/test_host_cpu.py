@@ -453,5 +453,9 @@ def test_kernel_choice_is_reported():
     assert name(M=1, N=11008, K=4096, Flags=0x4000) == "mfma-i8-rows16-splitk"
     assert name(M=1, N=11000, K=4096) == "mfma-i8-rows16-splitk"          # N % 16 != 0: not tiled
     assert name(M=16, N=11008, K=4096).startswith("mfma-i8-rows16")
-    assert name(M=1, N=11008, K=4096, Flags=0x4) == "mfma-i8-direct128x128x64"   # transposed B: tiled
+    # Transposed B takes the tiled kernels; 86 tiles of 128 over 64 stages of K split into 3 slices.
+    assert name(M=1, N=11008, K=4096, Flags=0x4) == "mfma-i8-direct128x128x64-splitk"
+    assert name(M=256, N=256, K=2304) == "mfma-i8-direct128x128x64-splitk"   # 4 tiles, 36 stages
+    assert name(M=1024, N=3072, K=768) == "mfma-i8-direct128x128x64"          # 192 tiles: no split
+    assert name(M=256, N=256, K=448) == "mfma-i8-direct128x128x64"            # 7 stages: too short to split
     assert name(M=1, N=11008, K=4096, Flags=0x400) == "portable-tile64x64x16"

@@ -423,6 +423,68 @@ def test_b_ending_at_its_last_valid_byte_takes_another_kernel():
     assert np.array_equal(bc.Read(), want)
 
 
+# Products whose 128 x 128 grid fills under half the chip and whose K has at least 8 stages: split along K.
+SPLIT_SHAPES = [  # m, n, k, batch, transposed B
+    (256, 256, 2304, 1, False), (200, 384, 1536, 1, False), (128, 256, 2048, 2, False), (1, 11008, 4096, 1, True),
+    (130, 128, 4096, 1, True)]
+
+
+@pytest.mark.parametrize("m, n, k, batch, trans", SPLIT_SHAPES)
+def test_split_k_products_are_bit_exact(m, n, k, batch, trans):
+    # The k slices each apply the zero points to their own range (every correction term is linear in the range);
+    # the summing pass adds them and applies the bias and the epilogue: int32, float (scale, float bias), scaled
+    # float and requantized outputs, both operand signednesses, zero points per row and column.
+    d = device()
+    gemm = og.Int8Gemm(d)
+    rng = np.random.default_rng(m + n + k)
+    a = rng.integers(0, 256, batch * m * k, dtype=np.uint8)
+    b = rng.integers(0, 256, batch * n * k, dtype=np.uint8)
+    za, zb = rng.integers(0, 256, m, dtype=np.uint8), rng.integers(0, 256, n, dtype=np.uint8)
+    ib = rng.integers(-5000, 5000, n).astype(np.int32)
+    scale = (rng.random(n, dtype=np.float32) * np.float32(1e-4)).astype(np.float32)
+    fb = rng.standard_normal(n).astype(np.float32)
+    mult = (rng.random(n, dtype=np.float32) * np.float32(2e-6)).astype(np.float32)
+    act = np.float32(0.37)
+    p = oracle.Gemm(m, n, k, Batch=batch, TransposeB=int(trans), StrideA=m * k, StrideB=n * k)
+    bad = 0
+    for a_signed, b_signed in ((False, True), (True, False), (True, True)):
+        sums = oracle.int8_gemm(p, a, a_signed, b, b_signed, (za, True, 0), (zb, True, 0))
+        ba = d.CreateBuffer(a.view(np.int8) if a_signed else a)
+        bb = d.CreateBuffer(b.view(np.int8) if b_signed else b)
+        bza = d.CreateBuffer(za.view(np.int8) if a_signed else za)
+        bzb = d.CreateBuffer(zb.view(np.int8) if b_signed else zb)
+        q = to_problem(p)
+        zpa, zpb = og.Int8Operand(bza, 0, True), og.Int8Operand(bzb, 0, True)
+        bib, bsc, bfb = d.CreateBuffer(ib), d.CreateBuffer(scale), d.CreateBuffer(fb)
+        # int32 with bias
+        bc = d.CreateBufferOf(og.ElementType.Int32, batch * m * n)
+        run(d, lambda e: gemm.EncodeInt32(e, q, ba, bb, bc, zpa, zpb, og.Int8Operand(bib, 0, True)))
+        assert d.LastKernel == "mfma-i8-direct128x128x64-splitk", d.LastKernel
+        want = (sums.astype(np.int64) + np.tile(ib, batch * m)).astype(np.int64)
+        bad += int(np.count_nonzero(bc.Read() != ((want & 0xFFFFFFFF).astype(np.uint32).view(np.int32))))
+        # float with scale per column and float bias
+        bf = d.CreateBufferOf(og.ElementType.Float32, batch * m * n)
+        run(d, lambda e: gemm.EncodeFloat(e, q, ba, bb, bf, og.Int8Operand(bsc, 0, True), zpa, zpb,
+                                          og.Int8Operand(bfb, 0, True), og.Int8Operand(bib, 0, True)))
+        wantf = oracle.float_epilogue(sums, n, scale, True, ib, fb)
+        bad += int(np.count_nonzero(bf.Read().view(np.uint32) != wantf.view(np.uint32)))
+        # scaled float: the column scale fl(act * scale[n])
+        bact = d.CreateBuffer(np.array([act], np.float32))
+        run(d, lambda e: gemm.EncodeFloatScaled(e, q, ba, bb, bf, og.Int8Operand(bact, 0), og.Int8Operand(bsc, 0, True),
+                                                zpa, zpb))
+        wants = oracle.float_epilogue(sums, n, (act * scale).astype(np.float32), True)
+        bad += int(np.count_nonzero(bf.Read().view(np.uint32) != wants.view(np.uint32)))
+        # requantized bytes
+        by = d.CreateBufferOf(og.ElementType.UInt8, batch * m * n)
+        bm = d.CreateBuffer(mult)
+        run(d, lambda e: gemm.EncodeRequantized(e, q, ba, bb, by, og.Int8Operand(bm, 0, True), 131, zpa, zpb,
+                                                og.Int8Operand(bib, 0, True)))
+        wantq = oracle.requant_array(sums, n, mult, True, 131, True, ib)
+        bad += int(np.count_nonzero(by.Read()[:batch * m * n] != wantq))
+    say(f"ROW split-k {m}x{n}x{k} batch {batch} {'N x K' if trans else 'K x N'}: wrong values {bad}")
+    assert bad == 0
+
+
 def test_scratch_semantics():
     # Int8ScratchTests.cs:27-89
     d = device()
