@@ -451,6 +451,73 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
     // MODE 0: int32 (+ bias); 1: float32, `opt` = float bias present; 2: requantized bytes, `opt` = uint8 output.
     auto store_all = [&](auto mode_tag, bool opt) {
         constexpr int MODE = decltype(mode_tag)::value;
+        if constexpr (BT == 128) {
+            // Staged through LDS: one store instruction per thread then writes four neighbouring columns (16 bytes, or
+            // 4 bytes of a requantized row) where the accumulator layout gives it one column per lane, so a tile takes
+            // a quarter of the store instructions, whose issue rate bounds this epilogue. Needs N % 4 == 0 and an
+            // aligned C.
+            const bool staged = N % 4 == 0 && (MODE == 2 ? ((uintptr_t)Yb & 3) == 0 : ((uintptr_t)Cb & 15) == 0);
+            if (staged) {
+                // The raw sums, [row][column] with rows of LDT ints (the pad puts the two half-waves' writes of one
+                // instruction on different banks), after the epilogue's arrays.
+                constexpr int LDT = BT + 4, T_OFF = 4096;
+                static_assert(T_OFF >= (2 * DBM + 5 * DBN) * 4 && T_OFF + BT * LDT * 4 <= NS * STAGE, "staging space");
+                int32_t *const T = reinterpret_cast<int32_t *>(smem + T_OFF);
+#pragma unroll
+                for (int i = 0; i < F; i++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++)
+#pragma unroll
+                            for (int j = 0; j < F; j++)
+                                T[(wm * WT + 32 * i + 8 * q + 4 * h2 + r) * LDT + wn * WT + 32 * j + i32] = acc[i][j][4 * q + r];
+                wait_lgkm_barrier();
+                // Thread t: columns 4 (t % 32) .. + 3 of the tile, rows t / 32 + 8 jj.
+                const int c4 = 4 * (tid & 31), r0 = tid >> 5;
+                uint32_t wz4[4], ct4[4], ib4[4];
+                float sc4[4], fb4[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    wz4[e] = SUM_A ? (uint32_t)ColW[c4 + e] : 0u;
+                    ct4[e] = SUM_B ? (uint32_t)ColSum[c4 + e] - Ku * wz4[e] : 0u;
+                    ib4[e] = (uint32_t)ColIB[c4 + e];
+                    sc4[e] = ColSc[c4 + e];
+                    fb4[e] = ColFb[c4 + e];
+                }
+                const int32_t n = n0 + c4;
+#pragma unroll 4
+                for (int jj = 0; jj < BT / 8; jj++) {
+                    const int rl = r0 + 8 * jj;
+                    const int32_t m = m0 + rl;
+                    if (m >= M || n >= N) continue;   // N % 4 == 0: the four columns are all in or all out
+                    const v4i raw = *reinterpret_cast<const v4i *>(&T[rl * LDT + c4]);
+                    const uint32_t ss = SUM_A ? (uint32_t)RowSum[rl] : 0u, zz = SUM_B ? (uint32_t)RowZ[rl] : 0u;
+                    uint32_t v[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) v[e] = (uint32_t)raw[e] - wz4[e] * ss - zz * ct4[e] + ib4[e];
+                    const int64_t at = (int64_t)m * N + n;
+                    if constexpr (MODE == 1) {
+                        float f[4];
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            f[e] = __fmul_rn((float)(int32_t)v[e], sc4[e]);
+                            if (opt) f[e] = __fadd_rn(f[e], fb4[e]);
+                        }
+                        *reinterpret_cast<v4i *>(Cb + at) =
+                            (v4i){__float_as_int(f[0]), __float_as_int(f[1]), __float_as_int(f[2]), __float_as_int(f[3])};
+                    } else if constexpr (MODE == 2) {
+                        uint32_t word = 0;
+#pragma unroll
+                        for (int e = 0; e < 4; e++) word |= requantize_byte(v[e], sc4[e], zp_y, opt) << (8 * e);
+                        *reinterpret_cast<uint32_t *>(Yb + at) = word;
+                    } else {
+                        *reinterpret_cast<v4i *>(Cb + at) = (v4i){(int32_t)v[0], (int32_t)v[1], (int32_t)v[2], (int32_t)v[3]};
+                    }
+                }
+                return;
+            }
+        }
 #pragma unroll
         for (int i = 0; i < F; i++) {
 #pragma unroll
