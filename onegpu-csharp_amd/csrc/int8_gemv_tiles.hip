@@ -171,47 +171,62 @@ __global__ __launch_bounds__(GT_THREADS) void k_gemv_tiles(GemmArgs g, int32_t s
     }
 }
 
-// The parts of slab (batch, slab) = x / row_groups added up, for rows 4 (x % row_groups) .. + 3 of column n0 + tid:
-// the zero points applied with the whole K, then the epilogue.
+// The parts of a slab added up, for a row group (4 rows) and 64 of its columns: workgroup x takes quarter x % 4 of the
+// columns, row group (x / 4) % row_groups of slab x / (4 row_groups). Thread t sums, for column t % 64, the parts
+// p = t / 64 (mod 4), all its loads in flight at once (one round for up to 16 parts); the four partial sums meet in
+// LDS and the first 64 threads apply the zero points with the whole K, then the epilogue.
 template <bool SUM_A, bool SUM_B, bool FLIP_A, bool FLIP_B>
 __global__ __launch_bounds__(GT_THREADS) void k_gemv_tiles_sum(GemmArgs g, int32_t slabs, int32_t nkc,
                                                                 const int32_t *parts)
 {
-    const int tid = threadIdx.x;
+    __shared__ v4i red_v[4][64], red_r[4][64];
+    __shared__ uint32_t red_c[4][64];
+    const int tid = threadIdx.x, cl = tid & 63, u = tid >> 6;
     const int32_t row_groups = (g.M + GT_ROWS_PER_SUM - 1) / GT_ROWS_PER_SUM;
-    const int64_t q = blockIdx.x / row_groups;
-    const int32_t m0 = (int32_t)(blockIdx.x % row_groups) * GT_ROWS_PER_SUM;
+    const int64_t x = blockIdx.x;
+    const int32_t cq = (int32_t)(x & 3);
+    const int64_t rest = x >> 2, q = rest / row_groups;
+    const int32_t m0 = (int32_t)(rest % row_groups) * GT_ROWS_PER_SUM;
     const int32_t b = (int32_t)(q / slabs), slab = (int32_t)(q % slabs);
     const int32_t M = g.M, N = g.N, K = g.K;
-    const int32_t n = slab * GT_COLS + tid;
+    const int32_t col = 64 * cq + cl, n = slab * GT_COLS + col;
     const int64_t stride = gemv_tile_part(M);
     const int32_t *pp = parts + q * nkc * stride;
     const int32_t gi = m0 / 4, groups = gemv_tile_groups(M);
     const bool cs_here = M / 4 == gi;   // the column sums (row M) share this row group
 
-    // Eight parts at a time, all their loads in flight together (parts past the last read the last one, inside the
-    // workspace, and are masked off).
     v4i v = {0, 0, 0, 0}, rs = {0, 0, 0, 0};
     uint32_t cs = 0;
-    for (int32_t p0 = 0; p0 < nkc; p0 += 8) {
-        v4i x[8], r[8];
-        uint32_t c[8];
+    for (int32_t p0 = u; p0 < nkc; p0 += 16) {
+        v4i xv[4], r[4];
+        uint32_t c[4];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int32_t *part = pp + min(p0 + u, nkc - 1) * stride;
-            x[u] = *reinterpret_cast<const v4i *>(part + (gi * GT_COLS + tid) * 4);
-            r[u] = SUM_A ? *reinterpret_cast<const v4i *>(part + groups * GT_COLS * 4 + 4 * gi) : (v4i){0, 0, 0, 0};
-            c[u] = (SUM_B && !cs_here) ? (uint32_t)part[((M / 4) * GT_COLS + tid) * 4 + (M & 3)] : 0u;
+        for (int e = 0; e < 4; e++) {
+            // Parts past the last read the last one (inside the workspace) and are masked off.
+            const int32_t *part = pp + min(p0 + 4 * e, nkc - 1) * stride;
+            xv[e] = *reinterpret_cast<const v4i *>(part + (gi * GT_COLS + col) * 4);
+            r[e] = SUM_A ? *reinterpret_cast<const v4i *>(part + groups * GT_COLS * 4 + 4 * gi) : (v4i){0, 0, 0, 0};
+            c[e] = (SUM_B && !cs_here) ? (uint32_t)part[((M / 4) * GT_COLS + col) * 4 + (M & 3)] : 0u;
         }
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int32_t keep = p0 + u < nkc ? -1 : 0;
-            v += x[u] & keep;
-            rs += r[u] & keep;
-            cs += (cs_here ? (uint32_t)x[u][M & 3] : c[u]) & (uint32_t)keep;
+        for (int e = 0; e < 4; e++) {
+            const int32_t keep = p0 + 4 * e < nkc ? -1 : 0;
+            v += xv[e] & keep;
+            rs += r[e] & keep;
+            cs += (cs_here ? (uint32_t)xv[e][M & 3] : c[e]) & (uint32_t)keep;
         }
     }
-    if (n >= N) return;
+    red_v[u][cl] = v;
+    red_r[u][cl] = rs;
+    red_c[u][cl] = cs;
+    __syncthreads();
+    if (u != 0 || n >= N) return;
+#pragma unroll
+    for (int w = 1; w < 4; w++) {
+        v += red_v[w][cl];
+        rs += red_r[w][cl];
+        cs += red_c[w][cl];
+    }
     uint32_t wz = 0;
     if (SUM_A) {
         const uint32_t w = g.ZB ? g.ZB[(g.flags & OG_GEMM_ZB_PER_COL) ? n : 0] : 0u;
@@ -243,7 +258,7 @@ bool gemv_tiles_ok(const GemmArgs &g)
     if (((g.lda | g.strideA | (int64_t)(uintptr_t)g.A) & 15) != 0) return false;
     if ((int64_t)GT_KT * g.ldb + GT_COLS > 0x7FFFFFFFll || (int64_t)16 * g.lda + GT_KT > 0x7FFFFFFFll) return false;
     const int64_t q = (int64_t)g.batch * ((g.N + GT_COLS - 1) / GT_COLS);
-    return q * ((g.K + GT_KT - 1) / GT_KT) <= 0x7FFFFFFFll && q * 4 <= 0x7FFFFFFFll;
+    return q * ((g.K + GT_KT - 1) / GT_KT) <= 0x7FFFFFFFll && q * 16 <= 0x7FFFFFFFll;
 }
 
 uint64_t gemv_tiles_workspace_bytes(const GemmArgs &g)
@@ -260,7 +275,7 @@ hipError_t launch_gemv_tiles(const GemmArgs &g, const Workspace &ws, hipStream_t
     const bool fa = !(g.flags & OG_GEMM_A_INT8), fb = !(g.flags & OG_GEMM_B_INT8);
     const bool sa = (g.flags & OG_GEMM_ZB) || fb, sb = (g.flags & OG_GEMM_ZA) || fa;
     const dim3 block(GT_THREADS);
-    const dim3 grid(step == 0 ? (uint32_t)(q * nkc) : (uint32_t)(q * ((g.M + GT_ROWS_PER_SUM - 1) / GT_ROWS_PER_SUM)));
+    const dim3 grid(step == 0 ? (uint32_t)(q * nkc) : (uint32_t)(q * ((g.M + GT_ROWS_PER_SUM - 1) / GT_ROWS_PER_SUM) * 4));
     *kernel = step == 0 ? "mfma-i8-rows16-tiles" : "rows16-tiles-sum";
 #define OG_GT(SA, SB, FA, FB)                                                                                       \
     do {                                                                                                           \

@@ -143,7 +143,7 @@ def test_float_and_requantized_forms_are_bit_exact(config):
 # Shapes that reach every kernel: few rows on the tiled few-rows kernel (or split k), the 128 and 256 direct kernels
 # (ragged M included), the register-staged 128 tile (K = 96), the generic kernel (unaligned rows), tiny products.
 REQUANT_KERNEL_SHAPES = [(1, 1, 1), (5, 7, 9), (4, 272, 512), (16, 256, 1024), (64, 64, 96), (33, 257, 77),
-                         (128, 384, 384), (130, 256, 512)]
+                         (128, 384, 384), (130, 256, 512), (2, 8192, 128)]
 
 
 @pytest.mark.parametrize("fused", [True, False], ids=["one launch", "two passes"])
@@ -521,8 +521,10 @@ def test_few_rows_kernels_are_bit_exact(config):
     gemm = og.Int8Gemm(d) if config == "tiles" else og.Int8Gemm(d, og.Int8GemmOptions(Tile=32))
     shapes = [(1, 16, 4, 1), (1, 256, 64, 1), (4, 272, 100, 1), (16, 1024, 4096, 1), (7, 528, 1500, 1),
               (16, 4096, 64, 1), (2, 4096, 8192, 1), (3, 512, 320, 3), (1, 11008, 4096, 1), (5, 48, 12, 2),
-              (16, 272, 4112, 2), (1, 32768, 512, 1), (15, 1040, 272, 1), (2, 1040, 272, 1)]
-    bad_total = 0
+              (16, 272, 4112, 2), (1, 32768, 512, 1), (15, 1040, 272, 1), (2, 1040, 272, 1),
+              (16, 8208, 1040, 1), (7, 4112, 336, 2), (4, 8192, 16, 1), (3, 12288, 64, 1), (1, 8192, 8192, 1),
+              (13, 8256, 208, 1)]
+    bad_total, kernels = 0, set()
     for i, (m, n, k, batch) in enumerate(shapes):
         a_s, b_s = (i & 1) != 0, (i & 2) == 0
         za_mode, zb_mode = i % 3, (i // 3) % 3
@@ -531,6 +533,7 @@ def test_few_rows_kernels_are_bit_exact(config):
         for rep in range(3 if i == 2 or i == 8 else 1):
             say(f"{config} case {c.name} signed {a_s}/{b_s} zp {za_mode}/{zb_mode} rep {rep}")
             bad, kernel = run_int32(d, gemm, c, 100 + i)
+            kernels.add(kernel)
             if tiled:
                 assert kernel == "mfma-i8-rows16-tiles", kernel
             else:
@@ -540,7 +543,8 @@ def test_few_rows_kernels_are_bit_exact(config):
         say(f"{config} float vec {vec}")
         bad_total += _float_case(d, gemm, 4, 256, 128, vec, True, True, 77 + vec)
         bad_total += _float_case(d, gemm, 16, 1024, 512, vec, False, True, 79 + vec)
-    say(f"ROW int8 gemm | few rows [{config}] | mismatches {bad_total}")
+        bad_total += _float_case(d, gemm, 3, 8192, 192, vec, True, True, 81 + vec)
+    say(f"ROW int8 gemm | few rows [{config}] | mismatches {bad_total}; kernels {sorted(kernels)}")
     assert bad_total == 0
 
 
