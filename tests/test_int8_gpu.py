@@ -306,6 +306,27 @@ def test_dynamic_quantize_large_inputs():
     assert bad == 0
 
 
+def test_dynamic_quantize_in_sequence():
+    # Consecutive launches of different sizes and ranges on one device, each checked against the oracle: nothing of
+    # one launch's ranges may leak into the next (the per-workgroup ranges live in a workspace the launches share).
+    d = device()
+    k = og.DynamicQuantizeKernels(d)
+    counts = [2_097_152, 1, 4097, 786_432, 2_097_153, 65_536, 2_000_001, 3, 1_048_577, 2_097_152, 257, 786_432]
+    for i, count in enumerate(counts):
+        kind = i % 7
+        x = oracle.dq_input(count, 900 + i, kind)
+        if i % 4 == 1:
+            x = -np.abs(x)   # all-negative ranges: lo far from zero, hi = 0
+        say(f"dq sequence {i}: count {count} kind {kind}")
+        wy, ws, wz = oracle.dynamic_quantize(x)
+        bx, by = d.CreateBuffer(x), d.CreateBufferOf(og.ElementType.UInt8, count + 4)
+        bs, bz = d.CreateBufferOf(og.ElementType.Float32, 1), d.CreateBufferOf(og.ElementType.UInt8, 4)
+        run(d, lambda e: k.Encode(e, bx, 0, count, by, 0, bs, 0, bz, 0))
+        here = int(np.count_nonzero(by.Read()[:count] != wy))
+        here += int(bs.Read()[0].view(np.uint32) != np.float32(ws).view(np.uint32)) + int(bz.Read()[0] != wz)
+        assert here == 0, f"launch {i}, count {count}: {here} wrong"
+
+
 def test_dynamic_quantize_special_values():
     d = device()
     k = og.DynamicQuantizeKernels(d)
