@@ -457,5 +457,6 @@ def test_kernel_choice_is_reported():
     assert name(M=1, N=11008, K=4096, Flags=0x4) == "mfma-i8-direct128x128x64-splitk"
     assert name(M=256, N=256, K=2304) == "mfma-i8-direct128x128x64-splitk"   # 4 tiles, 36 stages
     assert name(M=1024, N=3072, K=768) == "mfma-i8-direct128x128x64"          # 192 tiles: no split
+    assert name(M=2048, N=3072, K=768) == "mfma-i8-direct128x128x64"          # 384 tiles: two workgroups a CU
     assert name(M=256, N=256, K=448) == "mfma-i8-direct128x128x64"            # 7 stages: too short to split
     assert name(M=1, N=11008, K=4096, Flags=0x400) == "portable-tile64x64x16"

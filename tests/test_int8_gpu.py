@@ -143,7 +143,7 @@ def test_float_and_requantized_forms_are_bit_exact(config):
 # Shapes that reach every kernel: few rows on the tiled few-rows kernel (or split k), the 128 and 256 direct kernels
 # (ragged M included), the register-staged 128 tile (K = 96), the generic kernel (unaligned rows), tiny products.
 REQUANT_KERNEL_SHAPES = [(1, 1, 1), (5, 7, 9), (4, 272, 512), (16, 256, 1024), (64, 64, 96), (33, 257, 77),
-                         (128, 384, 384), (130, 256, 512), (2, 8192, 128)]
+                         (128, 384, 384), (130, 256, 512), (2, 8192, 128), (96, 208, 320)]
 
 
 @pytest.mark.parametrize("fused", [True, False], ids=["one launch", "two passes"])
