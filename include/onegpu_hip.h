@@ -249,9 +249,11 @@ typedef struct og_conv_params {
 #define OG_CONV_WZ_PER_CHANNEL  0x10u /* ... one per output channel */
 #define OG_CONV_NO_DEPTHWISE    0x20u /* convolutions with one input channel a group through the column matrix too */
 
-/* Bytes of column scratch one image needs: Groups * K * ldb with K = InChannels / Groups * KernelHeight * KernelWidth
- * and ldb = OutHeight * OutWidth rounded up to 16 (ConvIntegerKernels.ScratchBytesPerImage, ConvIntegerKernels.cs:78-89,
- * which rounds to 4). 0 when the geometry is invalid. */
+/* Bytes of column scratch one image needs: Groups * Kp * ldb with K = InChannels / Groups * KernelHeight * KernelWidth,
+ * ldb = OutHeight * OutWidth rounded up to 16 (ConvIntegerKernels.ScratchBytesPerImage, ConvIntegerKernels.cs:78-89,
+ * which rounds to 4) and Kp = K, or, when 64 <= K and K % 64 != 0, K rounded up to 64 plus 16 + OutChannels * Kp
+ * rounded up to 256 bytes for the weights in rows of Kp bytes. A scratch of n such figures holds n images' columns.
+ * 0 when the geometry is invalid. */
 uint64_t og_conv_integer_scratch_bytes(const og_conv_params *params);
 
 /* ONNX ConvInteger: y[n, m, oh, ow] = sum over c, kh, kw of (x - xz) * (w - wz[m]) in 32-bit wrap-around; taps in the

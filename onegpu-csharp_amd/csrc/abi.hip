@@ -693,7 +693,10 @@ namespace {
 // The geometry of a convolution after ConvKernels.CheckConv (ConvKernels.cs:895-956) and ConvIntegerKernels.Geometry
 // (ConvIntegerKernels.cs:296-318); `arg` names what failed.
 struct ConvGeometry {
-    int64_t oh, ow, cin_g, cout_g, k, ldb, per_image, x_image, y_image;
+    // kp: K padded to a multiple of 64 when 64 <= K and K % 64 != 0 (else K); cols_image: one image's column matrices;
+    // wp_bytes: the padded weight copy ahead of them (0 without padding, with room to align its start to 16 bytes);
+    // per_image = wp_bytes + cols_image, the scratch that one image needs.
+    int64_t oh, ow, cin_g, cout_g, k, kp, ldb, cols_image, wp_bytes, per_image, x_image, y_image;
     const char *arg;
     const char *msg;
 };
@@ -739,8 +742,13 @@ bool conv_geometry(const og_conv_params *p, ConvGeometry &g)
     g.x_image = (int64_t)p->InChannels * p->Height * p->Width;
     g.y_image = (int64_t)p->OutChannels * g.oh * g.ow;
     if (g.k > imax || g.ldb > imax || g.x_image * p->Batch > imax) return bad("shape", "the convolution is larger than the supported sizes");
-    g.per_image = (int64_t)p->Groups * g.k * g.ldb;
-    if (g.per_image > imax) return bad("InChannels", "the column matrix of one image is larger than the supported sizes");
+    const bool pad = g.k >= 64 && g.k % 64 != 0;
+    g.kp = pad ? (g.k + 63) / 64 * 64 : g.k;
+    g.cols_image = (int64_t)p->Groups * g.kp * g.ldb;
+    g.wp_bytes = pad ? 16 + ((int64_t)p->OutChannels * g.kp + 255) / 256 * 256 : 0;
+    g.per_image = g.wp_bytes + g.cols_image;
+    if (g.kp > imax || g.per_image > imax)
+        return bad("InChannels", "the column matrix of one image is larger than the supported sizes");
     return true;
 }
 
@@ -785,8 +793,8 @@ int og_conv_integer(og_ctx *ctx, const og_conv_params *p, og_buffer x, og_buffer
     if (!depthwise && !pointwise) {
         if (scratch_offset & 3) return fail(ctx, OG_ERR_INVALID_ARG, "scratchOffset", "offset %llu must be a multiple of 4", (unsigned long long)scratch_offset);
         if (!scratch.ptr || !fits(scratch_offset, (uint64_t)geo.per_image, scratch)) return fail(ctx, OG_ERR_INVALID_ARG, "scratch", "one image's columns (%lld bytes from %llu) reach past the buffer", (long long)geo.per_image, (unsigned long long)scratch_offset);
-        per_chunk = std::min<int64_t>(B, (int64_t)((scratch.bytes - scratch_offset) / (uint64_t)geo.per_image));
-        per_chunk = std::min<int64_t>(per_chunk, 0x7FFFFFFF / geo.per_image);   // one chunk's columns stay under 2 GiB
+        per_chunk = std::min<int64_t>(B, (int64_t)(scratch.bytes - scratch_offset - (uint64_t)geo.wp_bytes) / geo.cols_image);
+        per_chunk = std::min<int64_t>(per_chunk, 0x7FFFFFFF / geo.cols_image);   // one chunk's columns stay under 2 GiB
     }
     if (!ctx) return fail(ctx, OG_ERR_NO_DEVICE, "ctx", "no context: the arguments are valid but there is no device to run on");
     (void)hipSetDevice(ctx->device);
@@ -828,10 +836,11 @@ int og_conv_integer(og_ctx *ctx, const og_conv_params *p, og_buffer x, og_buffer
     const int64_t ncols = geo.oh * geo.ow;
     // The products: A = group g's weights [cout_g x k] (its zero point per row = per output channel), B = the group's
     // column matrix [k x ncols] (x's zero point), one batch entry per image.
-    auto product = [&](const uint8_t *b, int64_t ldb, int64_t stride_b, int64_t b_bytes, int64_t first, int32_t images,
-                       int64_t g) {
+    // a / kk: the weights and their row length (the padded copy and kp after a padded pack).
+    auto product = [&](const uint8_t *a, int64_t kk, const uint8_t *b, int64_t ldb, int64_t stride_b, int64_t b_bytes,
+                       int64_t first, int32_t images, int64_t g) {
         og::GemmArgs ga{};
-        ga.A = wb + g * geo.cout_g * geo.k;
+        ga.A = a + g * geo.cout_g * kk;
         ga.B = b;
         ga.C = yb + first * geo.y_image + g * geo.cout_g * ncols;
         ga.ZA = wzp ? wzp + ((p->Flags & OG_CONV_WZ_PER_CHANNEL) ? g * geo.cout_g : 0) : nullptr;
@@ -842,9 +851,9 @@ int og_conv_integer(og_ctx *ctx, const og_conv_params *p, og_buffer x, og_buffer
         ga.b_bytes = b_bytes;
         ga.M = (int32_t)geo.cout_g;
         ga.N = (int32_t)ncols;
-        ga.K = (int32_t)geo.k;
+        ga.K = (int32_t)kk;
         ga.batch = images;
-        ga.lda = (int32_t)geo.k;
+        ga.lda = (int32_t)kk;
         ga.ldb = (int32_t)ldb;
         ga.flags = p->GemmFlags | ((p->Flags & OG_CONV_W_INT8) ? OG_GEMM_A_INT8 : 0u) |
                    ((p->Flags & OG_CONV_X_INT8) ? OG_GEMM_B_INT8 : 0u) | (wzp ? OG_GEMM_ZA : 0u) |
@@ -854,11 +863,15 @@ int og_conv_integer(og_ctx *ctx, const og_conv_params *p, og_buffer x, og_buffer
     };
     if (pointwise) {
         for (int64_t g = 0; g < p->Groups && st == OG_OK; g++)
-            st = product(xb + g * geo.cin_g * plane, plane, geo.x_image,
+            st = product(wb, geo.k, xb + g * geo.cin_g * plane, plane, geo.x_image,
                          (int64_t)(x.bytes - p->OffsetX) - g * geo.cin_g * plane, 0, (int32_t)B, g);
         return st == OG_OK ? ok(ctx) : st;
     }
-    uint8_t *cols = static_cast<uint8_t *>(scratch.ptr) + scratch_offset;
+    // Scratch: [the padded weights, from the first 16-byte boundary] [the column matrices of a chunk of images].
+    uint8_t *const base = static_cast<uint8_t *>(scratch.ptr) + scratch_offset;
+    uint8_t *const wp = geo.wp_bytes ? reinterpret_cast<uint8_t *>(((uintptr_t)base + 15) & ~(uintptr_t)15) : nullptr;
+    uint8_t *const cols = geo.wp_bytes ? wp + (geo.wp_bytes - 16) : base;
+    const int64_t cols_room = (int64_t)scratch.bytes - (int64_t)(cols - static_cast<uint8_t *>(scratch.ptr));
     for (int64_t first = 0; first < B && st == OG_OK; first += per_chunk) {
         const int32_t images = (int32_t)std::min<int64_t>(per_chunk, B - first);
         og::ConvPackArgs pa{};
@@ -883,10 +896,14 @@ int og_conv_integer(og_ctx *ctx, const og_conv_params *p, og_buffer x, og_buffer
         pa.ph = (int32_t)p->PadTop;
         pa.pw = (int32_t)p->PadLeft;
         pa.ldb = geo.ldb;
+        pa.kp = (int32_t)geo.kp;
+        pa.wrows = geo.wp_bytes && first == 0 ? (int32_t)p->OutChannels : 0;   // the weights once, with the first chunk
+        pa.wt = wb;
+        pa.wp = wp;
         st = launch(ctx, "og_conv_integer", [&](const char **k) { return og::launch_conv_pack(pa, ctx->stream, k); });
         for (int64_t g = 0; g < p->Groups && st == OG_OK; g++)
-            st = product(cols + g * geo.k * geo.ldb, geo.ldb, p->Groups * geo.k * geo.ldb,
-                         (int64_t)(scratch.bytes - scratch_offset) - g * geo.k * geo.ldb, first, images, g);
+            st = product(geo.wp_bytes ? wp : wb, geo.kp, cols + g * geo.kp * geo.ldb, geo.ldb, p->Groups * geo.kp * geo.ldb,
+                         cols_room - g * geo.kp * geo.ldb, first, images, g);
     }
     return st == OG_OK ? ok(ctx) : st;
 }

@@ -8,6 +8,11 @@
 // of 16 bytes (ldb) so that the MFMA product can feed them to LDS with 16-byte DMA; the padding columns hold the zero
 // point too and the product never reads them. One thread writes 16 bytes of one row.
 //
+// Padded depth: when K is not a multiple of 64 the launcher pads it to one (kp), so that the products take the
+// LDS-DMA kernel. Rows k .. kp - 1 of every column matrix hold x's zero point, so each padded tap adds
+// (w - wz) (xz - xz) = 0, and the same launch copies the weights into rows of kp bytes, zero past k; the 16-byte
+// chunks of both go through one grid-stride loop (the column chunks first).
+//
 // Depthwise (one input channel a group): no matrix at all. One thread per output element sums its KH * KW taps,
 // (x - xz) * (w - wz[m]) in 32-bit wrap-around, skipping taps in the padding (they are the real value zero).
 #include "og_internal.hpp"
@@ -26,16 +31,46 @@ template <bool ALIGNED16>
 __global__ __launch_bounds__(kConvThreads) void k_conv_pack(ConvPackArgs a)
 {
     const int64_t chunks_per_row = a.ldb / 16;
-    const int64_t rows = (int64_t)a.images * a.groups * a.k;
-    const int64_t total = rows * chunks_per_row;
+    const int64_t rows = (int64_t)a.images * a.groups * a.kp;
+    const int64_t total = rows * chunks_per_row, wchunks = a.kp / 16, wtotal = (int64_t)a.wrows * wchunks;
     const int32_t taps = a.kh * a.kw;
     const uint32_t pad = a.xz ? (uint32_t)*a.xz : 0u;
     const int32_t ncols = a.oh * a.ow;
-    for (int64_t t = (int64_t)blockIdx.x * kConvThreads + threadIdx.x; t < total; t += (int64_t)gridDim.x * kConvThreads) {
+    for (int64_t t = (int64_t)blockIdx.x * kConvThreads + threadIdx.x; t < total + wtotal;
+         t += (int64_t)gridDim.x * kConvThreads) {
+        if (t >= total) {
+            // Weight chunk: row m, bytes 16 c .. + 15 of the padded copy.
+            const int64_t tw = t - total, m = tw / wchunks;
+            const int32_t c0 = 16 * (int32_t)(tw - m * wchunks);
+            uint32_t word[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                uint32_t wv = 0;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int32_t kk = c0 + 4 * q + e;
+                    wv |= (kk < a.k ? (uint32_t)a.wt[m * a.k + kk] : 0u) << (8 * e);
+                }
+                word[q] = wv;
+            }
+            *reinterpret_cast<uint4 *>(a.wp + m * a.kp + c0) = make_uint4(word[0], word[1], word[2], word[3]);
+            continue;
+        }
         const int64_t r = t / chunks_per_row;
         const int32_t c16 = (int32_t)(t - r * chunks_per_row);
-        const int64_t ig = r / a.k;
-        const int32_t k = (int32_t)(r - ig * a.k);
+        const int64_t ig = r / a.kp;
+        const int32_t k = (int32_t)(r - ig * a.kp);
+        uint8_t *dst = a.cols + r * a.ldb + 16 * (int64_t)c16;
+        if (k >= a.k) {   // a padding row
+            const uint32_t pw4 = pad * 0x01010101u;
+            if constexpr (ALIGNED16) {
+                *reinterpret_cast<uint4 *>(dst) = make_uint4(pw4, pw4, pw4, pw4);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; q++) reinterpret_cast<uint32_t *>(dst)[q] = pw4;
+            }
+            continue;
+        }
         const int64_t img = ig / a.groups;
         const int32_t g = (int32_t)(ig - img * a.groups);
         const int32_t c = k / taps, kk = k - c * taps, kh = kk / a.kw, kw = kk - kh * a.kw;
@@ -63,7 +98,6 @@ __global__ __launch_bounds__(kConvThreads) void k_conv_pack(ConvPackArgs a)
             }
             word[q] = wv;
         }
-        uint8_t *dst = a.cols + r * a.ldb + 16 * (int64_t)c16;
         if constexpr (ALIGNED16) {
             *reinterpret_cast<uint4 *>(dst) = make_uint4(word[0], word[1], word[2], word[3]);
         } else {
@@ -115,7 +149,7 @@ int64_t conv_grid(int64_t threads)
 hipError_t launch_conv_pack(const ConvPackArgs &a, hipStream_t s, const char **kernel)
 {
     *kernel = "conv-pack16";
-    const int64_t total = (int64_t)a.images * a.groups * a.k * (a.ldb / 16);
+    const int64_t total = (int64_t)a.images * a.groups * a.kp * (a.ldb / 16) + (int64_t)a.wrows * (a.kp / 16);
     if (total == 0) return hipSuccess;
     const dim3 grid((uint32_t)conv_grid(total)), block(kConvThreads);
     if (((uintptr_t)a.cols & 15) == 0) hipLaunchKernelGGL(k_conv_pack<true>, grid, block, 0, s, a);

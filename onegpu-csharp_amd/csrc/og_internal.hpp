@@ -147,6 +147,11 @@ struct ConvPackArgs {
     uint8_t *cols;
     int32_t images, groups, k, cin, cin_g, h, w, oh, ow, kh, kw, sh, sw, dh, dw, ph, pw;
     int64_t ldb;
+    // K padded to kp (>= k) rows: rows k .. kp - 1 of every column matrix hold x's zero point, and the weights
+    // [wrows x k] are copied to wp as [wrows x kp] with zeros past k (wrows = 0: no copy; wp 16-byte aligned).
+    int32_t kp, wrows;
+    const uint8_t *wt;
+    uint8_t *wp;
 };
 hipError_t launch_conv_pack(const ConvPackArgs &a, hipStream_t s, const char **kernel);
 

@@ -1018,8 +1018,30 @@ int64_t ConvIntegerKernels::ScratchBytesPerImage(const ConvProblem &problem)
 {
     int oh, ow;
     int64_t k, ldb;
-    ConvGeometry(problem, oh, ow, k, ldb);
-    return (int64_t)problem.Groups * k * ldb;
+    ConvGeometry(problem, oh, ow, k, ldb);   // throws for a geometry the library would refuse
+    // The library's figure: one image's column matrices, with their depth padded to a multiple of 64 (and the padded
+    // weight copy ahead of them) where that lets the products take the LDS-DMA kernel.
+    og_conv_params c{};
+    c.Batch = 1;
+    c.InChannels = (uint32_t)problem.InChannels;
+    c.Height = (uint32_t)problem.Height;
+    c.Width = (uint32_t)problem.Width;
+    c.OutChannels = (uint32_t)problem.OutChannels;
+    c.KernelHeight = (uint32_t)problem.KernelHeight;
+    c.KernelWidth = (uint32_t)problem.KernelWidth;
+    c.StrideHeight = (uint32_t)problem.StrideHeight;
+    c.StrideWidth = (uint32_t)problem.StrideWidth;
+    c.DilationHeight = (uint32_t)problem.DilationHeight;
+    c.DilationWidth = (uint32_t)problem.DilationWidth;
+    c.PadTop = (uint32_t)problem.PadTop;
+    c.PadLeft = (uint32_t)problem.PadLeft;
+    c.PadBottom = (uint32_t)problem.PadBottom;
+    c.PadRight = (uint32_t)problem.PadRight;
+    c.Groups = (uint32_t)problem.Groups;
+    const uint64_t bytes = og_conv_integer_scratch_bytes(&c);
+    if (bytes == 0 || bytes > (uint64_t)Check::MaxElements)
+        throw GpuKernelShapeException(kConv, "InChannels", "the column matrix of one image is larger than the supported sizes");
+    return (int64_t)bytes;
 }
 
 GpuBuffer ConvIntegerKernels::Own(ElementType t, int64_t bytes)
@@ -1076,9 +1098,7 @@ void ConvIntegerKernels::Encode(GpuCommandEncoder &encoder, const ConvProblem &p
         if (wZeroPoint->Buffer.Type() != w.Type()) throw GpuKernelShapeException(kConv, "wZeroPoint", "the zero point has a different type than w");
         Check::Range(kConv, "wZeroPoint", wZeroPoint->Buffer.Length(), wZeroPoint->Offset, wZeroPoint->IsVector ? p.OutChannels : 1);
     }
-    const int64_t perImage = (int64_t)p.Groups * k * ldb;
-    if (perImage > Check::MaxElements)
-        throw GpuKernelShapeException(kConv, "InChannels", "the column matrix of one image needs " + std::to_string(perImage) + " bytes, more than the supported sizes");
+    const int64_t perImage = ScratchBytesPerImage(p);
     const bool depthwise = DirectDepthwise && p.InChannels == p.Groups;   // one input channel a group: convolved directly
     // x is the matrix as it lies (the library's rule: a 1 x 1 window, unit strides, no padding, 16-byte rows and start)
     const bool pointwise = p.KernelHeight == 1 && p.KernelWidth == 1 && p.StrideHeight == 1 && p.StrideWidth == 1 &&

@@ -346,7 +346,8 @@ struct ConvProblem {
 
 // ONNX ConvInteger (ConvIntegerKernels.cs:6-351): the column matrix and the int8 products, or a direct kernel when
 // every group has one input channel. Same checks, exceptions and scratch rules as the reference; the column rows are
-// padded to 16 bytes here, so ScratchBytesPerImage is Groups * K * round16(OutHeight * OutWidth).
+// padded to 16 bytes here, so ScratchBytesPerImage is Groups * K * round16(OutHeight * OutWidth), with K padded to a
+// multiple of 64 (and room for the weights in rows of that length) when 64 <= K and K % 64 != 0.
 class ConvIntegerKernels {
 public:
     explicit ConvIntegerKernels(std::shared_ptr<GpuDevice> device, Int8GemmOptions options = {},

@@ -125,6 +125,26 @@ def test_model_shapes_are_bit_exact(index):
         assert bad == 0
 
 
+def test_padded_depth_with_groups_and_chunks():
+    # K = CinG * KH * KW not a multiple of 64 (and at least 64) is padded to one: the column matrices get rows of x's
+    # zero point and the weights are copied into padded rows by the pack launch of the first chunk of images. Groups,
+    # caller scratch that holds 1 or 2 images (a batch of 3 runs in chunks, the later chunks reusing the weight copy)
+    # at an offset that leaves the copy to align its own start, and every zero-point form.
+    d = device()
+    conv = og.ConvIntegerKernels(d)
+    base = cases.conv_problem(3, 80, 9, 11, 48, 3, 3, stride=1, pad=1, groups=2)   # K = 40 * 9 = 360 -> 384
+    seed = 900
+    for scratch_images, xs, ws, xzm, wzm in ((1, False, True, 1, 2), (2, True, False, 1, 1), (0, False, False, 0, 2),
+                                             (2, True, True, 1, 0)):
+        c = dict(name=f"padded depth, groups 2, scratch {scratch_images}", p=base, xs=xs, ws=ws, xzm=xzm, wzm=wzm,
+                 fill=-1, scratch_images=scratch_images)
+        say(f"conv {c['name']} signed {xs}/{ws} zp {xzm}/{wzm}")
+        bad, kern = _run_case(d, conv, c, seed)
+        seed += 1
+        assert bad == 0, f"{c['name']}: {bad} elements differ ({kern})"
+        assert kern.startswith("mfma-i8-direct"), kern
+
+
 def test_warm_calls_allocate_nothing_new():
     # WarmCallsBuildNoBindGroups (ConvIntegerTests.cs:331-347): the second identical call reuses the family's columns.
     d = device()

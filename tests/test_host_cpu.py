@@ -235,7 +235,13 @@ def test_conv_integer_geometry():
     assert og.ConvIntegerKernels.ScratchBytesPerImage(p) == 4 * 9 * 32
     q = og.ConvProblem.Conv1D(1, 80, 3000, 768, 3, padBegin=1, padEnd=1)
     assert (q.Height, q.OutHeight, q.OutWidth) == (1, 1, 3000)
-    assert og.ConvIntegerKernels.ScratchBytesPerImage(q) == 240 * 3008
+    # K = 240 is padded to 256, with the weights (768 x 256) in rows of 256 ahead of the columns.
+    assert og.ConvIntegerKernels.ScratchBytesPerImage(q) == 256 * 3008 + 16 + 768 * 256
+    stem = og.ConvProblem(1, 3, 224, 224, 64, 7, 7)
+    stem.StrideHeight = stem.StrideWidth = 2
+    stem.PadTop = stem.PadBottom = stem.PadLeft = stem.PadRight = 3
+    assert (stem.OutHeight, stem.OutWidth) == (112, 112)
+    assert og.ConvIntegerKernels.ScratchBytesPerImage(stem) == 192 * 12544 + 16 + 12288   # K = 147 padded to 192
     r = og.ConvProblem(1, 2, 14, 15, 3, 5, 5)
     r.DilationHeight = r.DilationWidth = 2
     r.PadTop = r.PadBottom = r.PadLeft = r.PadRight = 4
