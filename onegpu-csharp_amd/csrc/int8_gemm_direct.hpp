@@ -14,8 +14,9 @@
 //    (s = u ^ 0x80) after it is read, and the zero points are applied at the store from the byte sums:
 //        sum (s - z')(t - w') = sum s t - w' sum s - z' sum t + K z' w'   (mod 2^32; Int8GemmDot.hlsl:1-11 rearranges the same)
 //  - LDS layouts (16-byte chunks):
-//      A (and B stored N x K): row r of 64 bytes, chunk q at position q ^ ((r >> 1) & 3);
-//      B stored K x N: row k of 256 bytes, chunk c at position c ^ fB(k), fB(k) = (k & 7) | (((k >> 4) & 1) << 3).
+//      A (and B stored N x K): row r of 64 bytes, chunk q at position q ^ ((r >> 2) & 3);
+//      B stored K x N: row k of 256 bytes, chunk c at position c ^ fB(k), fB(k) = 2 (k & 7) | ((k >> 4) & 1)
+//      (128-byte rows at the 128 tile: c ^ (k & 7)).
 //    A buffer load writes 64 lanes x 16 bytes to consecutive LDS, so each lane loads the global chunk that belongs in
 //    its slot.
 //  - An A fragment (lane l: row l % 32, k 16 (l / 32) .. + 15 of a 32-deep half stage) is one ds_read_b128. A B
@@ -78,12 +79,16 @@ __device__ __forceinline__ void dma16(u4w rsrc, uint32_t base, uint32_t voff)
                  "s"(rsrc) : "memory");
 }
 
-__device__ __forceinline__ int a_pos(int r, int q) { return q ^ ((r >> 1) & 3); }
+// LDS serves 256 bytes a cycle: a 16-byte fragment read takes 16 lanes at a time (rows r .. r + 15 of A: the
+// position must differ across r & 3 and (r >> 2) & 3), a transpose read of 8 bytes 32 lanes (8 rows of B x two
+// neighbouring chunks c and c ^ 1: at 256-byte rows the 16 positions must all differ, so the rows take even offsets
+// and the chunk pair fills the odd ones). rocprofv3 counts no bank conflicts with these (SQ_LDS_BANK_CONFLICT = 0).
+__device__ __forceinline__ int a_pos(int r, int q) { return q ^ ((r >> 2) & 3); }
 template <int BT>
 __device__ __forceinline__ int b_pos(int k, int c)
 {
-    if constexpr (BT == 256) return c ^ ((k & 7) | (((k >> 4) & 1) << 3));
-    else return c ^ (k & 7);
+    if constexpr (BT == 256) return c ^ ((2 * (k & 7)) | ((k >> 4) & 1));
+    else return c ^ (k & 7);   // 128-byte rows: the row's parity picks the bank half, k & 7 the rest
 }
 
 // Waits until at most N of this wave's DMA loads are outstanding, then meets the other waves. A compiler barrier as
