@@ -593,3 +593,38 @@ def test_golden_fixtures_on_every_kernel():
         run(d, lambda e: gemm.EncodeInt32(e, og.Int8GemmProblem(2, 3, 2), ca, cb, c2))
         bad += int(np.count_nonzero(c2.Read() != cf["c"]))
     assert bad == 0
+
+
+@pytest.mark.parametrize("config", ["default", "tiled only", "large tile"])
+def test_seeded_random_products_are_bit_exact(config):
+    # A seeded sweep beyond the reference's case lists: shapes, batches (shared or distinct B), both layouts of B,
+    # signedness and zero-point modes, in three kinds of case: aligned rows with K a multiple of 64 (the direct and
+    # few-rows kernels), aligned rows with K a multiple of 16 only (the register-staged tiles), and odd offsets with
+    # padded rows (the generic kernel). Every product against the oracle, sentinels included.
+    d = device()
+    gemm = dict(configs(d, True))[config]
+    rng = np.random.default_rng({"default": 11, "tiled only": 12, "large tile": 13}[config])
+    bad, kernels = 0, set()
+    for i in range(40):
+        kind = i % 3
+        batch = int(rng.choice([1, 1, 1, 2, 3]))
+        trans = bool(rng.integers(0, 2))
+        if kind < 2:
+            m = int(rng.choice([1, 4, 16, 63, 128, 130, 256, 300]))
+            n = 16 * int(rng.integers(1, 33))
+            k = 64 * int(rng.integers(1, 17)) if kind == 0 else 16 * int(rng.integers(1, 40)) // 64 * 64 + 16 * int(rng.integers(1, 4))
+            offs = {}
+        else:
+            m, n, k = (int(rng.integers(1, 300)) for _ in range(3))
+            offs = dict(off_a=int(rng.integers(0, 20)), off_b=int(rng.integers(0, 20)), off_c=int(rng.integers(0, 9)),
+                        lda_extra=int(rng.integers(0, 9)), ldb_extra=int(rng.integers(0, 9)))
+        share = batch > 1 and bool(rng.integers(0, 2))
+        c = cases.Case(f"random {i}: {m}x{n}x{k} b{batch}{' shared B' if share else ''}{' T' if trans else ''}",
+                       cases.problem(m, n, k, batch=batch, trans_b=trans, share_b=share, **offs),
+                       bool(rng.integers(0, 2)), bool(rng.integers(0, 2)), int(rng.integers(0, 3)), int(rng.integers(0, 3)))
+        say(f"[{config}] {c.name} signed {c.a_signed}/{c.b_signed} zp {c.za_mode}/{c.zb_mode} {offs}")
+        here, kern = run_int32(d, gemm, c, 5000 + i)
+        kernels.add(kern)
+        assert here == 0, f"{c.name} [{config}, {kern}]: {here} wrong"
+        bad += here
+    say(f"ROW seeded random products [{config}]: 40 cases, mismatches {bad}; kernels {sorted(kernels)}")
