@@ -177,3 +177,36 @@ def test_products_wider_than_one_grid_axis_are_bit_exact(m, n):
         bad = int(np.count_nonzero(bc.Read() != want))
         say(f"ROW wide product {m} x {n} x {k} [{d.LastKernel}]: {bad} elements differ")
         assert bad == 0
+
+
+def test_seeded_random_convolutions_are_bit_exact():
+    # A seeded sweep of geometries beyond the reference's lists: batches, channel and group counts (depthwise among
+    # them), windows, strides, dilations and paddings chosen per axis, every signedness and zero-point form; depths of
+    # 64 and more that are not multiples of 64 take the padded pack. Each against the oracle, output sentinels included.
+    d = device()
+    conv = og.ConvIntegerKernels(d)
+    rng = np.random.default_rng(77)
+    kernels = set()
+    for i in range(30):
+        groups = int(rng.choice([1, 1, 2, 3, 4]))
+        cin_g, cout_g = int(rng.integers(1, 24)), int(rng.integers(1, 20))
+        if i % 5 == 4:
+            cin_g = 1   # depthwise-shaped groups
+            groups = int(rng.integers(2, 9))
+        kh, kw = int(rng.integers(1, 6)), int(rng.integers(1, 6))
+        sh, sw, dh, dw = (int(rng.integers(1, 4)) for _ in range(4))
+        pt, pb, pl, pr = (int(rng.integers(0, 3)) for _ in range(4))
+        h = int(rng.integers(max(1, dh * (kh - 1) + 1 - pt - pb), 24))
+        w = int(rng.integers(max(1, dw * (kw - 1) + 1 - pl - pr), 24))
+        p = cases.conv_problem(int(rng.integers(1, 4)), cin_g * groups, h, w, cout_g * groups, kh, kw, groups=groups)
+        p.update(StrideHeight=sh, StrideWidth=sw, DilationHeight=dh, DilationWidth=dw, PadTop=pt, PadBottom=pb,
+                 PadLeft=pl, PadRight=pr)
+        s = int(rng.integers(0, 4))
+        c = dict(name=f"random {i}: {p['Batch']}x{p['InChannels']}x{h}x{w} -> {p['OutChannels']}, {kh}x{kw} s{sh},{sw} "
+                      f"d{dh},{dw} groups {groups}", p=p, xs=(s & 1) != 0, ws=(s & 2) != 0, xzm=int(rng.integers(0, 2)),
+                 wzm=int(rng.integers(0, 3)), fill=-1, scratch_images=int(rng.integers(0, 3)))
+        say(f"conv {c['name']} signed {c['xs']}/{c['ws']} zp {c['xzm']}/{c['wzm']} scratch {c['scratch_images']}")
+        bad, kern = _run_case(d, conv, c, 3000 + i)
+        kernels.add(kern)
+        assert bad == 0, f"{c['name']}: {bad} elements differ ({kern})"
+    say(f"ROW seeded random convolutions: 30 geometries exact; kernels {sorted(kernels)}")
