@@ -628,3 +628,31 @@ def test_seeded_random_products_are_bit_exact(config):
         assert here == 0, f"{c.name} [{config}, {kern}]: {here} wrong"
         bad += here
     say(f"ROW seeded random products [{config}]: 40 cases, mismatches {bad}; kernels {sorted(kernels)}")
+
+
+@pytest.mark.parametrize("config", ["default", "large tile"])
+def test_seeded_random_epilogues_are_bit_exact(config):
+    # The float (scale per tensor or column, int and float biases) and requantized (multiplier per tensor or column,
+    # either output type, zero point, bias) epilogues on seeded random shapes, aligned (the direct and few-rows kernels)
+    # and not; the requantized ones both fused into the product's store and as the separate pass.
+    d = device()
+    rng = np.random.default_rng({"default": 21, "large tile": 22}[config])
+    fused = og.Int8Gemm(d, og.Int8GemmOptions(**CONFIG_OPTIONS[config], FusedRequantize=True))
+    passes = og.Int8Gemm(d, og.Int8GemmOptions(**CONFIG_OPTIONS[config], FusedRequantize=False))
+    bad, kernels = 0, set()
+    for i in range(24):
+        if i % 2 == 0:
+            m, n, k = int(rng.choice([1, 3, 16, 100, 128, 257])), 16 * int(rng.integers(1, 40)), 64 * int(rng.integers(1, 12))
+        else:
+            m, n, k = (int(rng.integers(1, 260)) for _ in range(3))
+        vec, ib, fb = (bool(rng.integers(0, 2)) for _ in range(3))
+        say(f"[{config}] epilogues {m}x{n}x{k} vec {vec} ib {ib} fb {fb}")
+        bad += _float_case(d, fused, m, n, k, vec, ib, fb, 6000 + i)
+        kernels.add(d.LastKernel)
+        unsigned, zero = cases.REQUANT_OUT[i % len(cases.REQUANT_OUT)]
+        for gemm in (fused, passes):
+            bad += _requant_case(d, gemm, m, n, k, vec, unsigned, zero, ib, 6100 + i, bool(rng.integers(0, 2)),
+                                 bool(rng.integers(0, 2)))
+            kernels.add(d.LastKernel)
+        assert bad == 0, f"{m}x{n}x{k}: {bad} wrong"
+    say(f"ROW seeded random epilogues [{config}]: 24 shapes exact; kernels {sorted(kernels)}")
