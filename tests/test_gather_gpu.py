@@ -153,3 +153,32 @@ def test_int8_embedding_lookups_are_exact(vocab, hidden):
         bad = int(np.count_nonzero(got != want))
         say(f"ROW int8 embedding {vocab} x {hidden}, {batch} x 512 tokens ({d.LastKernel}): wrong bytes {bad}")
         assert bad == 0
+
+
+def test_seeded_random_gathers_are_exact():
+    # Seeded random ranks, extents, axes, index counts, payload widths and index types; indices drawn from the whole
+    # valid range with negatives, and in every third case a few out of range (zero rows and the smallest position).
+    # GatherCase's offsets (GatherTests.cs:6) leave the rows unaligned, so these take the byte copies; the 16-byte
+    # copies have the aligned and embedding tests above.
+    d = device()
+    k = og.GatherKernels(d)
+    rng = np.random.default_rng(99)
+    kernels = set()
+    for i in range(40):
+        rank = int(rng.integers(1, 5))
+        shape = [int(rng.integers(1, 9)) for _ in range(rank)]
+        if rng.integers(0, 2):
+            shape[-1] = int(rng.choice([16, 48, 64, 384]))   # rows that can take the 16-byte copies
+        axis = int(rng.integers(0, rank))
+        count = int(rng.integers(1, 40))
+        dtype, itype = PAYLOADS[int(rng.integers(0, len(PAYLOADS)))]
+        n_axis = shape[axis]
+        vals = rng.integers(-n_axis, n_axis, count)
+        if i % 3 == 2 and count > 0:
+            for j in rng.integers(0, count, 2):
+                vals[j] = n_axis + int(rng.integers(0, 5)) if rng.integers(0, 2) else -n_axis - 1 - int(rng.integers(0, 5))
+        say(f"gather random {i}: shape {shape} axis {axis} count {count} {np.dtype(dtype).name}/{np.dtype(itype).name}")
+        bad, _, kern = _gather_case(d, k, dtype, itype, shape, axis, count, 700 + i, idx_values=vals.tolist())
+        kernels.add(kern)
+        assert bad == 0, f"case {i}: {bad} wrong"
+    say(f"ROW seeded random gathers: 40 cases exact; kernels {sorted(kernels)}")
