@@ -8,8 +8,8 @@
 // of 16 bytes (ldb) so that the MFMA product can feed them to LDS with 16-byte DMA; the padding columns hold the zero
 // point too and the product never reads them. One thread writes 16 bytes of one row.
 //
-// Padded depth: when K is not a multiple of 64 the launcher pads it to one (kp), so that the products take the
-// LDS-DMA kernel. Rows k .. kp - 1 of every column matrix hold x's zero point, so each padded tap adds
+// Padded depth: when K is at least 64 and not a multiple of 64, the launcher pads it to one (kp) so that the products
+// take the LDS-DMA kernel. Rows k .. kp - 1 of every column matrix hold x's zero point, so each padded tap adds
 // (w - wz) (xz - xz) = 0, and the same launch copies the weights into rows of kp bytes, zero past k; the 16-byte
 // chunks of both go through one grid-stride loop (the column chunks first).
 //
