@@ -70,7 +70,19 @@ __global__ __launch_bounds__(DQ_THREADS) void k_dq_minmax(const float *x, uint32
     if (((uintptr_t)x & 15) == 0) {
         const uint32_t n4 = count / 4;
         const f4 *x4 = reinterpret_cast<const f4 *>(x);
-        for (uint32_t i = tid; i < n4; i += nthreads) {
+        // Four 16-byte loads in flight a thread (each instruction still reads contiguous memory across the wave): a
+        // loop of one load a trip waits out a whole memory round trip per trip.
+        uint32_t i = tid;
+        for (; i + 3 * nthreads < n4; i += 4 * nthreads) {
+            f4 v[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) v[q] = __builtin_nontemporal_load(&x4[i + q * nthreads]);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                minmax_acc(v[q].x, mn, mx); minmax_acc(v[q].y, mn, mx); minmax_acc(v[q].z, mn, mx); minmax_acc(v[q].w, mn, mx);
+            }
+        }
+        for (; i < n4; i += nthreads) {
             f4 v = __builtin_nontemporal_load(&x4[i]);
             minmax_acc(v.x, mn, mx); minmax_acc(v.y, mn, mx); minmax_acc(v.z, mn, mx); minmax_acc(v.w, mn, mx);
         }
