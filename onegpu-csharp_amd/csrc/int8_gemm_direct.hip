@@ -78,8 +78,22 @@ __global__ __launch_bounds__(256) void k_splitk_sum(GemmArgs g, int32_t ks, cons
         const int32_t n = (int32_t)(r % g.N);
         const int32_t *p = parts + b * ks * mn + r;
         if constexpr (V4) {
+            // Four slices' loads in flight at a time (a trip of one load waits out a memory round trip per slice).
             uint4 sum = make_uint4(0u, 0u, 0u, 0u);
-            for (int32_t kc = 0; kc < ks; kc++) {
+            int32_t kc = 0;
+            for (; kc + 4 <= ks; kc += 4) {
+                uint4 v[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) v[u] = *reinterpret_cast<const uint4 *>(p + (kc + u) * mn);
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    sum.x += v[u].x;
+                    sum.y += v[u].y;
+                    sum.z += v[u].z;
+                    sum.w += v[u].w;
+                }
+            }
+            for (; kc < ks; kc++) {
                 const uint4 v = *reinterpret_cast<const uint4 *>(p + kc * mn);
                 sum.x += v.x;
                 sum.y += v.y;
