@@ -107,7 +107,14 @@ __global__ __launch_bounds__(256) void k_splitk_sum(GemmArgs g, int32_t ks, cons
             store_value(g, c + 3, n + 3, sum.w);
         } else {
             uint32_t sum = 0;
-            for (int32_t kc = 0; kc < ks; kc++) sum += (uint32_t)p[kc * mn];
+            int32_t kc = 0;
+            for (; kc + 4 <= ks; kc += 4) {
+                uint32_t v[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) v[u] = (uint32_t)p[(kc + u) * mn];
+                sum += v[0] + v[1] + v[2] + v[3];
+            }
+            for (; kc < ks; kc++) sum += (uint32_t)p[kc * mn];
             store_value(g, b * g.strideC + r, n, sum);
         }
     }
