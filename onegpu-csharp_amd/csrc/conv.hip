@@ -107,7 +107,9 @@ __global__ __launch_bounds__(kConvThreads) void k_conv_pack(ConvPackArgs a)
     }
 }
 
-template <bool XS, bool WS>
+// K3: the window is 3 x 3 (known at compile time), so the nine taps' loads are all issued before the first is used
+// (a tap in the padding loads the plane's first byte and adds nothing); otherwise a loop over the window.
+template <bool XS, bool WS, bool K3>
 __global__ __launch_bounds__(kConvThreads) void k_conv_depthwise(ConvDepthwiseArgs a)
 {
     const int64_t plane = (int64_t)a.oh * a.ow;
@@ -124,6 +126,28 @@ __global__ __launch_bounds__(kConvThreads) void k_conv_depthwise(ConvDepthwiseAr
         const uint8_t *wp = a.wt + (int64_t)m * a.kh * a.kw;
         const int32_t wz = a.wz ? byte_val(a.wz[a.wz_per_channel ? m : 0], WS) : 0;
         uint32_t acc = 0;
+        if constexpr (K3) {
+            int64_t off[9];
+            bool in[9];
+#pragma unroll
+            for (int q = 0; q < 9; q++) {
+                const int64_t ih = (int64_t)i * a.sh + (int64_t)(q / 3) * a.dh - a.ph;
+                const int64_t iw = (int64_t)j * a.sw + (int64_t)(q % 3) * a.dw - a.pw;
+                in[q] = ih >= 0 && ih < a.h && iw >= 0 && iw < a.w;
+                off[q] = in[q] ? ih * a.w + iw : 0;
+            }
+            uint8_t xv[9], wv[9];
+#pragma unroll
+            for (int q = 0; q < 9; q++) {
+                xv[q] = xp[off[q]];
+                wv[q] = wp[q];
+            }
+#pragma unroll
+            for (int q = 0; q < 9; q++)
+                if (in[q]) acc += (uint32_t)(byte_val(xv[q], XS) - xz) * (uint32_t)(byte_val(wv[q], WS) - wz);
+            a.y[t] = (int32_t)acc;
+            continue;
+        }
         for (int32_t kh = 0; kh < a.kh; kh++) {
             const int64_t ih = (int64_t)i * a.sh + (int64_t)kh * a.dh - a.ph;
             if (ih < 0 || ih >= a.h) continue;
@@ -163,13 +187,19 @@ hipError_t launch_conv_depthwise(const ConvDepthwiseArgs &a, hipStream_t s, cons
     const int64_t total = (int64_t)a.batch * a.cout * a.oh * a.ow;
     if (total == 0) return hipSuccess;
     const dim3 grid((uint32_t)conv_grid(total)), block(kConvThreads);
+#define OG_DW(XS, WS)                                                                                     \
+    do {                                                                                                 \
+        if (a.kh == 3 && a.kw == 3) hipLaunchKernelGGL((k_conv_depthwise<XS, WS, true>), grid, block, 0, s, a);  \
+        else hipLaunchKernelGGL((k_conv_depthwise<XS, WS, false>), grid, block, 0, s, a);                       \
+    } while (0)
     if (a.x_signed) {
-        if (a.w_signed) hipLaunchKernelGGL((k_conv_depthwise<true, true>), grid, block, 0, s, a);
-        else hipLaunchKernelGGL((k_conv_depthwise<true, false>), grid, block, 0, s, a);
+        if (a.w_signed) OG_DW(true, true);
+        else OG_DW(true, false);
     } else {
-        if (a.w_signed) hipLaunchKernelGGL((k_conv_depthwise<false, true>), grid, block, 0, s, a);
-        else hipLaunchKernelGGL((k_conv_depthwise<false, false>), grid, block, 0, s, a);
+        if (a.w_signed) OG_DW(false, true);
+        else OG_DW(false, false);
     }
+#undef OG_DW
     return hipGetLastError();
 }
 
