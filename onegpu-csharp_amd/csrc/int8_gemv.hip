@@ -80,10 +80,20 @@ __global__ __launch_bounds__(256) void k_gemm_skinny(GemmArgs g, int32_t ks, int
     for (int32_t k0 = k_begin; k0 < k_end; k0 += 64) {
         uint4 av = load_row16_s(arow, k0 + 16 * g4, k_end, row_ok, vec_a, flip_a);
         uint32_t rb[16];
+        if (vec_b && n + 4 <= g.N && k0 + 16 * g4 + 16 <= k_end) {
+            // All 16 rows and 4 columns in range: 16 word loads in flight together.
+            const uint8_t *bp = B + (int64_t)(k0 + 16 * g4) * g.ldb + n;
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            int32_t gk = k0 + 16 * g4 + r;
-            rb[r] = load_cols4_s(B + (int64_t)gk * g.ldb, n, g.N, gk < k_end, vec_b, flip_b);
+            for (int r = 0; r < 16; r++)
+                rb[r] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(bp + (int64_t)r * g.ldb));
+#pragma unroll
+            for (int r = 0; r < 16; r++) rb[r] ^= flip_b;
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                int32_t gk = k0 + 16 * g4 + r;
+                rb[r] = load_cols4_s(B + (int64_t)gk * g.ldb, n, g.N, gk < k_end, vec_b, flip_b);
+            }
         }
         uint32_t col[4][4];
 #pragma unroll
