@@ -166,8 +166,17 @@ __global__ __launch_bounds__(256) void k_gemm_skinny_reduce(GemmArgs g, int32_t 
     const int32_t m = (int32_t)(r / g.N), n = (int32_t)(r % g.N);
     const int32_t *p = partials + ((int64_t)batch * slices * g.M + m) * np + n;
     const int64_t slice_stride = (int64_t)g.M * np;
+    // Eight slices' loads in flight at a time (a trip of one load waits out a memory round trip per slice).
     uint32_t v = 0;
-    for (int32_t s = 0; s < slices; s++) v += (uint32_t)p[s * slice_stride];
+    int32_t s = 0;
+    for (; s + 8 <= slices; s += 8) {
+        uint32_t x[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) x[u] = (uint32_t)p[(s + u) * slice_stride];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v += x[u];
+    }
+    for (; s < slices; s++) v += (uint32_t)p[s * slice_stride];
     store_value(g, batch * g.strideC + (int64_t)m * g.N + n, n, v);
 }
 
