@@ -19,6 +19,11 @@
  *    message)); OG_ERR_UNSUPPORTED maps to GpuUnsupportedException, OG_ERR_OUT_OF_MEMORY to GpuOutOfMemoryException,
  *    OG_ERR_DEVICE_LOST to GpuDeviceLostException, OG_ERR_LAUNCH_FAILED to GpuCommandFailedException.
  *  - Like the reference families, a context is not thread-safe (src/RecursiveAI.OneGpu.Kernels/Int8Gemm.cs:122).
+ *  - Workspace: a context owns its partial-sum workspace and the few-rows kernel's arrival words. A product that needs
+ *    more than the context holds grows them first; growth is refused with OG_ERR_INVALID_ARG (argument "workspace")
+ *    while the context's stream is being captured into a HIP graph, so capture a product only after one of at least
+ *    its size has run on the context. Replaced workspaces stay allocated until og_destroy, so a graph captured earlier
+ *    never replays into freed memory.
  */
 #ifndef ONEGPU_HIP_H
 #define ONEGPU_HIP_H
@@ -62,7 +67,9 @@ int og_device_name(og_ctx *ctx, char *buf, size_t len);
 int og_device_limits(og_ctx *ctx, uint64_t *max_buffer_bytes, uint32_t *compute_units, uint32_t *lds_bytes_per_group);
 /* The hipStream_t the context records on, for callers that interleave their own work. */
 int og_stream(og_ctx *ctx, void **hip_stream);
-/* Waits for everything recorded so far (GpuDevice.WaitIdle); reports a failed launch as OG_ERR_LAUNCH_FAILED. */
+/* Waits for everything recorded so far (GpuDevice.WaitIdle); reports a failed launch as OG_ERR_LAUNCH_FAILED, and so
+ * a one-launch few-rows product whose column slab did not run on one XCD (its output may then be wrong; the context
+ * uses the two-launch form from then on). */
 int og_sync(og_ctx *ctx);
 /* Buffers (GpuDevice.CreateBuffer / GpuBuffer<T>.Dispose, GpuBufferOfT.cs:11-89). */
 int og_alloc(og_ctx *ctx, uint64_t bytes, void **dptr);
@@ -125,6 +132,7 @@ typedef struct og_int8_gemm_params {
 #define OG_GEMM_NO_DIRECT     0x1000u /* never use the few-rows kernel's single-pass form (always split k) */
 #define OG_GEMM_LARGE_TILE    0x2000u /* take the 256 x 256 tile kernels whatever the size (with NO_SKINNY: every shape) */
 #define OG_GEMM_NO_STREAM     0x4000u /* never use the tiled few-rows kernel (the split-k one instead) */
+#define OG_GEMM_TWO_PASS      0x8000u /* the tiled few-rows kernel in two launches (its parts added by a second kernel) */
 
 /* Epi (Int8GemmEpilogue.hlsli:1-12): bit 0 float32 result, bit 1 int32 bias per column, bit 2 scale per column (else one),
  * bit 3 float32 bias per column. 0 stores the raw int32 sums. */

@@ -17,6 +17,16 @@ struct og_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
     og::Workspace ws{};
+    // Workspaces replaced by larger ones: work recorded earlier (or captured into a graph) may still name them, so
+    // they are freed only by og_destroy.
+    std::vector<void *> retired;
+    // The one-launch few-rows kernel's words (one a column slab, zero between launches) and the flag it raises in
+    // host memory if a slab's tiles did not share an XCD or its parts were never all counted; xcd_local: og_init's
+    // probe saw workgroup ids dealt round-robin to the XCDs, so that kernel may run.
+    unsigned long long *xcd_words = nullptr;
+    uint64_t xcd_word_count = 0;
+    uint32_t *xcd_flag = nullptr;
+    bool xcd_local = false;
     std::string error;
     std::string argument;
     const char *last_kernel = "";
@@ -98,20 +108,73 @@ bool fits(uint64_t offset_bytes, uint64_t extent_bytes, const og_buffer &b)
     return offset_bytes <= b.bytes && extent_bytes <= b.bytes - offset_bytes;
 }
 
+// A workspace must grow: refused while the stream is being captured into a graph (the allocation would not be part
+// of the graph, and a replay must not find its memory freed); otherwise allowed, and the caller retires the old one.
+int growth_allowed(og_ctx *ctx, const char *what)
+{
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(ctx->stream, &cs);
+    if (e != hipSuccess) return hip_status(ctx, e, what);
+    if (cs != hipStreamCaptureStatusNone)
+        return fail(ctx, OG_ERR_INVALID_ARG, "workspace",
+                    "%s must grow while the stream is being captured: run one product of this size before capturing", what);
+    return OG_OK;
+}
+
 int ensure_partials(og_ctx *ctx, uint64_t bytes)
 {
     if (bytes <= ctx->ws.partial_bytes) return OG_OK;
-    // Grow geometrically, outside any launch; the old region may still be in use by recorded work, so wait first.
+    int st = growth_allowed(ctx, "the partial-sum workspace");
+    if (st != OG_OK) return st;
+    // Grow geometrically. Work already recorded may still use the old region, and a graph captured earlier may name
+    // it, so it is kept until og_destroy rather than freed.
     uint64_t size = ctx->ws.partial_bytes * 2 > bytes ? ctx->ws.partial_bytes * 2 : bytes;
-    hipError_t e = hipStreamSynchronize(ctx->stream);
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, size);
     if (e != hipSuccess) return hip_status(ctx, e, "workspace");
-    if (ctx->ws.partials) (void)hipFree(ctx->ws.partials);
-    ctx->ws.partials = nullptr;
-    ctx->ws.partial_bytes = 0;
-    e = hipMalloc(&ctx->ws.partials, size);
-    if (e != hipSuccess) return hip_status(ctx, e, "workspace");
+    if (ctx->ws.partials) ctx->retired.push_back(ctx->ws.partials);
+    ctx->ws.partials = static_cast<int32_t *>(p);
     ctx->ws.partial_bytes = size;
     return OG_OK;
+}
+
+// The one-launch few-rows kernel's words: zero when allocated, and every launch leaves them zero.
+int ensure_xcd_words(og_ctx *ctx, uint64_t words)
+{
+    if (words <= ctx->xcd_word_count) return OG_OK;
+    int st = growth_allowed(ctx, "the few-rows count words");
+    if (st != OG_OK) return st;
+    uint64_t n = ctx->xcd_word_count * 2 > words ? ctx->xcd_word_count * 2 : words;
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, n * 8);
+    if (e == hipSuccess) e = og::launch_fill_bytes(p, 0, n * 8, ctx->stream);
+    if (e != hipSuccess) {
+        if (p) (void)hipFree(p);
+        return hip_status(ctx, e, "workspace");
+    }
+    if (ctx->xcd_words) ctx->retired.push_back(ctx->xcd_words);
+    ctx->xcd_words = static_cast<unsigned long long *>(p);
+    ctx->xcd_word_count = n;
+    return OG_OK;
+}
+
+// Whether this device deals workgroup ids round-robin to its XCDs (id x on XCD (x + c) % 8 for one c a launch), which
+// the one-launch few-rows kernel needs: all tiles of a column slab have ids equal modulo 8. Two probe launches of
+// 4096 workgroups record where each ran.
+bool probe_xcd_mapping(og_ctx *ctx)
+{
+    constexpr uint32_t kGroups = 4096;
+    uint32_t *d = nullptr;
+    std::vector<uint32_t> h(kGroups);
+    bool good = hipMalloc(&d, kGroups * 4) == hipSuccess;
+    for (int rep = 0; good && rep < 2; rep++) {
+        good = og::launch_xcc_probe(d, kGroups, ctx->stream) == hipSuccess &&
+               hipMemcpyAsync(h.data(), d, kGroups * 4, hipMemcpyDeviceToHost, ctx->stream) == hipSuccess &&
+               hipStreamSynchronize(ctx->stream) == hipSuccess;
+        for (uint32_t x = 0; good && x < kGroups; x++) good = h[x] == ((h[0] + x) & 7u);
+    }
+    if (d) (void)hipFree(d);
+    return good;
 }
 
 }  // namespace
@@ -162,6 +225,14 @@ int og_init(int device_ordinal, og_ctx **out)
             (void)hipFree(p);
         }
     }
+    if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void **>(&ctx->xcd_flag), sizeof(uint32_t), hipHostMallocDefault);
+    if (e == hipSuccess) {
+        *ctx->xcd_flag = 0;
+        ctx->xcd_local = probe_xcd_mapping(ctx);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess && ensure_xcd_words(ctx, 4096) != OG_OK) e = hipErrorOutOfMemory;
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) {
         int st = hip_status(nullptr, e, "og_init");
         og_destroy(ctx);
@@ -187,6 +258,9 @@ int og_destroy(og_ctx *ctx)
     if (ctx->region_stop) (void)hipEventDestroy(ctx->region_stop);
     if (ctx->ws.partials) (void)hipFree(ctx->ws.partials);
     if (ctx->ws.dq_ranges) (void)hipFree(ctx->ws.dq_ranges);
+    if (ctx->xcd_words) (void)hipFree(ctx->xcd_words);
+    for (void *p : ctx->retired) (void)hipFree(p);
+    if (ctx->xcd_flag) (void)hipHostFree(ctx->xcd_flag);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return OG_OK;
@@ -220,6 +294,19 @@ int og_sync(og_ctx *ctx)
     if (!ctx) return fail(ctx, OG_ERR_INVALID_ARG, "ctx", "null context");
     (void)hipSetDevice(ctx->device);
     int st = hip_status(ctx, hipStreamSynchronize(ctx->stream), "og_sync");
+    if (st == OG_OK && ctx->xcd_flag && __atomic_load_n(ctx->xcd_flag, __ATOMIC_ACQUIRE) != 0) {
+        // A one-launch few-rows product found a column slab's tiles on different XCDs (flag 1: its sums may be
+        // wrong) or gave up waiting for a slab's parts (flag 2: that slab's columns of C were not written). The
+        // context stops using that kernel.
+        const uint32_t why = *ctx->xcd_flag;
+        *ctx->xcd_flag = 0;
+        ctx->xcd_local = false;
+        return fail(ctx, OG_ERR_LAUNCH_FAILED, nullptr,
+                    why == 2 ? "og_sync: a one-launch few-rows product timed out waiting for a column slab's parts; "
+                               "its output is incomplete and the two-launch form is used from now on"
+                             : "og_sync: a one-launch few-rows product ran a column slab's tiles on different XCDs; "
+                               "its output may be wrong and the two-launch form is used from now on");
+    }
     return st == OG_OK ? ok(ctx) : st;
 }
 
@@ -370,6 +457,7 @@ const char *gemm_kernel_name(GemmKernel k)
     case GemmKernel::Skinny: return "mfma-i8-rows16-splitk";
     case GemmKernel::SkinnyDirect: return "mfma-i8-rows16-direct";
     case GemmKernel::RowTiles: return "mfma-i8-rows16-tiles";
+    case GemmKernel::RowXcd: return "mfma-i8-rows16-xcd";
     default: return "mfma-i8-tile128x128x64";
     }
 }
@@ -379,7 +467,8 @@ const char *gemm_kernel_name(GemmKernel k)
 extern "C" {
 
 static const uint32_t kKnownGemmFlags =
-    0x7Fu | 0x380u | OG_GEMM_PORTABLE | OG_GEMM_NO_SKINNY | OG_GEMM_NO_DIRECT | OG_GEMM_LARGE_TILE | OG_GEMM_NO_STREAM;
+    0x7Fu | 0x380u | OG_GEMM_PORTABLE | OG_GEMM_NO_SKINNY | OG_GEMM_NO_DIRECT | OG_GEMM_LARGE_TILE | OG_GEMM_NO_STREAM |
+    OG_GEMM_TWO_PASS;
 
 // Checks the parameter block alone; returns OG_OK or the failing status (message and argument set).
 // `requant`: the parameters of og_int8_gemm_requantized, whose Epi holds only the int bias and per-column bits.
@@ -447,9 +536,12 @@ int og_int8_gemm_kernel_name(const og_int8_gemm_params *p, uint32_t batch, char 
         else name = large ? "mfma-i8-tile256x256x64" : "mfma-i8-tile128x128x128";
     }
     // The few-rows products take the tiled kernel when the operands' rows are aligned.
+    // In one launch unless asked for two (a context whose probe found no round-robin XCD mapping runs two as well:
+    // og_last_kernel then names the kernel that ran).
     if ((k == og::GemmKernel::Skinny || k == og::GemmKernel::SkinnyDirect) && !(p->Flags & OG_GEMM_NO_STREAM) &&
         og::gemv_tiles_ok(g))
-        name = og::gemm_kernel_name(og::GemmKernel::RowTiles);
+        name = og::gemm_kernel_name(!(p->Flags & OG_GEMM_TWO_PASS) && og::gemv_xcd_ok(g) ? og::GemmKernel::RowXcd
+                                                                                         : og::GemmKernel::RowTiles);
     snprintf(buf, len, "%s", name);
     return OG_OK;
 }
@@ -462,7 +554,8 @@ static int launch_product(og_ctx *ctx, const og::GemmArgs &g)
     og::GemmKernel k = og::choose_gemm_kernel(g.M, g.N, g.K, g.batch, g.flags);
     if ((k == og::GemmKernel::Skinny || k == og::GemmKernel::SkinnyDirect) && !(g.flags & OG_GEMM_NO_STREAM) &&
         og::gemv_tiles_ok(g))
-        k = og::GemmKernel::RowTiles;
+        k = ctx->xcd_local && !(g.flags & OG_GEMM_TWO_PASS) && og::gemv_xcd_ok(g) ? og::GemmKernel::RowXcd
+                                                                                 : og::GemmKernel::RowTiles;
     switch (k) {
     case og::GemmKernel::Portable:
         st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_portable(g, ctx->stream, n); });
@@ -485,6 +578,14 @@ static int launch_product(og_ctx *ctx, const og::GemmArgs &g)
         st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_tiled(g, ctx->stream, n); });
         break;
     }
+    case og::GemmKernel::RowXcd:
+        st = ensure_partials(ctx, og::gemv_xcd_workspace_bytes(g));
+        if (st == OG_OK) st = ensure_xcd_words(ctx, og::gemv_xcd_words(g));
+        if (st != OG_OK) return st;
+        st = launch(ctx, "og_int8_gemm", [&](const char **n) {
+            return og::launch_gemv_xcd(g, ctx->ws.partials, ctx->xcd_words, ctx->xcd_flag, ctx->stream, n);
+        });
+        break;
     case og::GemmKernel::RowTiles:
         st = ensure_partials(ctx, og::gemv_tiles_workspace_bytes(g));
         if (st != OG_OK) return st;
@@ -768,7 +869,8 @@ int og_conv_integer(og_ctx *ctx, const og_conv_params *p, og_buffer x, og_buffer
     if (!conv_geometry(p, geo)) return fail(ctx, OG_ERR_INVALID_ARG, geo.arg, "%s", geo.msg);
     const uint32_t known = OG_CONV_X_INT8 | OG_CONV_W_INT8 | OG_CONV_XZ | OG_CONV_WZ | OG_CONV_WZ_PER_CHANNEL | OG_CONV_NO_DEPTHWISE;
     if (p->Flags & ~known) return fail(ctx, OG_ERR_INVALID_ARG, "Flags", "unknown flag bits 0x%x", p->Flags & ~known);
-    const uint32_t gemm_known = OG_GEMM_PORTABLE | OG_GEMM_NO_SKINNY | OG_GEMM_NO_DIRECT | OG_GEMM_LARGE_TILE | OG_GEMM_NO_STREAM;
+    const uint32_t gemm_known =
+        OG_GEMM_PORTABLE | OG_GEMM_NO_SKINNY | OG_GEMM_NO_DIRECT | OG_GEMM_LARGE_TILE | OG_GEMM_NO_STREAM | OG_GEMM_TWO_PASS;
     if (p->GemmFlags & ~gemm_known) return fail(ctx, OG_ERR_INVALID_ARG, "GemmFlags", "flag bits 0x%x are not product options", p->GemmFlags & ~gemm_known);
     if ((p->Flags & OG_CONV_WZ_PER_CHANNEL) && !(p->Flags & OG_CONV_WZ)) return fail(ctx, OG_ERR_INVALID_ARG, "Flags", "a per-channel zero point without a zero point");
     const int64_t B = p->Batch;

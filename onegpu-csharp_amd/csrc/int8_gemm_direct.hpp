@@ -70,13 +70,16 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p)
 
 // One LDS DMA: lane l's 16 bytes at rsrc + voff land at LDS address base + OFF + 16 l. Issued from inline assembly
 // so that the compiler neither reorders LDS accesses across it nor adds waits of its own for it: the stages wait for
-// exactly the loads they need (vmcnt counts these loads in issue order). M0 holds the LDS address; nothing else in
-// the kernel uses M0 (no indexed register access, messages or LDS intrinsics), so it is set without being saved.
+// exactly the loads they need (vmcnt counts these loads in issue order). The address is formed outside the
+// assembly (an s_add there would change SCC behind the compiler's back) and moved into M0 with s_mov, which leaves
+// SCC alone. M0 is written without being saved: the compiler reserves M0 and these kernels give it nothing to hold
+// across a DMA (no indexed register access, s_sendmsg, GWS or LDS-DMA intrinsics; checked in the disassembly of
+// every kernel that includes this file: M0 is written only here).
 template <int OFF>
 __device__ __forceinline__ void dma16(u4w rsrc, uint32_t base, uint32_t voff)
 {
-    asm volatile("s_add_u32 m0, %0, %1\n\tbuffer_load_dwordx4 %2, %3, 0 offen lds" : : "s"(base), "n"(OFF), "v"(voff),
-                 "s"(rsrc) : "memory");
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" : : "s"(base + (uint32_t)OFF),
+                 "v"(voff), "s"(rsrc) : "memory");
 }
 
 // LDS serves 256 bytes a cycle: a 16-byte fragment read takes 16 lanes at a time (rows r .. r + 15 of A: the

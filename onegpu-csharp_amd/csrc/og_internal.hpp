@@ -52,7 +52,7 @@ constexpr int kDqMaxGroups = 1024;
 
 
 // Kernel choice for a product, as og_int8_gemm_kernel_name reports it.
-enum class GemmKernel { Portable, Tiled, Skinny, SkinnyDirect, RowTiles };
+enum class GemmKernel { Portable, Tiled, Skinny, SkinnyDirect, RowTiles, RowXcd };
 GemmKernel choose_gemm_kernel(int32_t M, int32_t N, int32_t K, int32_t batch, uint32_t flags);
 const char *gemm_kernel_name(GemmKernel k);
 
@@ -91,6 +91,18 @@ uint64_t skinny_workspace_bytes(int32_t M, int32_t N, int32_t K, int32_t batch);
 bool gemv_tiles_ok(const GemmArgs &g);
 uint64_t gemv_tiles_workspace_bytes(const GemmArgs &g);
 hipError_t launch_gemv_tiles(const GemmArgs &g, const Workspace &ws, hipStream_t s, const char **kernel, int step);
+// The same tiles in one launch: every tile but the last row band of a column slab stores its part into `parts` and
+// counts it in the slab's word of `words`; the last row band's tile waits for the count, adds the parts and stores C.
+// The tiles of a slab run on one XCD (ids equal modulo 8), so the parts pass through that XCD's L2 alone. `words`
+// (gemv_xcd_words 64-bit words) must be zero before the launch and is zero again after it; `flag` is set to 1 if a
+// slab's tiles did not share an XCD, 2 if a slab's parts were never all counted (its columns of C not written).
+bool gemv_xcd_ok(const GemmArgs &g);
+uint64_t gemv_xcd_workspace_bytes(const GemmArgs &g);
+uint64_t gemv_xcd_words(const GemmArgs &g);
+hipError_t launch_gemv_xcd(const GemmArgs &g, int32_t *parts, unsigned long long *words, uint32_t *flag,
+                           hipStream_t s, const char **kernel);
+// out[x] = the XCD (HW_REG_XCC_ID) workgroup x of a `groups`-workgroup launch ran on.
+hipError_t launch_xcc_probe(uint32_t *out, uint32_t groups, hipStream_t s);
 
 struct EpilogueArgs {
     const int32_t *acc;

@@ -590,6 +590,7 @@ static uint32_t OptionFlags(const Int8GemmOptions &o)
     if (o.Tile == 64) flags |= OG_GEMM_NO_SKINNY;
     if (o.Tile == 256) flags |= OG_GEMM_NO_SKINNY | OG_GEMM_LARGE_TILE;
     if (o.Tile == 32) flags |= OG_GEMM_NO_DIRECT | OG_GEMM_NO_STREAM;
+    if (!o.FewRowsOneLaunch) flags |= OG_GEMM_TWO_PASS;
     return flags;
 }
 

@@ -184,6 +184,9 @@ struct Int8GemmOptions {
     // sums (og_int8_gemm_requantized), so no scratch is written. false keeps the reference's two passes (the product
     // into scratch, then Finish). The bytes written are the same either way.
     bool FusedRequantize = true;
+    // This library's own: the tiled few-rows kernel (M <= 16) adds its tiles' parts in the same launch (the last tile
+    // of a column slab finishes it). false keeps the two-launch form (a second kernel adds the parts). Same output.
+    bool FewRowsOneLaunch = true;
 };
 
 // A zero point, scale, multiplier or bias operand (Int8Gemm.cs:23-29).

@@ -169,17 +169,20 @@ PYBIND11_MODULE(_onegpu_host, m)
         .def_property_readonly("Context", [](const GpuDevice &d) { return (uintptr_t)d.Context(); });
 
     py::class_<Int8GemmOptions>(m, "Int8GemmOptions")
-        .def(py::init([](bool allow, int tile, bool fused) {
+        .def(py::init([](bool allow, int tile, bool fused, bool one_launch) {
                  Int8GemmOptions o;
                  o.AllowPackedDot = allow;
                  o.Tile = tile;
                  o.FusedRequantize = fused;
+                 o.FewRowsOneLaunch = one_launch;
                  return o;
              }),
-             py::arg("AllowPackedDot") = true, py::arg("Tile") = 0, py::arg("FusedRequantize") = true)
+             py::arg("AllowPackedDot") = true, py::arg("Tile") = 0, py::arg("FusedRequantize") = true,
+             py::arg("FewRowsOneLaunch") = true)
         .def_readwrite("AllowPackedDot", &Int8GemmOptions::AllowPackedDot)
         .def_readwrite("Tile", &Int8GemmOptions::Tile)
-        .def_readwrite("FusedRequantize", &Int8GemmOptions::FusedRequantize);
+        .def_readwrite("FusedRequantize", &Int8GemmOptions::FusedRequantize)
+        .def_readwrite("FewRowsOneLaunch", &Int8GemmOptions::FewRowsOneLaunch);
 
     py::class_<Int8Operand>(m, "Int8Operand")
         .def(py::init([](GpuBuffer b, int off, bool vec) { return Int8Operand{b, off, vec}; }), py::arg("Buffer"),

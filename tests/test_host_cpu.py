@@ -454,7 +454,10 @@ def test_kernel_choice_is_reported():
     assert name(M=256, N=256, K=64, Ldb=260) == "mfma-i8-tile128x128x128"   # rows of B 4-byte aligned only
     assert name(M=256, N=256, K=64, Lda=72) == "mfma-i8-generic128x128x64"  # rows of A 8-byte aligned only
     assert name(M=256, N=256, K=64, Flags=0x2000) == "mfma-i8-direct256x256x64"
-    assert name(M=1, N=11008, K=4096) == "mfma-i8-rows16-tiles"
+    assert name(M=1, N=11008, K=4096) == "mfma-i8-rows16-xcd"             # 43 slabs: one launch
+    assert name(M=1, N=11008, K=4096, Flags=0x8000) == "mfma-i8-rows16-tiles"   # OG_GEMM_TWO_PASS
+    assert name(M=1, N=1536, K=768) == "mfma-i8-rows16-tiles"             # 12 slabs of 128: under two an XCD
+    assert name(M=16, N=4096, K=4096) == "mfma-i8-rows16-xcd"
     assert name(M=1, N=11008, K=4100) == "mfma-i8-rows16-splitk"          # K % 16 != 0: not tiled
     assert name(M=1, N=11008, K=4096, Flags=0x4000) == "mfma-i8-rows16-splitk"
     assert name(M=1, N=11000, K=4096) == "mfma-i8-rows16-splitk"          # N % 16 != 0: not tiled

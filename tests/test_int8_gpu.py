@@ -143,7 +143,7 @@ def test_float_and_requantized_forms_are_bit_exact(config):
 # Shapes that reach every kernel: few rows on the tiled few-rows kernel (or split k), the 128 and 256 direct kernels
 # (ragged M included), the register-staged 128 tile (K = 96), the generic kernel (unaligned rows), tiny products.
 REQUANT_KERNEL_SHAPES = [(1, 1, 1), (5, 7, 9), (4, 272, 512), (16, 256, 1024), (64, 64, 96), (33, 257, 77),
-                         (128, 384, 384), (130, 256, 512), (2, 8192, 128), (96, 208, 320)]
+                         (128, 384, 384), (130, 256, 512), (2, 8192, 128), (96, 208, 320), (3, 4608, 272)]
 
 
 @pytest.mark.parametrize("fused", [True, False], ids=["one launch", "two passes"])
@@ -167,8 +167,8 @@ def test_requantized_product_on_every_kernel(config, fused):
         f"{sorted(kernels)}")
     assert bad == 0
     if fused and config == "default":
-        assert {"mfma-i8-rows16-tiles", "mfma-i8-direct128x128x64", "mfma-i8-tile128x128x128",
-                "mfma-i8-generic128x128x64"} <= kernels, kernels
+        assert {"mfma-i8-rows16-tiles", "mfma-i8-rows16-xcd", "mfma-i8-direct128x128x64",
+                "mfma-i8-tile128x128x128", "mfma-i8-generic128x128x64"} <= kernels, kernels
     if fused and config == "large tile":
         assert "mfma-i8-direct256x256x64" in kernels, kernels
     if not fused:
@@ -530,33 +530,39 @@ def test_scratch_semantics():
     assert ex.value.Argument == "scratch"
 
 
-@pytest.mark.parametrize("config", ["tiles", "split k"])
+@pytest.mark.parametrize("config", ["tiles", "tiles two launches", "split k"])
 def test_few_rows_kernels_are_bit_exact(config):
-    # The few-rows products (M <= 16, B stored K x N) on the tiled kernel (one workgroup per 256 x 256 tile writing
-    # its part, then a pass adding a slab's parts) and on the split-k one (partial sums per k-slice, then their sum):
-    # one slab or many, one tile per slab or several, K past the last full tile or 64 rows, N past the last full slab,
-    # M = 16 (no spare MFMA row), batches, every signedness and zero-point form; one case three times in a row and a
-    # smaller M after a larger one. Aligned operands; the tiled kernel takes K and N multiples of 16, the split-k one
-    # the rest.
+    # The few-rows products (M <= 16, B stored K x N) on the tiled kernel, in one launch (the last tile of a column slab
+    # adds the slab's parts; shapes with at least 16 slabs) or two (a second kernel adds them), and on the split-k one
+    # (partial sums per k-slice, then their sum): one slab or many, one tile per slab or several, K past the last full
+    # tile or 64 rows, N past the last full slab, M = 16 (no spare MFMA row), batches, every signedness and zero-point
+    # form, configuration 3's shape at M = 1, 4 and 16; one case three times in a row and a smaller M after a larger
+    # one. Aligned operands; the tiled kernel takes K and N multiples of 16, the split-k one the rest.
     d = device()
-    gemm = og.Int8Gemm(d) if config == "tiles" else og.Int8Gemm(d, og.Int8GemmOptions(Tile=32))
+    opts = {"tiles": og.Int8GemmOptions(), "tiles two launches": og.Int8GemmOptions(FewRowsOneLaunch=False),
+            "split k": og.Int8GemmOptions(Tile=32)}[config]
+    gemm = og.Int8Gemm(d, opts)
     shapes = [(1, 16, 4, 1), (1, 256, 64, 1), (4, 272, 100, 1), (16, 1024, 4096, 1), (7, 528, 1500, 1),
               (16, 4096, 64, 1), (2, 4096, 8192, 1), (3, 512, 320, 3), (1, 11008, 4096, 1), (5, 48, 12, 2),
               (16, 272, 4112, 2), (1, 32768, 512, 1), (15, 1040, 272, 1), (2, 1040, 272, 1),
               (16, 8208, 1040, 1), (7, 4112, 336, 2), (4, 8192, 16, 1), (3, 12288, 64, 1), (1, 8192, 8192, 1),
-              (13, 8256, 208, 1)]
+              (13, 8256, 208, 1), (4, 11008, 4096, 1), (16, 11008, 4096, 1), (8, 2048, 2048, 8)]
     bad_total, kernels = 0, set()
     for i, (m, n, k, batch) in enumerate(shapes):
         a_s, b_s = (i & 1) != 0, (i & 2) == 0
         za_mode, zb_mode = i % 3, (i // 3) % 3
         c = cases.Case(f"rows {m}x{n}x{k} b{batch}", cases.problem(m, n, k, batch=batch), a_s, b_s, za_mode, zb_mode)
-        tiled = config == "tiles" and k % 16 == 0 and n % 16 == 0
+        tiled = config != "split k" and k % 16 == 0 and n % 16 == 0
+        one_launch = config == "tiles" and batch * ((n + 127) // 128) >= 16
         for rep in range(3 if i == 2 or i == 8 else 1):
             say(f"{config} case {c.name} signed {a_s}/{b_s} zp {za_mode}/{zb_mode} rep {rep}")
             bad, kernel = run_int32(d, gemm, c, 100 + i)
+            d.WaitIdle()   # reports a one-launch product whose parts never arrived
+            if bad:
+                say(f"  {kernel}: {bad} wrong")
             kernels.add(kernel)
             if tiled:
-                assert kernel == "mfma-i8-rows16-tiles", kernel
+                assert kernel == ("mfma-i8-rows16-xcd" if one_launch else "mfma-i8-rows16-tiles"), kernel
             else:
                 assert kernel in ("mfma-i8-rows16-splitk", "mfma-i8-rows16-direct"), kernel
             bad_total += bad
