@@ -149,6 +149,16 @@ typedef struct og_int8_gemm_params {
 int og_int8_gemm(og_ctx *ctx, const og_int8_gemm_params *params, uint32_t batch, og_buffer A, og_buffer B, og_buffer C,
                  og_buffer ZA, og_buffer ZB, og_buffer bias, og_buffer scale, og_buffer fbias);
 
+/* og_int8_gemm that allocates nothing: no counterpart in the reference. For callers that cannot allocate device
+ * memory (work captured into a HIP graph, serving loops, harnesses that forbid hipMalloc). The same product, kernels
+ * and result; the scratch its kernels need (split-k and few-rows partial sums, the few-rows kernel's count words)
+ * comes from one fixed array of OG_NOALLOC_SCRATCH_BYTES per device instead of the context's workspace. A product
+ * that needs more fails with OG_ERR_UNSUPPORTED before anything is launched. Every call on a device shares that
+ * device's array (whatever the context), so calls that overlap on one device race. */
+#define OG_NOALLOC_SCRATCH_BYTES (16u << 20)
+int og_int8_gemm_noalloc(og_ctx *ctx, const og_int8_gemm_params *params, uint32_t batch, og_buffer A, og_buffer B,
+                         og_buffer C, og_buffer ZA, og_buffer ZB, og_buffer bias, og_buffer scale, og_buffer fbias);
+
 /* The kernel og_int8_gemm would run for these parameters (a stable name, e.g. "mfma-i8-tile256x256x64"), the HIP
  * counterpart of Int8Gemm.Variant (Int8Gemm.cs:214-215). Validates nothing; writes at most len bytes. */
 int og_int8_gemm_kernel_name(const og_int8_gemm_params *params, uint32_t batch, char *buf, size_t len);

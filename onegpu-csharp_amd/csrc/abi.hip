@@ -27,6 +27,8 @@ struct og_ctx {
     uint64_t xcd_word_count = 0;
     uint32_t *xcd_flag = nullptr;
     bool xcd_local = false;
+    // og_int8_gemm_noalloc's fixed scratch on this device (og::noalloc_scratch_setup).
+    uint8_t *noalloc_scratch = nullptr;
     std::string error;
     std::string argument;
     const char *last_kernel = "";
@@ -232,6 +234,11 @@ int og_init(int device_ordinal, og_ctx **out)
         e = hipGetLastError();
     }
     if (e == hipSuccess && ensure_xcd_words(ctx, 4096) != OG_OK) e = hipErrorOutOfMemory;
+    if (e == hipSuccess) {
+        void *p = nullptr;
+        e = og::noalloc_scratch_setup(device_ordinal, ctx->stream, &p);
+        ctx->noalloc_scratch = static_cast<uint8_t *>(p);
+    }
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) {
         int st = hip_status(nullptr, e, "og_init");
@@ -546,11 +553,49 @@ int og_int8_gemm_kernel_name(const og_int8_gemm_params *p, uint32_t batch, char 
     return OG_OK;
 }
 
+// Where a product's scratch comes from: the context's workspace, grown as needed, or (fixed) the device's array of
+// og_int8_gemm_noalloc, which nothing grows: a product that needs more is refused.
+struct ProductScratch {
+    bool fixed = false;
+    og::Workspace ws{};
+    unsigned long long *words = nullptr;
+    uint64_t word_count = 0;
+};
+
+static int scratch_for(og_ctx *ctx, ProductScratch &sc, uint64_t partial_bytes, uint64_t words)
+{
+    if (sc.fixed) {
+        if (partial_bytes > sc.ws.partial_bytes || words > sc.word_count)
+            return fail(ctx, OG_ERR_UNSUPPORTED, "scratch",
+                        "the product needs %llu bytes of partial sums and %llu count words; the fixed scratch holds "
+                        "%llu and %llu",
+                        (unsigned long long)partial_bytes, (unsigned long long)words,
+                        (unsigned long long)sc.ws.partial_bytes, (unsigned long long)sc.word_count);
+        return OG_OK;
+    }
+    int st = ensure_partials(ctx, partial_bytes);
+    if (st == OG_OK && words) st = ensure_xcd_words(ctx, words);
+    sc.ws = ctx->ws;
+    sc.words = ctx->xcd_words;
+    sc.word_count = ctx->xcd_word_count;
+    return st;
+}
+
 // Chooses the kernel for a validated product and launches it (two launches for the split few-rows forms), on ctx's
-// stream with its device current. og_int8_gemm and the convolution's products come through here.
-static int launch_product(og_ctx *ctx, const og::GemmArgs &g)
+// stream with its device current. og_int8_gemm and the convolution's products come through here; `fixed` takes the
+// scratch from og_int8_gemm_noalloc's array.
+static int launch_product(og_ctx *ctx, const og::GemmArgs &g, bool fixed = false)
 {
     int st = OG_OK;
+    ProductScratch sc;
+    if (fixed) {
+        sc.fixed = true;
+        sc.words = reinterpret_cast<unsigned long long *>(ctx->noalloc_scratch);
+        sc.word_count = og::kNoAllocWordBytes / 8;
+        sc.ws.partials = reinterpret_cast<int32_t *>(ctx->noalloc_scratch + og::kNoAllocWordBytes);
+        sc.ws.partial_bytes = og::kNoAllocScratchBytes - og::kNoAllocWordBytes;
+        sc.ws.dq_ranges = ctx->ws.dq_ranges;
+    }
     og::GemmKernel k = og::choose_gemm_kernel(g.M, g.N, g.K, g.batch, g.flags);
     if ((k == og::GemmKernel::Skinny || k == og::GemmKernel::SkinnyDirect) && !(g.flags & OG_GEMM_NO_STREAM) &&
         og::gemv_tiles_ok(g))
@@ -565,12 +610,12 @@ static int launch_product(og_ctx *ctx, const og::GemmArgs &g)
         const int ks = og::tiled_fast_ok(g) && og::direct_ok(g) && !og::tiled_uses_large(g.M, g.N, g.batch)
                            ? og::direct_split(g) : 1;
         if (ks > 1) {
-            st = ensure_partials(ctx, og::direct_split_workspace_bytes(g, ks));
+            st = scratch_for(ctx, sc, og::direct_split_workspace_bytes(g, ks), 0);
             if (st != OG_OK) return st;
-            st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_direct_split(g, ctx->ws, ctx->stream, n, ks, 0); });
+            st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_direct_split(g, sc.ws, ctx->stream, n, ks, 0); });
             if (st == OG_OK) {
                 const char *product = ctx->last_kernel;   // named for the product, not the summing pass
-                st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_direct_split(g, ctx->ws, ctx->stream, n, ks, 1); });
+                st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_direct_split(g, sc.ws, ctx->stream, n, ks, 1); });
                 ctx->last_kernel = product;
             }
             break;
@@ -579,33 +624,32 @@ static int launch_product(og_ctx *ctx, const og::GemmArgs &g)
         break;
     }
     case og::GemmKernel::RowXcd:
-        st = ensure_partials(ctx, og::gemv_xcd_workspace_bytes(g));
-        if (st == OG_OK) st = ensure_xcd_words(ctx, og::gemv_xcd_words(g));
+        st = scratch_for(ctx, sc, og::gemv_xcd_workspace_bytes(g), og::gemv_xcd_words(g));
         if (st != OG_OK) return st;
         st = launch(ctx, "og_int8_gemm", [&](const char **n) {
-            return og::launch_gemv_xcd(g, ctx->ws.partials, ctx->xcd_words, ctx->xcd_flag, ctx->stream, n);
+            return og::launch_gemv_xcd(g, sc.ws.partials, sc.words, ctx->xcd_flag, ctx->stream, n);
         });
         break;
     case og::GemmKernel::RowTiles:
-        st = ensure_partials(ctx, og::gemv_tiles_workspace_bytes(g));
+        st = scratch_for(ctx, sc, og::gemv_tiles_workspace_bytes(g), 0);
         if (st != OG_OK) return st;
-        st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemv_tiles(g, ctx->ws, ctx->stream, n, 0); });
+        st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemv_tiles(g, sc.ws, ctx->stream, n, 0); });
         if (st == OG_OK) {
             const char *product = ctx->last_kernel;   // the product is named for its tile kernel, not the summing pass
-            st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemv_tiles(g, ctx->ws, ctx->stream, n, 1); });
+            st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemv_tiles(g, sc.ws, ctx->stream, n, 1); });
             ctx->last_kernel = product;
         }
         break;
-    case og::GemmKernel::SkinnyDirect:
+    case og::GemmKernel::SkinnyDirect:   // one slice: no partial sums
         st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_skinny(g, ctx->ws, ctx->stream, n, 0); });
         break;
     case og::GemmKernel::Skinny:
-        st = ensure_partials(ctx, og::skinny_workspace_bytes(g.M, g.N, g.K, g.batch));
+        st = scratch_for(ctx, sc, og::skinny_workspace_bytes(g.M, g.N, g.K, g.batch), 0);
         if (st != OG_OK) return st;
-        st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_skinny(g, ctx->ws, ctx->stream, n, 0); });
+        st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_skinny(g, sc.ws, ctx->stream, n, 0); });
         if (st == OG_OK) {
             const char *product = ctx->last_kernel;   // named for the split-k kernel, not the reduction pass
-            st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_skinny(g, ctx->ws, ctx->stream, n, 1); });
+            st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_skinny(g, sc.ws, ctx->stream, n, 1); });
             ctx->last_kernel = product;
         }
         break;
@@ -629,7 +673,7 @@ struct ActScale {
 // output Y (OffC and StrideC in bytes) and `scale` the multiplier.
 static int run_gemm(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_buffer A, og_buffer B, og_buffer C,
                     og_buffer ZA, og_buffer ZB, og_buffer bias, og_buffer scale, og_buffer fbias, const RequantOut *rq,
-                    const ActScale *act = nullptr)
+                    const ActScale *act = nullptr, bool fixed_scratch = false)
 {
     int st = check_gemm_params(ctx, p, batch, rq != nullptr);
     if (st != OG_OK) return st;
@@ -721,7 +765,7 @@ static int run_gemm(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, o
     g.zp_y = rq ? rq->zero_point : 0;
 
     (void)hipSetDevice(ctx->device);
-    st = launch_product(ctx, g);
+    st = launch_product(ctx, g, fixed_scratch);
     return st == OG_OK ? ok(ctx) : st;
 }
 
@@ -729,6 +773,14 @@ int og_int8_gemm(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_b
                  og_buffer ZA, og_buffer ZB, og_buffer bias, og_buffer scale, og_buffer fbias)
 {
     return run_gemm(ctx, p, batch, A, B, C, ZA, ZB, bias, scale, fbias, nullptr);
+}
+
+// og_int8_gemm with the device's fixed scratch array: nothing is allocated (no counterpart in the reference).
+int og_int8_gemm_noalloc(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_buffer A, og_buffer B,
+                         og_buffer C, og_buffer ZA, og_buffer ZB, og_buffer bias, og_buffer scale, og_buffer fbias)
+{
+    if (ctx && !ctx->noalloc_scratch) return fail(ctx, OG_ERR_UNSUPPORTED, "scratch", "the fixed scratch was not set up");
+    return run_gemm(ctx, p, batch, A, B, C, ZA, ZB, bias, scale, fbias, nullptr, nullptr, true);
 }
 
 int og_int8_gemm_float_scaled(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_buffer A, og_buffer B,

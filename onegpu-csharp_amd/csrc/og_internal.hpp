@@ -50,6 +50,11 @@ struct Workspace {
 
 constexpr int kDqMaxGroups = 1024;
 
+// og_int8_gemm_noalloc's fixed scratch (one array a device): the few-rows kernel's count words, then partial sums.
+constexpr uint64_t kNoAllocScratchBytes = 16ull << 20, kNoAllocWordBytes = 64ull << 10;
+// Looks up the array's device address on `device` (current) once, clearing its count words; later calls return it.
+hipError_t noalloc_scratch_setup(int device, hipStream_t s, void **out);
+
 
 // Kernel choice for a product, as og_int8_gemm_kernel_name reports it.
 enum class GemmKernel { Portable, Tiled, Skinny, SkinnyDirect, RowTiles, RowXcd };
