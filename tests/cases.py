@@ -159,6 +159,27 @@ REQUANT_OUT = [(True, 128), (False, 0), (True, 0), (False, -5), (True, 255), (Fa
 REQUANT_TIES = [(0.5, 10, True), (0.5, -10, False), (2.5, 0, True), (1e9, 3, True), (-1e9, 3, False),
                 (float("nan"), 5, True), (float("nan"), 5, False), (float("inf"), 1, False), (0.0, 7, True)]
 
+# The three worked examples of the ONNX DynamicQuantizeLinear specification (x, expected y, expected zero point):
+# a range across zero, an all-negative input (max adjusted to 0) and an all-positive one (min adjusted to 0).
+DQ_ONNX_EXAMPLES = [
+    ([0, 2, -3, -2.5, 1.34, 0.5], [153, 255, 0, 26, 221, 179], 153),
+    ([-1.0, -2.1, -1.3, -2.5, -3.34, -4.0], [191, 121, 172, 96, 42, 0], 255),
+    ([1, 2.1, 1.3, 2.5, 3.34, 4.0, 1.5, 2.6, 3.9, 4.0, 3.0, 2.345], [64, 134, 83, 159, 213, 255, 96, 166, 249, 255, 191,
+                                                                    149], 0),
+]
+
+# Vectors derived by hand, all values exact in float32 (x, expected y, expected scale, expected zero point):
+#  - range [0, 255]: scale 1, zero point 0, and x / scale lands on .5: rounds half to even (0.5 -> 0, 1.5 -> 2,
+#    2.5 -> 2);
+#  - all negative: the range [-255, 0], zero point rne(255) = 255 clamps nothing; -0.5 rounds to -0, giving 255;
+#  - range [-127.5, 127.5]: zero point rne(127.5) = 128 (the even neighbour), 127.5 -> 128 + 128 = 256 clamps to 255,
+#    -127.5 -> -128 + 128 = 0, +-0.5 -> 0 + 128.
+DQ_HAND_VECTORS = [
+    ([0, 255, 0.5, 1.5, 2.5], [0, 255, 0, 2, 2], 1.0, 0),
+    ([-255, -1, -0.5], [0, 254, 255], 1.0, 255),
+    ([-127.5, 127.5, 0.5, -0.5], [0, 255, 128, 128], 1.0, 128),
+]
+
 
 def float_case_data(m, n, k, scale_vec, seed):
     """FloatCase inputs (Int8Tests.cs:334-373): u8 A with scalar zp, int8 B with per-column zp, scales and biases."""

@@ -113,3 +113,43 @@ def test_full_size_products(name, m, n, k, a_signed, b_signed, za_row, zb_col, t
     say(f"ROW full size | {name} | {kernel} | column sums off {bad_cols}, row sums off {bad_rows}, "
         f"sampled rows off {bad_sampled}")
     assert bad_cols == 0 and bad_rows == 0 and bad_sampled == 0
+
+
+@pytest.mark.gpu
+def test_configuration_5_at_full_size():
+    # Configuration 5 as the bench runs it: 32 batches of 512 x 4096 x 4096 with 32 distinct weight matrices, the
+    # activations one DynamicQuantizeLinear of N(0, 1) over all 67 M elements (uint8 with its scalar zero point), int8
+    # weights with no zero point. The 32 batches fill the chip with 256 x 256 tiles. Every batch is checked through
+    # its column and row sums and four oracle rows.
+    d = device()
+    batch, m, n, k = 32, 512, 4096, 4096
+    rng = np.random.default_rng(55)
+    say("full size: configuration 5 (32 x 512 x 4096 x 4096, distinct B, DQ'd activations)")
+    x = rng.standard_normal(batch * m * k, dtype=np.float32)
+    a, _, zp = oracle.dynamic_quantize(x)
+    del x
+    za = np.array([zp], np.uint8)
+    b = rng.integers(-127, 128, (batch, k, n), dtype=np.int8)
+    ba, bb, bza = d.CreateBuffer(a), d.CreateBuffer(b.ravel()), d.CreateBuffer(za)
+    bc = d.CreateBufferOf(og.ElementType.Int32, batch * m * n)
+    p = og.Int8GemmProblem(m, n, k)
+    p.Batch = batch
+    p.StrideA, p.StrideB = m * k, k * n
+    gemm = og.Int8Gemm(d)
+    run(d, lambda e: gemm.EncodeInt32(e, p, ba, bb, bc, og.Int8Operand(bza, 0)))
+    kernel = d.LastKernel
+    assert kernel == "mfma-i8-direct256x256x64", kernel
+    c = bc.Read().reshape(batch, m, n)
+    a = a.reshape(batch, m, k)
+    bad_cols = bad_rows = bad_sampled = 0
+    rows = np.array([0, 1, 171, m - 1])
+    g = oracle.Gemm(m, n, k)
+    for bi in range(batch):
+        bcols, brows = _checks(a[bi], b[bi].view(np.uint8), za, None, c[bi], False, True)
+        bad_cols += bcols
+        bad_rows += brows
+        want = oracle.int8_gemm_rows(g, a[bi].ravel(), False, b[bi].ravel().view(np.uint8), True, rows, (za, False, 0))
+        bad_sampled += int(np.count_nonzero(c[bi][rows] != want))
+    say(f"ROW full size | configuration 5 | {kernel} | zero point {zp} | column sums off {bad_cols}, row sums off "
+        f"{bad_rows}, sampled rows off {bad_sampled}")
+    assert bad_cols == 0 and bad_rows == 0 and bad_sampled == 0

@@ -3,8 +3,9 @@
 The reference ships no golden vectors for this path (its tests compute their expectations on the fly in C#), so the
 oracle is pinned by: the reference's closed forms, brute force / library routines that compute the same mathematics
 independently (numpy int64 matmul, IEEE float32 arithmetic, numpy's float16 cast, np.rint), the signed-domain identity
-agreeing with the definition form, and the reference kernel's own integer division agreeing with IEEE division.
-tests/test_oracle_mutants.py shows each pin catches a planted mistake.
+agreeing with the definition form, the reference kernel's own integer division agreeing with IEEE division, and the
+worked examples of the ONNX specifications (DynamicQuantizeLinear, Gather, ConvInteger). tests/test_oracle_mutants.py
+runs the same pins against deliberately broken implementations and shows that each one fails them.
 """
 import numpy as np
 import pytest
@@ -181,6 +182,24 @@ def test_dynamic_quantize_special_inputs():
     y, s, z = oracle.dynamic_quantize(np.array([0, 255, 17], np.float32))
     assert (s, z, y.tolist()) == (1.0, 0, [0, 255, 17])
     assert oracle.dynamic_quantize(np.zeros(5, np.float32))[1:] == (1.0, 0)
+
+
+def test_dynamic_quantize_onnx_examples():
+    # The ONNX DynamicQuantizeLinear specification's worked examples: published outputs, so they pin the formula
+    # (range adjusted to include 0, scale = range / 255, zero point = rne(-lo / scale) clamped) and its float32
+    # rounding (-2.5 / scale is -127.49999... in float32, hence 26, not 25).
+    for x, want_y, want_z in cases.DQ_ONNX_EXAMPLES:
+        y, s, z = oracle.dynamic_quantize(np.array(x, np.float32))
+        assert y.tolist() == want_y and z == want_z, x
+        lo, hi = min(0.0, min(x)), max(0.0, max(x))
+        assert np.float32(s) == np.float32(np.float32(hi) - np.float32(lo)) / np.float32(255)
+
+
+def test_dynamic_quantize_hand_vectors():
+    # Ties, a clamped output and a zero point that is itself a tie (cases.DQ_HAND_VECTORS, derived by hand).
+    for x, want_y, want_s, want_z in cases.DQ_HAND_VECTORS:
+        y, s, z = oracle.dynamic_quantize(np.array(x, np.float32))
+        assert (y.tolist(), float(s), z) == (want_y, want_s, want_z), x
 
 
 def test_div_exact_equals_ieee_division():
