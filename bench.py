@@ -75,14 +75,16 @@ def synth(d, etype, n, seed, tensor, lo, hi, kind):
     return b
 
 
-def sym_weights(d, k, n, seed, tensor):
-    """N(0, 0.02) float weights [K, N] -> per-column scale max|w| / 127 -> QuantizeLinear to int8 (axis 1)."""
+def sym_weights(d, k, n, seed, tensor, q=None, q_off=0, scale=None, scale_off=0):
+    """N(0, 0.02) float weights [K, N] -> per-column scale max|w| / 127 -> QuantizeLinear to int8 (axis 1), into new
+    buffers or at element offsets of the given ones (a batch of weight matrices and their scale vectors)."""
     w = synth(d, og.ElementType.Float32, k * n, seed, tensor, 0.0, 0.02, 2)
-    scale = d.CreateBufferOf(og.ElementType.Float32, n)
-    _ok(_abi().og_util_col_absmax_scale(d.Context, _b(w), k, n, 127.0, _b(scale)), d)
-    q = d.CreateBufferOf(og.ElementType.Int8, k * n)
+    scale = d.CreateBufferOf(og.ElementType.Float32, n) if scale is None else scale
+    q = d.CreateBufferOf(og.ElementType.Int8, k * n) if q is None else q
+    _ok(_abi().og_util_col_absmax_scale(d.Context, _b(w), k, n, 127.0,
+                                        _Buf(scale.DevicePointer + 4 * scale_off, 4 * n)), d)
     e = d.BeginCommands()
-    og.DequantizeKernels(d).EncodeQuantize(e, w, 0, [k, n], 1, True, scale, 0, None, 0, q, 0)
+    og.DequantizeKernels(d).EncodeQuantize(e, w, 0, [k, n], 1, True, scale, scale_off, None, 0, q, q_off)
     d.Submit(e)
     d.WaitIdle()
     w.Dispose()
@@ -127,6 +129,15 @@ def kernel_stats(times, name_prefix=None):
     return statistics.mean(ms), statistics.median(ms), (times[0][1] if times else "")
 
 
+def per_kernel_us(times):
+    """{kernel: {"mean_us", "median_us", "n"}} over the individually timed dispatches (one HIP event pair around each,
+    so a short kernel's figure includes the dispatch's own start-up of about 1-2 us)."""
+    per = {}
+    for t, k in times:
+        per.setdefault(k, []).append(t * 1e3)
+    return {k: {"mean_us": statistics.mean(v), "median_us": statistics.median(v), "n": len(v)} for k, v in per.items()}
+
+
 # ------------------------------------------------------------------ configurations
 
 def c4_square(d, steps, warmup, check=True, constant=False, trans_b=False, plain=False):
@@ -148,7 +159,8 @@ def c4_square(d, steps, warmup, check=True, constant=False, trans_b=False, plain
     wall, region, times = timed(d, lambda e, i: gemm.EncodeInt32(e, p, a, b, c, zpa), steps, warmup)
     pair_ms, pair_med_ms, kname = kernel_stats(times)
     res = {"ops": 2.0 * M * N * K, "wall_s": wall, "kernel_mean_ms": region / steps * 1e3,
-           "event_pair_mean_ms": pair_ms, "kernel": kname, "bytes": M * K + K * N + M + 4 * M * N}
+           "event_pair_mean_ms": pair_ms, "event_pair_median_ms": pair_med_ms, "kernel": kname,
+           "bytes": M * K + K * N + M + 4 * M * N}
     if check:
         import oracle
         rows = np.array([0, 1, 777, 2048, 4095])
@@ -189,7 +201,8 @@ def c3_gemv(d, m, steps, warmup, copies=9, check=True):
     step_ms = [sum(times[i * n_disp + j][0] for j in range(n_disp)) for i in range(steps)]
     bytes_ = K * N + m * K + 4 * m * N + 4 * N + 4 + 1
     res = {"m": m, "ops": 2.0 * m * N * K, "bytes": bytes_, "wall_s": wall, "step_mean_ms": region / steps * 1e3,
-           "event_pair_step_mean_ms": statistics.mean(step_ms), "kernels": [k for _, k in times[:n_disp]],
+           "event_pair_step_mean_ms": statistics.mean(step_ms), "event_pair_step_median_ms": statistics.median(step_ms),
+           "kernels": [k for _, k in times[:n_disp]],
            "dispatch_mean_ms": [statistics.mean(times[i * n_disp + j][0] for i in range(steps)) for j in range(n_disp)]}
     if check:
         import oracle
@@ -229,12 +242,16 @@ def c2_bert_ffn(d, steps, warmup, check=True, fused_scale=True):
             gemm.EncodeFloat(e, p, ya, q, c, og.Int8Operand(sc, 0, True), og.Int8Operand(z, 0))
 
     wall, region, times = timed(d, step, steps, warmup)
-    per = {}
-    for t, k in times:
-        per.setdefault(k, []).append(t)
-    res = {"ops": 2.0 * M * N * K, "wall_s": wall, "chain_mean_ms": region / steps * 1e3,
-           "dispatch_mean_ms": {k: statistics.mean(v) for k, v in per.items()},
-           "bytes_gemm": M * K + K * N + 4 * M * N + 4 * N, "bytes_dq": 4 * M * K + M * K + 5}
+    per = per_kernel_us(times)
+    # Bytes each dispatch moves at least once: the range pass reads x; the quantize pass reads x and writes y (the
+    # per-workgroup ranges are a few KB); the product reads A, B and the scales and writes the float32 output.
+    kbytes = {"dq-minmax": 4 * M * K, "dq-quantize": 4 * M * K + M * K + 5, "scale-product": 8 * N + 4}
+    for k in per:
+        per[k]["bytes"] = kbytes.get(k, M * K + K * N + 4 * M * N + 4 * N + 5)
+        per[k]["gbs_median"] = per[k]["bytes"] / (per[k]["median_us"] * 1e-6) / 1e9
+        per[k]["hbm_frac_median"] = per[k]["gbs_median"] / PEAK_HBM_GBS
+    res = {"ops": 2.0 * M * N * K, "wall_s": wall, "chain_mean_ms": region / steps * 1e3, "per_kernel": per,
+           "chain_bytes": 4 * M * K + K * N + 4 * N + 4 * M * N}
     if check:
         import oracle
         Y, Z, Q, WS = ya.Read(), int(z.Read()[0]), q.Read(), wscale.Read()
@@ -249,70 +266,225 @@ def c2_bert_ffn(d, steps, warmup, check=True, fused_scale=True):
     return res
 
 
-def c5_batched(d, steps, warmup, check=True):
-    """Configuration 5: 32 x (A u8 [512 x 4096] from one DQ of N(0,1)) x (32 distinct B int8 [4096 x 4096]), int32."""
+class C5:
+    """Configuration 5's operands, resident on the device: x [32 x 512 x 4096] float32 N(0,1); 32 distinct int8 weight
+    matrices [4096 x 4096] (each N(0, 0.02) quantized symmetric per column) with their 32 x 4096 column scales."""
     Bt, M, K, N = 32, 512, 4096, 4096
-    x = synth(d, og.ElementType.Float32, Bt * M * K, 5, 40, 0.0, 1.0, 2)
-    ya = d.CreateBufferOf(og.ElementType.UInt8, Bt * M * K)
-    s = d.CreateBufferOf(og.ElementType.Float32, 1)
-    z = d.CreateBufferOf(og.ElementType.UInt8, 4)
-    e = d.BeginCommands()
-    og.DynamicQuantizeKernels(d).Encode(e, x, 0, Bt * M * K, ya, 0, s, 0, z, 0)
-    d.Submit(e)
-    x.Dispose()
-    b = synth(d, og.ElementType.Int8, Bt * K * N, 5, 41, -127, 127, 0)
-    c = d.CreateBufferOf(og.ElementType.Int32, Bt * M * N)
-    gemm = og.Int8Gemm(d)
-    p = og.Int8GemmProblem(M, N, K)
-    p.Batch, p.StrideA, p.StrideB = Bt, M * K, K * N
-    zpa = og.Int8Operand(z, 0)
-    wall, region, times = timed(d, lambda e, i: gemm.EncodeInt32(e, p, ya, b, c, zpa), steps, warmup)
-    kname = kernel_stats(times)[2]
-    res = {"ops": 2.0 * Bt * M * N * K, "wall_s": wall, "kernel_mean_ms": region / steps * 1e3, "kernel": kname,
-           "bytes": Bt * (M * K + K * N + 4 * M * N)}
-    if check:
+
+    def __init__(self, d):
+        Bt, M, K, N = self.Bt, self.M, self.K, self.N
+        self.x = synth(d, og.ElementType.Float32, Bt * M * K, 5, 40, 0.0, 1.0, 2)
+        self.b = d.CreateBufferOf(og.ElementType.Int8, Bt * K * N)
+        self.wscale = d.CreateBufferOf(og.ElementType.Float32, Bt * N)
+        for i in range(Bt):
+            sym_weights(d, K, N, 5, 41 + i, self.b, i * K * N, self.wscale, i * N)
+        self.ya = d.CreateBufferOf(og.ElementType.UInt8, Bt * M * K)
+        self.s = d.CreateBufferOf(og.ElementType.Float32, 1)
+        self.z = d.CreateBufferOf(og.ElementType.UInt8, 4)
+        self.c = d.CreateBufferOf(og.ElementType.Int32, Bt * M * N)
+        self.sc = d.CreateBufferOf(og.ElementType.Float32, Bt * N)
+        self.y = d.CreateBufferOf(og.ElementType.Float32, Bt * M * N)
+        self.p = og.Int8GemmProblem(M, N, K)
+        self.p.Batch, self.p.StrideA, self.p.StrideB = Bt, M * K, K * N
+        self.dq, self.gemm, self.deq = og.DynamicQuantizeKernels(d), og.Int8Gemm(d), og.DequantizeKernels(d)
+        self.ops = 2.0 * Bt * M * N * K
+        self.product_bytes = Bt * (M * K + K * N + 4 * M * N)
+
+    def quantize(self, e):
+        self.dq.Encode(e, self.x, 0, self.Bt * self.M * self.K, self.ya, 0, self.s, 0, self.z, 0)
+
+    def product(self, e):
+        self.gemm.EncodeInt32(e, self.p, self.ya, self.b, self.c, og.Int8Operand(self.z, 0))
+
+    def rescale(self, e):
+        # y[b, m, n] = DequantizeLinear(c[b, m, n], fl(actScale * wScale[b, n])): the 32 x 4096 scale vector on the
+        # device, then one per-column DequantizeLinear per batch (each batch has its own column scales).
+        e.RecordScaleProduct(self.s, self.wscale, self.Bt * self.N, self.sc)
+        for i in range(self.Bt):
+            self.deq.Encode(e, self.c, i * self.M * self.N, [self.M, self.N], 1, True, self.sc, i * self.N, None, 0,
+                            self.y, i * self.M * self.N)
+
+    def check(self, with_y):
         import oracle
-        Y, Z, Bh = ya.Read(), int(z.Read()[0]), b.Read().view(np.uint8)
+        Bt, M, K, N = self.Bt, self.M, self.K, self.N
+        X = self.x.Read()
+        wy, ws_, wz = oracle.dynamic_quantize(X)
+        del X
+        Y, Z = self.ya.Read(), int(self.z.Read()[0])
+        ok = np.array_equal(Y, wy) and Z == wz and np.float32(self.s.Read()[0]) == np.float32(ws_)
+        del wy
+        Bh = self.b.Read().view(np.uint8)
         pr = oracle.Gemm(M, N, K, Batch=Bt, StrideA=M * K, StrideB=K * N)
         rows = np.array([0, 511, 7 * M + 100, 31 * M + 511])
         want = oracle.int8_gemm_rows(pr, Y, False, Bh, True, rows, (np.array([Z], np.uint8), False, 0))
-        got = c.Read().reshape(Bt * M, N)[rows]
-        res["check"] = "bit-exact on sampled rows" if np.array_equal(got, want) else "MISMATCH"
+        C = self.c.Read().reshape(Bt * M, N)
+        ok = ok and np.array_equal(C[rows], want)
+        if with_y:
+            sc = (np.float32(ws_) * self.wscale.Read().astype(np.float32)).astype(np.float32).reshape(Bt, 1, N)
+            wanty = (C.reshape(Bt, M, N).astype(np.float32) * sc).astype(np.float32)
+            ok = ok and np.array_equal(self.y.Read().view(np.uint32), wanty.reshape(-1).view(np.uint32))
+        return ok
+
+
+def c5_batched(d, steps, warmup, check=True, c5=None):
+    """Configuration 5's product alone: 32 x (u8 A [512 x 4096], one DQ of N(0,1)) x (32 distinct int8 B [4096 x 4096]),
+    int32 out. The DQ runs once before the timed region."""
+    c5 = c5 or C5(d)
+    e = d.BeginCommands()
+    c5.quantize(e)
+    d.Submit(e)
+    d.WaitIdle()
+    wall, region, times = timed(d, lambda e, i: c5.product(e), steps, warmup)
+    _, med, kname = kernel_stats(times)
+    res = {"ops": c5.ops, "bytes": c5.product_bytes, "wall_s": wall, "kernel_mean_ms": region / steps * 1e3,
+           "event_pair_median_ms": med, "kernel": kname}
+    if check:
+        res["check"] = "bit-exact on sampled rows" if c5.check(False) else "MISMATCH"
+    return res, c5
+
+
+def c5_chain(d, steps, warmup, check=True, c5=None):
+    """Configuration 5 as BASELINE states it, one step = DynamicQuantizeLinear of the 67 M activations (two passes) ->
+    the batched int32 product -> DequantizeLinear to float32 with each batch's column scales (a scale-product dispatch,
+    then one per batch). Checked whole: the DQ and the rescale against the oracle on every element, the sums on
+    sampled rows."""
+    c5 = c5 or C5(d)
+
+    def step(e, i):
+        c5.quantize(e)
+        c5.product(e)
+        c5.rescale(e)
+
+    wall, region, times = timed(d, step, steps, warmup)
+    per = per_kernel_us(times)
+    n_act, n_out = c5.Bt * c5.M * c5.K, c5.Bt * c5.M * c5.N
+    kbytes = {"dq-minmax": 4 * n_act, "dq-quantize": 5 * n_act + 5, "scale-product": 8 * c5.Bt * c5.N + 4}
+    for k in per:
+        per[k]["bytes"] = kbytes.get(k, c5.product_bytes if k.startswith("mfma") else 8 * n_out // c5.Bt)
+        per[k]["gbs_median"] = per[k]["bytes"] / (per[k]["median_us"] * 1e-6) / 1e9
+        per[k]["hbm_frac_median"] = per[k]["gbs_median"] / PEAK_HBM_GBS
+    # The chain's operands once: x read, B and the weight scales read, y written.
+    chain_bytes = 4 * n_act + c5.Bt * c5.K * c5.N + 4 * c5.Bt * c5.N + 4 * n_out
+    res = {"ops": c5.ops, "chain_bytes": chain_bytes, "wall_s": wall, "chain_mean_ms": region / steps * 1e3,
+           "dispatches_per_step": len(times) // steps, "per_kernel": per}
+    if check:
+        res["check"] = "bit-exact (DQ and rescale whole, sums on sampled rows)" if c5.check(True) else "MISMATCH"
+    return res, c5
+
+
+def elementwise_c5(d, steps, warmup, which, check=True):
+    """The element-wise passes alone at configuration 5's sizes, each one launch over 67,108,864 elements:
+    'dequant' DequantizeLinear int32 [16384 x 4096] -> float32 with a per-column scale (axis 1); 'quant' QuantizeLinear
+    float32 -> uint8 with one scale and zero point; 'dq' DynamicQuantizeLinear of N(0,1) float32 (its two passes).
+    Bytes are every operand read or written once."""
+    R, N = 32 * 512, 4096
+    n = R * N
+    if which == "dequant":
+        x = synth(d, og.ElementType.Int32, n, 8, 70, -2**31, 2**31 - 1, 1)
+        sc = d.CreateBuffer(np.random.default_rng(71).uniform(1e-6, 1e-4, N).astype(np.float32))
+        out = d.CreateBufferOf(og.ElementType.Float32, n)
+        k = og.DequantizeKernels(d)
+        rec = lambda e, i: k.Encode(e, x, 0, [R, N], 1, True, sc, 0, None, 0, out, 0)  # noqa: E731
+        bytes_ = 8 * n + 4 * N
+    elif which == "quant":
+        x = synth(d, og.ElementType.Float32, n, 8, 72, 0.0, 1.0, 2)
+        sc = d.CreateBuffer(np.array([4.7 / 255], np.float32))
+        zp = d.CreateBuffer(np.array([117, 0, 0, 0], np.uint8))
+        out = d.CreateBufferOf(og.ElementType.UInt8, n)
+        k = og.DequantizeKernels(d)
+        rec = lambda e, i: k.EncodeQuantize(e, x, 0, [n], 0, False, sc, 0, zp, 0, out, 0)  # noqa: E731
+        bytes_ = 5 * n + 5
+    else:
+        x = synth(d, og.ElementType.Float32, n, 8, 73, 0.0, 1.0, 2)
+        out = d.CreateBufferOf(og.ElementType.UInt8, n)
+        s, z = d.CreateBufferOf(og.ElementType.Float32, 1), d.CreateBufferOf(og.ElementType.UInt8, 4)
+        k = og.DynamicQuantizeKernels(d)
+        rec = lambda e, i: k.Encode(e, x, 0, n, out, 0, s, 0, z, 0)  # noqa: E731
+        bytes_ = 9 * n + 5
+    wall, region, times = timed(d, rec, steps, warmup)
+    per = per_kernel_us(times)
+    step_us = region / steps * 1e6
+    res = {"elements": n, "bytes": bytes_, "wall_s": wall, "step_mean_us": step_us, "per_kernel": per,
+           "gbs": bytes_ / (step_us * 1e-6) / 1e9}
+    res["hbm_frac"] = res["gbs"] / PEAK_HBM_GBS
+    if which == "dq":
+        per["dq-minmax"]["bytes"], per["dq-quantize"]["bytes"] = 4 * n, 5 * n + 5
+        for kk in per:
+            per[kk]["gbs_median"] = per[kk]["bytes"] / (per[kk]["median_us"] * 1e-6) / 1e9
+            per[kk]["hbm_frac_median"] = per[kk]["gbs_median"] / PEAK_HBM_GBS
+    if check:
+        import oracle
+        X, got = x.Read(), out.Read()
+        if which == "dequant":
+            ok = np.array_equal(got.view(np.uint32), oracle.dequantize(X, sc.Read(), True, N, 1).view(np.uint32))
+        elif which == "quant":
+            ok = np.array_equal(got, oracle.quantize(X, np.array([4.7 / 255], np.float32), False,
+                                                     zero=np.array([117], np.uint8)))
+        else:
+            wy, ws_, wz = oracle.dynamic_quantize(X)
+            ok = np.array_equal(got, wy) and int(z.Read()[0]) == wz and np.float32(s.Read()[0]) == np.float32(ws_)
+        res["check"] = "bit-exact (every element)" if ok else "MISMATCH"
+    for b in (x, out):
+        b.Dispose()
     return res
 
 
-def cpu_baseline_c4(host_operands, budget_s=10.0):
-    """The oracle (reference-semantics CPU restatement) on rows of the 4096^3 product, repeated over the rows until
-    about budget_s of CPU work (a whole pass of 4096 rows takes well under a second on a many-core host)."""
-    import oracle
-    A, B, Z = host_operands
-    M = N = K = 4096
-    threads = max(1, min(16, os.cpu_count() or 1))
-    rows_done, t_total = 0, 0.0
-    chunk = max(threads, 16)
-    while t_total < budget_s:
-        start = rows_done % M
-        rows = np.arange(start, min(M, start + chunk))
-        t0 = time.perf_counter()
-        oracle.int8_gemm_rows(oracle.Gemm(M, N, K), A, False, B.view(np.uint8), True, rows, (Z, True, 0), threads=threads)
-        dt = time.perf_counter() - t0
-        t_total += dt
-        rows_done += len(rows)
-        if dt < budget_s / 16 and chunk < M:
-            chunk *= 2
-    ops = 2.0 * rows_done * N * K
-    cpu = "unknown"
+def host_cpu():
+    """(threads to use, description): the threads this process may use (its CPU affinity, capped by OMP_NUM_THREADS
+    where the host sets it: a GPU box's share of cores for one GPU), beside nproc and the CPU model."""
+    nproc = os.cpu_count() or 1
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = nproc
+    threads = affinity
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        threads = min(threads, int(omp))
+    model = "unknown"
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
                 if line.startswith("model name"):
-                    cpu = line.split(":", 1)[1].strip()
+                    model = line.split(":", 1)[1].strip()
                     break
     except OSError:
         pass
-    return {"value": ops / t_total / 1e12, "unit": "TOPS", "cores": threads, "kind": "port",
-            "sample": f"{rows_done} rows ({rows_done / M:.1f} passes over the 4096 rows) of the 4096^3 product (u8 A "
-                      f"with per-row zero point x int8 B), {t_total:.1f} s, oracle/oracle.c ora_int8_gemm_rows on {threads} threads of {cpu}"}
+    return threads, {"nproc": nproc, "affinity": affinity, "omp_num_threads": omp or None, "cpu_model": model}
+
+
+def cpu_baseline_c4(host_operands, budget_s=12.0, runs=5):
+    """The oracle (the reference's CPU definition restated in C, std::thread over rows) on the 4096^3 product's
+    operands: `runs` timed runs, each over a fresh block of rows sized to about budget_s / runs seconds, reported as
+    the median run's throughput."""
+    import oracle
+    A, B, Z = host_operands
+    M = N = K = 4096
+    threads, host = host_cpu()
+    p = oracle.Gemm(M, N, K)
+
+    def run_rows(start, count):
+        rows = np.arange(start, start + count) % M
+        t0 = time.perf_counter()
+        oracle.int8_gemm_rows(p, A, False, B.view(np.uint8), True, rows, (Z, True, 0), threads=threads)
+        return time.perf_counter() - t0
+
+    chunk = threads
+    while True:   # size one run's block of rows
+        dt = run_rows(0, chunk)
+        if dt >= budget_s / runs / 2 or chunk >= M:
+            break
+        chunk = min(M, chunk * 2)
+    chunk = max(threads, min(M, int(chunk * (budget_s / runs) / max(dt, 1e-3))))
+    times, start = [], 0
+    for _ in range(runs):
+        times.append(run_rows(start, chunk))
+        start += chunk
+    rates = sorted(2.0 * chunk * N * K / t / 1e12 for t in times)
+    return {"value": rates[len(rates) // 2], "unit": "TOPS", "cores": threads, "kind": "port",
+            "sample": f"median of {runs} runs, each {chunk} rows of the 4096^3 product (u8 A with per-row zero point x "
+                      f"int8 B), {sum(times):.1f} s in all; oracle/oracle.c ora_int8_gemm_rows on {threads} threads",
+            "runs_tops": rates, **host}
 
 
 def traffic_of(kernel, workload):
@@ -500,7 +672,11 @@ def only(d, name, steps, warmup):
     elif name == "c2":
         r = c2_bert_ffn(d, steps, warmup, check=False)
     elif name == "c5":
-        r = c5_batched(d, steps, warmup, check=False)
+        r = c5_batched(d, steps, warmup, check=False)[0]
+    elif name == "c5chain":
+        r = c5_chain(d, steps, warmup, check=False)[0]
+    elif name in ("dequant", "quant", "dq"):
+        r = elementwise_c5(d, steps, warmup, name, check=False)
     elif name in ("c2q", "c2q2"):
         r = qlinear_c2(d, steps, warmup, fused=name == "c2q", check=False)
     elif name in ("resnet50", "whisper", "depthwise"):
@@ -526,12 +702,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline configuration only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["c4", "c4const", "c4nt", "c4plain", "c4plainnt", "gemv1", "gemv4", "gemv16", "c2", "c2q", "c2q2", "c5", "gather4096", "gather65536", "resnet50", "whisper", "depthwise", "copy", "vendor"],
+    ap.add_argument("--only", choices=["c4", "c4const", "c4nt", "c4plain", "c4plainnt", "gemv1", "gemv4", "gemv16", "c2", "c2q", "c2q2", "c5", "c5chain", "dequant", "quant", "dq", "gather4096", "gather65536", "resnet50", "whisper", "depthwise", "copy", "vendor"],
                     help="run one workload alone and print its summary (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported (see DESIGN.md for "
-                                   "how the path would shard)"}))
+        print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported"}))
         sys.exit(2)
     if args.only == "vendor":
         # torch's bundled HIP runtime must own the device in this process: no context of this library is opened.
@@ -549,7 +724,10 @@ def main():
     kern_tops = c4["ops"] / (c4["kernel_mean_ms"] * 1e-3) / 1e12
     configs = {"c4_square_4096": {"tops_wall": tops, "tops_kernel": kern_tops, "kernel": c4["kernel"],
                                   "kernel_mean_us": c4["kernel_mean_ms"] * 1e3,
-                                  "event_pair_mean_us": c4["event_pair_mean_ms"] * 1e3, "check": c4["check"]}}
+                                  "event_pair_mean_us": c4["event_pair_mean_ms"] * 1e3,
+                                  "event_pair_median_us": c4["event_pair_median_ms"] * 1e3,
+                                  "tops_event_pair_median": c4["ops"] / (c4["event_pair_median_ms"] * 1e-3) / 1e12,
+                                  "check": c4["check"]}}
     log(json.dumps(configs["c4_square_4096"]))
 
     gemv = {}
@@ -560,7 +738,8 @@ def main():
         gemv[m] = {"gbs": gbs, "frac": gbs / PEAK_HBM_GBS, "step_mean_us": r["step_mean_ms"] * 1e3,
                    "tops": r["ops"] / (r["step_mean_ms"] * 1e-3) / 1e12, "kernels": r["kernels"],
                    "dispatch_mean_us": [t * 1e3 for t in r["dispatch_mean_ms"]],
-                   "event_pair_step_mean_us": r["event_pair_step_mean_ms"] * 1e3, "bytes": r["bytes"],
+                   "event_pair_step_mean_us": r["event_pair_step_mean_ms"] * 1e3,
+                   "event_pair_step_median_us": r["event_pair_step_median_ms"] * 1e3, "bytes": r["bytes"],
                    "check": r["check"]}
         configs[f"c3_gemv_m{m}"] = gemv[m]
         log(json.dumps(gemv[m]))
@@ -569,14 +748,14 @@ def main():
         r = c2_bert_ffn(d, args.steps, args.warmup)
         configs["c2_bert_ffn"] = {"chain_wall_us": r["wall_s"] / args.steps * 1e6,
                                   "chain_mean_us": r["chain_mean_ms"] * 1e3,
-                                  "dispatch_mean_us": {k: v * 1e3 for k, v in r["dispatch_mean_ms"].items()},
-                                  "check": r["check"]}
+                                  "chain_gbs": r["chain_bytes"] / (r["chain_mean_ms"] * 1e-3) / 1e9,
+                                  "tops": r["ops"] / (r["chain_mean_ms"] * 1e-3) / 1e12,
+                                  "per_kernel": r["per_kernel"], "check": r["check"]}
         log(json.dumps(configs["c2_bert_ffn"]))
         log("config 2: BERT FFN chain with the scale product as its own dispatch (the reference's chain)")
         r = c2_bert_ffn(d, args.steps, args.warmup, fused_scale=False)
         configs["c2_bert_ffn_separate_scale"] = {"chain_mean_us": r["chain_mean_ms"] * 1e3,
-                                                 "dispatch_mean_us": {k: v * 1e3 for k, v in r["dispatch_mean_ms"].items()},
-                                                 "check": r["check"]}
+                                                 "per_kernel": r["per_kernel"], "check": r["check"]}
         log(json.dumps(configs["c2_bert_ffn_separate_scale"]))
         for fused, key in ((True, "qlinear_c2_one_launch"), (False, "qlinear_c2_two_passes")):
             log(f"QLinearMatMul on configuration 2's product, {'one launch' if fused else 'two passes'}")
@@ -603,11 +782,31 @@ def main():
                                             "dispatches_per_step": r["dispatches_per_step"],
                                             "kernel_us_per_step": {k: v * 1e3 for k, v in r["kernel_ms_per_step"].items()}}
             log(json.dumps(configs[f"conv_{which}_b1"]))
-        log("config 5: batched 32 x 512 x 4096 x 4096")
-        r = c5_batched(d, max(3, args.steps // 5), 2)
-        configs["c5_batched"] = {"tops_kernel": r["ops"] / (r["kernel_mean_ms"] * 1e-3) / 1e12,
-                                 "kernel_mean_us": r["kernel_mean_ms"] * 1e3, "kernel": r["kernel"], "check": r["check"]}
+        log("config 5: batched 32 x 512 x 4096 x 4096, the product alone")
+        c5_steps = max(3, args.steps // 5)
+        r, c5 = c5_batched(d, c5_steps, 2)
+        tops5 = r["ops"] / (r["kernel_mean_ms"] * 1e-3) / 1e12
+        gbs5 = r["bytes"] / (r["kernel_mean_ms"] * 1e-3) / 1e9
+        configs["c5_batched"] = {"tops_kernel": tops5, "mfma_frac": tops5 / PEAK_INT8_TOPS, "gbs": gbs5,
+                                 "hbm_frac": gbs5 / PEAK_HBM_GBS, "kernel_mean_us": r["kernel_mean_ms"] * 1e3,
+                                 "event_pair_median_us": r["event_pair_median_ms"] * 1e3, "kernel": r["kernel"],
+                                 "bytes": r["bytes"], "check": r["check"]}
         log(json.dumps(configs["c5_batched"]))
+        log("config 5 as a chain: DynamicQuantizeLinear -> batched product -> DequantizeLinear per batch")
+        r, _ = c5_chain(d, c5_steps, 2, c5=c5)
+        del c5
+        us = r["chain_mean_ms"] * 1e3
+        configs["c5_chain"] = {"chain_mean_us": us, "tops": r["ops"] / (us * 1e-6) / 1e12,
+                               "mfma_frac": r["ops"] / (us * 1e-6) / 1e12 / PEAK_INT8_TOPS,
+                               "chain_gbs": r["chain_bytes"] / (us * 1e-6) / 1e9,
+                               "hbm_frac": r["chain_bytes"] / (us * 1e-6) / 1e9 / PEAK_HBM_GBS,
+                               "chain_bytes": r["chain_bytes"], "dispatches_per_step": r["dispatches_per_step"],
+                               "per_kernel": r["per_kernel"], "check": r["check"]}
+        log(json.dumps(configs["c5_chain"]))
+        for which in ("dequant", "quant", "dq"):
+            log(f"element-wise at configuration 5's size: {which}")
+            configs[f"{which}_c5_size"] = elementwise_c5(d, args.steps // 2 or 1, 2, which)
+            log(json.dumps(configs[f"{which}_c5_size"]))
 
     roof = {"bound": "mfma", "achieved": kern_tops, "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
             "frac": kern_tops / PEAK_INT8_TOPS, "traffic": traffic_of(c4["kernel"], "c4"),

@@ -104,9 +104,11 @@ __device__ __forceinline__ uint32_t dq_one(float x, float scale, float zp)
 }
 
 // Pass 2: every workgroup combines pass 1's ranges (the kernel boundary orders them; min and max are order-free, so
-// every workgroup derives the same scale and zero point) and quantizes its grid-stride share of x, 16 elements a
-// thread with 16-byte loads and one 16-byte store when x and y are 16-byte aligned. Workgroup 0 writes the scale and
-// the zero point (one byte, its neighbours untouched).
+// every workgroup derives the same scale and zero point) and quantizes blocks of 4096 elements, grid-stride. In a
+// whole block with x and y 16-byte aligned, lane l of wave w takes elements 1024 w + 256 c + 4 l .. + 3 (c = 0..3)
+// with one 16-byte load and one 4-byte store each, so every instruction covers one contiguous span across the wave;
+// otherwise lane t takes elements t, t + 256, ... Workgroup 0 writes the scale and the zero point (one byte, its
+// neighbours untouched).
 __global__ __launch_bounds__(DQ_THREADS) void k_dq_quantize(const float *x, uint8_t *y, uint32_t count,
                                                             const float *ranges, uint32_t groups, float *scale_out,
                                                             uint8_t *zero_out)
@@ -133,20 +135,19 @@ __global__ __launch_bounds__(DQ_THREADS) void k_dq_quantize(const float *x, uint
     __syncthreads();
     const float scale = sparam[0], zp = sparam[1];
     const bool vec = (((uintptr_t)x | (uintptr_t)y) & 15) == 0;
-    const uint64_t stride = (uint64_t)gridDim.x * DQ_THREADS * 16;
-    for (uint64_t i0 = ((uint64_t)blockIdx.x * DQ_THREADS + threadIdx.x) * 16; i0 < count; i0 += stride) {
-        if (vec && i0 + 16 <= count) {
-            const f4 *x4 = reinterpret_cast<const f4 *>(x + i0);
-            uint32_t w[4];
+    const uint32_t lane_off = (threadIdx.x >> 6) * 1024u + (threadIdx.x & 63u) * 4u;
+    for (uint64_t blk = (uint64_t)blockIdx.x * 4096; blk < count; blk += (uint64_t)gridDim.x * 4096) {
+        if (vec && blk + 4096 <= count) {
+            f4 v[4];
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                f4 v = __builtin_nontemporal_load(&x4[q]);
-                w[q] = dq_one(v.x, scale, zp) | (dq_one(v.y, scale, zp) << 8) | (dq_one(v.z, scale, zp) << 16) |
-                       (dq_one(v.w, scale, zp) << 24);
-            }
-            *reinterpret_cast<uint4 *>(y + i0) = make_uint4(w[0], w[1], w[2], w[3]);
+            for (int c = 0; c < 4; c++) v[c] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(x + blk + lane_off + 256 * c));
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                *reinterpret_cast<uint32_t *>(y + blk + lane_off + 256 * c) =
+                    dq_one(v[c].x, scale, zp) | (dq_one(v[c].y, scale, zp) << 8) | (dq_one(v[c].z, scale, zp) << 16) |
+                    (dq_one(v[c].w, scale, zp) << 24);
         } else {
-            for (uint64_t i = i0; i < i0 + 16 && i < count; i++) y[i] = (uint8_t)dq_one(x[i], scale, zp);
+            for (uint64_t i = blk + threadIdx.x; i < blk + 4096 && i < count; i += DQ_THREADS) y[i] = (uint8_t)dq_one(x[i], scale, zp);
         }
     }
 }
@@ -166,10 +167,9 @@ hipError_t launch_dynamic_quantize(const DqArgs &d, const Workspace &ws, hipStre
         hipLaunchKernelGGL(k_dq_minmax, dim3(groups), dim3(DQ_THREADS), 0, s, d.x, d.count, ws.dq_ranges);
     } else {
         *kernel = "dq-quantize";
-        // 16 elements a thread, at most 2048 workgroups (each re-reads the ranges).
-        const uint64_t threads = ((uint64_t)d.count + 15) / 16;
-        uint64_t wgs = (threads + DQ_THREADS - 1) / DQ_THREADS;
-        wgs = wgs > 2048 ? 2048 : wgs;
+        // One block of 4096 elements a workgroup, at most 2048 workgroups (each re-reads the ranges).
+        uint64_t wgs = ((uint64_t)d.count + 4095) / 4096;
+        wgs = wgs > 2048 ? 2048 : (wgs < 1 ? 1 : wgs);
         hipLaunchKernelGGL(k_dq_quantize, dim3((uint32_t)wgs), dim3(DQ_THREADS), 0, s, d.x, d.y, d.count,
                            (const float *)ws.dq_ranges, groups, d.scale, d.zero);
     }
@@ -177,94 +177,303 @@ hipError_t launch_dynamic_quantize(const DqArgs &d, const Workspace &ws, hipStre
 }
 
 // ------------------------------------------------------------------ DequantizeLinear / QuantizeLinear
+//
+// Both are element-wise streams; a workgroup of 256 threads takes 4096 consecutive elements. When every tensor the
+// pass streams starts 16-byte aligned, lane l of wave w moves elements 1024 w + 256 c + 4 l .. + 3 for c = 0..3 with
+// one vector access each (4, 8 or 16 bytes): every instruction then reads or writes one contiguous span across the
+// wave, which is what streams at HBM rate (16 contiguous elements a lane, a 64-byte stride across the wave, runs at
+// half of it). Otherwise, and in the tensor's last partial block, lane t takes elements t, t + 256, ... one at a time.
+// The scale (and zero point) of element j is the one at axis index (j / inner) % axis_len: found once a run of 4.
 
-// binary32 -> binary16, round to nearest even, overflow to infinity, NaN to a quiet NaN of the same sign
-// (the integer conversion of Common.hlsl:52-92, so the bits do not depend on the hardware converter).
+constexpr int kEwThreads = 256, kEwBlock = 4096;
+
+typedef int32_t i4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+
+// binary32 -> binary16 bits: the hardware conversion (round to nearest even, binary16 subnormals kept, overflow to
+// infinity), with every NaN made the quiet NaN 0x7E00 of its sign, as the reference's integer conversion writes it.
 __device__ __forceinline__ uint16_t f2h(float f)
 {
-    uint32_t x = __float_as_uint(f);
-    uint32_t s = (x >> 16) & 0x8000u, a = x & 0x7FFFFFFFu;
-    if (a > 0x7F800000u) return (uint16_t)(s | 0x7E00u);
-    if (a >= 0x477FF000u) return (uint16_t)(s | 0x7C00u);
-    if (a < 0x38800000u) {
-        if (a < 0x33000000u) return (uint16_t)s;
-        uint32_t e = a >> 23, mant = (a & 0x7FFFFFu) | 0x800000u, sh = 126u - e;
-        uint32_t m = mant >> sh, rem = mant & ((1u << sh) - 1u), halfway = 1u << (sh - 1u);
-        if (rem > halfway || (rem == halfway && (m & 1u) != 0u)) m += 1u;
-        return (uint16_t)(s | m);
-    }
-    uint32_t r = a - 0x38000000u;
-    r += 0xFFFu + ((r >> 13) & 1u);
-    return (uint16_t)(s | (r >> 13));
+    const uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)f);
+    return is_nan_bits(f) ? (uint16_t)(((__float_as_uint(f) >> 16) & 0x8000u) | 0x7E00u) : h;
 }
 
 template <int KIND>
 __device__ __forceinline__ int32_t load_q(const void *p, uint32_t i)
 {
-    if (KIND == OG_KIND_U8) return (int32_t)static_cast<const uint8_t *>(p)[i];
+    if (KIND == OG_KIND_U8) return (int32_t) static_cast<const uint8_t *>(p)[i];
     if (KIND == OG_KIND_I8) return (int32_t) static_cast<const int8_t *>(p)[i];
     return static_cast<const int32_t *>(p)[i];
 }
 
-template <int KIND, bool F16>
-__global__ __launch_bounds__(256) void k_dequantize(DequantArgs d)
+// The axis index of a run of consecutive elements, starting at element j and moved one element by step().
+template <bool PER_AXIS>
+struct AxisWalk {
+    uint32_t a = 0, r = 0;
+    __device__ __forceinline__ AxisWalk(const DequantArgs &d, uint32_t j)
+    {
+        if (PER_AXIS) {
+            if (d.inner == 1) {
+                a = j % d.axis_len;
+            } else {
+                const uint32_t q = j / d.inner;
+                r = j - q * d.inner;
+                a = q % d.axis_len;
+            }
+        }
+    }
+    __device__ __forceinline__ void step(const DequantArgs &d)
+    {
+        if (PER_AXIS && ++r == d.inner) {
+            r = 0;
+            if (++a == d.axis_len) a = 0;
+        }
+    }
+};
+
+// The first element of lane run c (0..3) of this thread in an aligned block.
+__device__ __forceinline__ uint32_t ew_run(uint32_t block, int c)
 {
-    const uint32_t j = blockIdx.x * 256 + threadIdx.x;
-    if (j >= d.count) return;
-    const uint32_t a = d.per_axis ? (j / d.inner) % d.axis_len : 0u;
-    const int32_t zp = d.has_zero ? load_q<KIND>(d.zero, a) : 0;
-    const int32_t q = (int32_t)((uint32_t)load_q<KIND>(d.x, j) - (uint32_t)zp);   // wraps in 32 bits
-    const float y = __fmul_rn((float)q, d.scale[a]);
-    if (F16) static_cast<uint16_t *>(d.out)[j] = f2h(y);
-    else static_cast<float *>(d.out)[j] = y;
+    return block * kEwBlock + (threadIdx.x >> 6) * 1024u + (uint32_t)c * 256u + (threadIdx.x & 63u) * 4u;
+}
+
+// The scale and zero point at axis index a.
+template <int KIND>
+struct DequantParam {
+    int32_t zp;
+    float scale;
+    __device__ __forceinline__ DequantParam(const DequantArgs &d, uint32_t a)
+        : zp(d.has_zero ? load_q<KIND>(d.zero, a) : 0), scale(d.scale[a]) {}
+};
+
+// y = fl((x - zp) * scale), the difference wrapping in 32 bits (DequantizeKernels.cs:64-150).
+template <int KIND>
+__device__ __forceinline__ float dequant_one(int32_t x, const DequantParam<KIND> &p)
+{
+    return __fmul_rn((float)(int32_t)((uint32_t)x - (uint32_t)p.zp), p.scale);
+}
+
+template <bool F16>
+__device__ __forceinline__ void store_y(void *out, uint32_t j, float y)
+{
+    if (F16) static_cast<uint16_t *>(out)[j] = f2h(y);
+    else static_cast<float *>(out)[j] = y;
+}
+
+// The scales and zero points of a run of four elements whose axis indices are a .. a + 3 (per column: inner 1, an
+// axis length that is a multiple of 4, the scales 16-byte and the zero points 4-element aligned): one vector load each.
+template <int KIND>
+__device__ __forceinline__ void column_params(const DequantArgs &d, uint32_t a, DequantParam<KIND> p[4])
+{
+    const f4 s = *reinterpret_cast<const f4 *>(d.scale + a);
+    int32_t z[4] = {0, 0, 0, 0};
+    if (d.has_zero) {
+        if constexpr (KIND == OG_KIND_I32) {
+            const i4v v = *reinterpret_cast<const i4v *>(static_cast<const int32_t *>(d.zero) + a);
+            z[0] = v.x; z[1] = v.y; z[2] = v.z; z[3] = v.w;
+        } else {
+            const uint32_t v = *reinterpret_cast<const uint32_t *>(static_cast<const uint8_t *>(d.zero) + a);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t b = (v >> (8 * e)) & 0xFFu;
+                z[e] = KIND == OG_KIND_I8 ? (int32_t)(int8_t)b : (int32_t)b;
+            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        p[e].zp = z[e];
+        p[e].scale = s[e];
+    }
+}
+
+// PER: 0 one scale for the tensor, 1 per axis, 2 per column in runs of four (column_params' conditions).
+template <int KIND, bool F16, int PER, bool VEC>
+__global__ __launch_bounds__(kEwThreads) void k_dequantize(DequantArgs d)
+{
+    constexpr bool PER_AXIS = PER != 0;
+    if (VEC && ((uint64_t)blockIdx.x + 1) * kEwBlock <= d.count) {
+        int32_t q[4][4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {   // all loads first, so that the four are in flight together
+            const uint32_t j = ew_run(blockIdx.x, c);
+            if constexpr (KIND == OG_KIND_I32) {
+                const i4v v = __builtin_nontemporal_load(reinterpret_cast<const i4v *>(static_cast<const int32_t *>(d.x) + j));
+                q[c][0] = v.x; q[c][1] = v.y; q[c][2] = v.z; q[c][3] = v.w;
+            } else {
+                const uint32_t v = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(static_cast<const uint8_t *>(d.x) + j));
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const uint32_t b = (v >> (8 * e)) & 0xFFu;
+                    q[c][e] = KIND == OG_KIND_I8 ? (int32_t)(int8_t)b : (int32_t)b;
+                }
+            }
+        }
+        const DequantParam<KIND> p0(d, 0);   // the one scale and zero point of a per-tensor pass
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t j = ew_run(blockIdx.x, c);
+            float y[4];
+            if constexpr (PER == 2) {
+                DequantParam<KIND> p[4] = {p0, p0, p0, p0};
+                column_params<KIND>(d, j % d.axis_len, p);
+#pragma unroll
+                for (int e = 0; e < 4; e++) y[e] = dequant_one<KIND>(q[c][e], p[e]);
+            } else {
+                AxisWalk<PER_AXIS> w(d, j);
+#pragma unroll
+                for (int e = 0; e < 4; e++, w.step(d)) y[e] = dequant_one<KIND>(q[c][e], PER_AXIS ? DequantParam<KIND>(d, w.a) : p0);
+            }
+            if constexpr (F16) {
+                const u2v h = {(uint32_t)f2h(y[0]) | ((uint32_t)f2h(y[1]) << 16), (uint32_t)f2h(y[2]) | ((uint32_t)f2h(y[3]) << 16)};
+                *reinterpret_cast<u2v *>(static_cast<uint16_t *>(d.out) + j) = h;
+            } else {
+                *reinterpret_cast<f4 *>(static_cast<float *>(d.out) + j) = f4{y[0], y[1], y[2], y[3]};
+            }
+        }
+    } else {
+#pragma unroll 4
+        for (int e = 0; e < kEwBlock / kEwThreads; e++) {
+            const uint64_t j = (uint64_t)blockIdx.x * kEwBlock + (uint64_t)e * kEwThreads + threadIdx.x;
+            if (j < d.count) {
+                const AxisWalk<PER_AXIS> w(d, (uint32_t)j);
+                store_y<F16>(d.out, (uint32_t)j, dequant_one<KIND>(load_q<KIND>(d.x, (uint32_t)j), DequantParam<KIND>(d, w.a)));
+            }
+        }
+    }
+}
+
+static bool ew_aligned(const void *a, const void *b) { return (((uintptr_t)a | (uintptr_t)b) & 15) == 0; }
+
+static dim3 ew_grid(uint32_t count) { return dim3((uint32_t)(((uint64_t)count + kEwBlock - 1) / kEwBlock)); }
+
+template <int KIND, bool F16>
+static void launch_dequantize_as(const DequantArgs &d, bool vec, hipStream_t s)
+{
+    const dim3 grid = ew_grid(d.count), block(kEwThreads);
+    const uintptr_t zero_align = KIND == OG_KIND_I32 ? 15 : 3;
+    const bool columns = d.per_axis && d.inner == 1 && d.axis_len % 4 == 0 && ((uintptr_t)d.scale & 15) == 0 &&
+                         (!d.has_zero || ((uintptr_t)d.zero & zero_align) == 0);
+    if (vec && columns) hipLaunchKernelGGL((k_dequantize<KIND, F16, 2, true>), grid, block, 0, s, d);
+    else if (d.per_axis) {
+        if (vec) hipLaunchKernelGGL((k_dequantize<KIND, F16, 1, true>), grid, block, 0, s, d);
+        else hipLaunchKernelGGL((k_dequantize<KIND, F16, 1, false>), grid, block, 0, s, d);
+    } else {
+        if (vec) hipLaunchKernelGGL((k_dequantize<KIND, F16, 0, true>), grid, block, 0, s, d);
+        else hipLaunchKernelGGL((k_dequantize<KIND, F16, 0, false>), grid, block, 0, s, d);
+    }
 }
 
 hipError_t launch_dequantize(const DequantArgs &d, int kind, bool f16_out, hipStream_t s, const char **kernel)
 {
-    *kernel = f16_out ? "dequantize-f16" : "dequantize-f32";
+    const bool vec = ew_aligned(d.x, d.out);
+    *kernel = f16_out ? (vec ? "dequantize4-f16" : "dequantize-f16") : (vec ? "dequantize4-f32" : "dequantize-f32");
     if (d.count == 0) return hipSuccess;
-    dim3 grid((d.count + 255) / 256), block(256);
-#define OG_DQ(K, H) hipLaunchKernelGGL((k_dequantize<K, H>), grid, block, 0, s, d)
     switch (kind * 2 + (f16_out ? 1 : 0)) {
-    case 0: OG_DQ(OG_KIND_U8, false); break;
-    case 1: OG_DQ(OG_KIND_U8, true); break;
-    case 2: OG_DQ(OG_KIND_I8, false); break;
-    case 3: OG_DQ(OG_KIND_I8, true); break;
-    case 4: OG_DQ(OG_KIND_I32, false); break;
-    default: OG_DQ(OG_KIND_I32, true); break;
+    case 0: launch_dequantize_as<OG_KIND_U8, false>(d, vec, s); break;
+    case 1: launch_dequantize_as<OG_KIND_U8, true>(d, vec, s); break;
+    case 2: launch_dequantize_as<OG_KIND_I8, false>(d, vec, s); break;
+    case 3: launch_dequantize_as<OG_KIND_I8, true>(d, vec, s); break;
+    case 4: launch_dequantize_as<OG_KIND_I32, false>(d, vec, s); break;
+    default: launch_dequantize_as<OG_KIND_I32, true>(d, vec, s); break;
     }
-#undef OG_DQ
     return hipGetLastError();
 }
 
-template <bool SIGNED, bool F16>
-__global__ __launch_bounds__(256) void k_quantize(DequantArgs d)
+// The scale and zero point (as a float) at axis index a.
+template <bool SIGNED>
+struct QuantParam {
+    float zp, scale;
+    __device__ __forceinline__ QuantParam(const DequantArgs &d, uint32_t a)
+        : zp(!d.has_zero ? 0.0f
+                         : (float)(SIGNED ? (int32_t) static_cast<const int8_t *>(d.zero)[a]
+                                          : (int32_t) static_cast<const uint8_t *>(d.zero)[a])),
+          scale(d.scale[a]) {}
+};
+
+// y = saturate(rne(x / scale) + zp), NaN to the lowest value (DequantizeKernels.cs:204-272).
+template <bool SIGNED>
+__device__ __forceinline__ uint32_t quant_one(float x, const QuantParam<SIGNED> &p)
 {
-    const uint32_t j = blockIdx.x * 256 + threadIdx.x;
-    if (j >= d.count) return;
-    const uint32_t a = d.per_axis ? (j / d.inner) % d.axis_len : 0u;
-    int32_t zp = 0;
-    if (d.has_zero) zp = SIGNED ? (int32_t) static_cast<const int8_t *>(d.zero)[a] : (int32_t) static_cast<const uint8_t *>(d.zero)[a];
-    const float x = F16 ? (float)__builtin_bit_cast(_Float16, static_cast<const uint16_t *>(d.x)[j])
-                        : static_cast<const float *>(d.x)[j];
     const float lo = SIGNED ? -128.0f : 0.0f, hi = SIGNED ? 127.0f : 255.0f;
-    float v = __fadd_rn(rintf(x / d.scale[a]), (float)zp);
+    float v = __fadd_rn(rintf(x / p.scale), p.zp);
     if (is_nan_bits(v)) v = lo;
-    const int32_t q = (int32_t)fminf(fmaxf(v, lo), hi);
-    static_cast<uint8_t *>(d.out)[j] = (uint8_t)q;
+    return (uint32_t)(int32_t)fminf(fmaxf(v, lo), hi) & 0xFFu;
+}
+
+template <bool F16>
+__device__ __forceinline__ float load_x(const void *p, uint32_t j)
+{
+    return F16 ? (float)__builtin_bit_cast(_Float16, static_cast<const uint16_t *>(p)[j]) : static_cast<const float *>(p)[j];
+}
+
+template <bool SIGNED, bool F16, bool PER_AXIS, bool VEC>
+__global__ __launch_bounds__(kEwThreads) void k_quantize(DequantArgs d)
+{
+    uint8_t *out = static_cast<uint8_t *>(d.out);
+    if (VEC && ((uint64_t)blockIdx.x + 1) * kEwBlock <= d.count) {
+        float x[4][4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t j = ew_run(blockIdx.x, c);
+            if constexpr (F16) {
+                const u2v v = __builtin_nontemporal_load(reinterpret_cast<const u2v *>(static_cast<const uint16_t *>(d.x) + j));
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    x[c][e] = (float)__builtin_bit_cast(_Float16, (uint16_t)(v[e >> 1] >> (16 * (e & 1))));
+            } else {
+                const f4 v = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(static_cast<const float *>(d.x) + j));
+                x[c][0] = v.x; x[c][1] = v.y; x[c][2] = v.z; x[c][3] = v.w;
+            }
+        }
+        const QuantParam<SIGNED> p0(d, 0);   // the one scale and zero point of a per-tensor pass
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t j = ew_run(blockIdx.x, c);
+            AxisWalk<PER_AXIS> w(d, j);
+            uint32_t y = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++, w.step(d)) y |= quant_one<SIGNED>(x[c][e], PER_AXIS ? QuantParam<SIGNED>(d, w.a) : p0) << (8 * e);
+            *reinterpret_cast<uint32_t *>(out + j) = y;
+        }
+    } else {
+#pragma unroll 4
+        for (int e = 0; e < kEwBlock / kEwThreads; e++) {
+            const uint64_t j = (uint64_t)blockIdx.x * kEwBlock + (uint64_t)e * kEwThreads + threadIdx.x;
+            if (j < d.count) {
+                const AxisWalk<PER_AXIS> w(d, (uint32_t)j);
+                out[j] = (uint8_t)quant_one<SIGNED>(load_x<F16>(d.x, (uint32_t)j), QuantParam<SIGNED>(d, w.a));
+            }
+        }
+    }
+}
+
+template <bool SIGNED, bool F16>
+static void launch_quantize_as(const DequantArgs &d, bool vec, hipStream_t s)
+{
+    const dim3 grid = ew_grid(d.count), block(kEwThreads);
+    if (d.per_axis) {
+        if (vec) hipLaunchKernelGGL((k_quantize<SIGNED, F16, true, true>), grid, block, 0, s, d);
+        else hipLaunchKernelGGL((k_quantize<SIGNED, F16, true, false>), grid, block, 0, s, d);
+    } else {
+        if (vec) hipLaunchKernelGGL((k_quantize<SIGNED, F16, false, true>), grid, block, 0, s, d);
+        else hipLaunchKernelGGL((k_quantize<SIGNED, F16, false, false>), grid, block, 0, s, d);
+    }
 }
 
 hipError_t launch_quantize(const DequantArgs &d, bool is_signed, bool f16_in, hipStream_t s, const char **kernel)
 {
-    *kernel = is_signed ? (f16_in ? "quantize-f16-i8" : "quantize-f32-i8") : (f16_in ? "quantize-f16-u8" : "quantize-f32-u8");
+    const bool vec = ew_aligned(d.x, d.out);
+    static const char *names[2][2][2] = {{{"quantize-f32-u8", "quantize-f16-u8"}, {"quantize-f32-i8", "quantize-f16-i8"}},
+                                         {{"quantize4-f32-u8", "quantize4-f16-u8"}, {"quantize4-f32-i8", "quantize4-f16-i8"}}};
+    *kernel = names[vec][is_signed][f16_in];
     if (d.count == 0) return hipSuccess;
-    dim3 grid((d.count + 255) / 256), block(256);
     if (is_signed) {
-        if (f16_in) hipLaunchKernelGGL((k_quantize<true, true>), grid, block, 0, s, d);
-        else hipLaunchKernelGGL((k_quantize<true, false>), grid, block, 0, s, d);
+        if (f16_in) launch_quantize_as<true, true>(d, vec, s);
+        else launch_quantize_as<true, false>(d, vec, s);
     } else {
-        if (f16_in) hipLaunchKernelGGL((k_quantize<false, true>), grid, block, 0, s, d);
-        else hipLaunchKernelGGL((k_quantize<false, false>), grid, block, 0, s, d);
+        if (f16_in) launch_quantize_as<false, true>(d, vec, s);
+        else launch_quantize_as<false, false>(d, vec, s);
     }
     return hipGetLastError();
 }

@@ -137,6 +137,13 @@ DEQUANT_SHAPES = [
     ([384, 768], 1, True),
 ]
 
+# Beyond the reference's shapes: tensors of several 4096-element blocks (the aligned kernels' vector path), per axis
+# with inner 5 and 4100 (an axis step inside a run of four elements and across blocks), per column with axes of 300
+# and 4096 (runs of four columns read with one vector load) and of 7 (the axis wraps inside a run), and a per-tensor
+# count with a ragged last block.
+DEQUANT_SHAPES_BLOCKS = [([64, 96, 5], 1, True), ([3, 4100], 0, True), ([8, 7, 300], 2, True), ([33, 4096], 1, True),
+                         ([2000, 7], 1, True), ([5, 4099], -1, False)]
+
 # DequantizeTests.cs:270: the scale sets of QuantizeIsExact.
 QUANT_SCALE_SETS = [[0.5], [1.0], [0.0137, 0.25, 3.3], [1.0 / 255.0, 0.09999], [1e-6, 1e3, 0.7]]
 

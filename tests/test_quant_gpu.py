@@ -10,7 +10,20 @@ from gpu_rig import device, run, say
 
 pytestmark = pytest.mark.gpu
 
-OffX, OffS, OffZ, OffO = 3, 1, 2, 5
+# Element offsets of x, scale, zero point and output: the reference's (every tensor unaligned, so each element moves on
+# its own), and all zero (16-byte aligned starts: a thread's 16 elements move with vector loads and stores).
+UNALIGNED, ALIGNED = (3, 1, 2, 5), (0, 0, 0, 0)
+
+
+def run_named(d, record) -> list:
+    """Records one pass with a timing pair around each dispatch and returns the dispatches' kernel names."""
+    e = d.BeginCommands()
+    e.BeginPassTiming(1)
+    record(e)
+    e.EndPassTiming()
+    d.Submit(e)
+    d.WaitIdle()
+    return [k for _, k in d.ReadPassTimes()]
 
 
 def _quantized(dtype, n, seed):
@@ -20,8 +33,9 @@ def _quantized(dtype, n, seed):
     return oracle.dequant_input_bytes(og.padded_bool_length(max(n, 1)), seed).view(dtype)
 
 
-def _dequant_case(d, k, dtype, shape, axis, per_axis, with_zero, half, seed):
+def _dequant_case(d, k, dtype, shape, axis, per_axis, with_zero, half, seed, offs=UNALIGNED):
     """DequantizeTests.Case (DequantizeTests.cs:36-88)."""
+    OffX, OffS, OffZ, OffO = offs
     n, axis_len, inner = cases.axis_split(shape, axis, per_axis)
     x = _quantized(dtype, n + OffX, seed)
     scale = oracle.rig_random(axis_len + OffS, seed + 1, 0.001, 2.0)
@@ -32,7 +46,10 @@ def _dequant_case(d, k, dtype, shape, axis, per_axis, with_zero, half, seed):
     sentinel = np.float16(-77) if half else np.float32(-77)
     out = np.full(length, sentinel, np.float16 if half else np.float32)
     bx, bs, bz, bo = d.CreateBuffer(x), d.CreateBuffer(scale), d.CreateBuffer(zeros), d.CreateBuffer(out)
-    run(d, lambda e: k.Encode(e, bx, OffX, shape, axis, per_axis, bs, OffS, bz if with_zero else None, OffZ, bo, OffO))
+    names = run_named(d, lambda e: k.Encode(e, bx, OffX, shape, axis, per_axis, bs, OffS, bz if with_zero else None, OffZ,
+                                             bo, OffO))
+    want_kernel = ("dequantize4-" if offs == ALIGNED else "dequantize-") + ("f16" if half else "f32")
+    assert names == [want_kernel], names
     got = bo.Read()
     gbits = got.view(np.uint16 if half else np.uint32)
     wbits = want.view(np.uint16) if half else want.view(np.uint32)
@@ -42,23 +59,57 @@ def _dequant_case(d, k, dtype, shape, axis, per_axis, with_zero, half, seed):
     return bad
 
 
+@pytest.mark.parametrize("offs", [UNALIGNED, ALIGNED], ids=["unaligned", "aligned"])
 @pytest.mark.parametrize("dtype,seed0", [(np.uint8, 1), (np.int8, 100), (np.int32, 200)])
-def test_dequantize_is_exact(dtype, seed0):
-    # DequantizeIsExact (DequantizeTests.cs:113-124)
+def test_dequantize_is_exact(dtype, seed0, offs):
+    # DequantizeIsExact (DequantizeTests.cs:113-124), at the reference's offsets and at aligned ones
     d = device()
     k = og.DequantizeKernels(d)
     seed, bad = seed0, 0
-    for shape, axis, per_axis in cases.DEQUANT_SHAPES:
+    for shape, axis, per_axis in cases.DEQUANT_SHAPES + cases.DEQUANT_SHAPES_BLOCKS:
         for with_zero in (True, False):
             for half in (False, True):
-                say(f"dequantize {np.dtype(dtype).name} {shape} axis {axis} per {per_axis} zero {with_zero} f16 {half}")
-                bad += _dequant_case(d, k, dtype, shape, axis, per_axis, with_zero, half, seed)
+                say(f"dequantize {np.dtype(dtype).name} {shape} axis {axis} per {per_axis} zero {with_zero} f16 {half} "
+                    f"offsets {offs}")
+                bad += _dequant_case(d, k, dtype, shape, axis, per_axis, with_zero, half, seed, offs)
                 seed += 1
     assert bad == 0
 
 
-def _quant_case(d, k, signed, shape, axis, per_axis, with_zero, half_in, scales, seed):
+def test_binary16_conversion_is_exact():
+    # Every binary32 -> binary16 case the output conversion meets, through DequantizeLinear of int32 ones with one scale
+    # per element (y = fl(1 * s) = s): ties to even at the normal/subnormal/zero boundaries, the largest finite value and
+    # the first to overflow, infinities, signed zeros and NaNs with payloads and either sign (all become 0x7E00 of their
+    # sign). Checked against numpy's float16 cast, with the NaNs canonicalised, and against the oracle's conversion.
+    f = np.float32
+    halfulp = lambda v: f(v) * f(1 + 2**-11)  # noqa: E731
+    probes = [0.0, -0.0, 1.0, -1.0, 1.0 + 2**-11, 1.0 + 3 * 2**-11, 1.0 + 2**-11 + 2**-20, 65504.0, 65519.996,
+              65520.0, -65520.0, 2**-14, 2**-14 * (1 - 2**-11), 2**-24, 2**-25, 2**-25 * (1 + 2**-20), -2**-25,
+              3 * 2**-25, 2**-26, 1e-8, 6e-5, 6.1e-5, -3.14159, 0.1, 1e30, -1e-30, float(halfulp(2.0))]
+    probes += [np.inf, -np.inf]
+    nans = np.array([0x7FC00000, 0xFFC00000, 0x7F800001, 0xFFBFFFFF, 0x7FC0ABCD], np.uint32).view(np.float32)
+    rng = np.random.default_rng(16)
+    rand = np.concatenate([rng.uniform(-70000, 70000, 200), rng.uniform(-1e-4, 1e-4, 200),
+                           rng.standard_normal(200) * 2.0 ** rng.integers(-30, 17, 200)]).astype(np.float32)
+    s = np.concatenate([np.array(probes, np.float32), nans, rand]).astype(np.float32)
+    n = s.size
+    d = device()
+    k = og.DequantizeKernels(d)
+    out = np.zeros(og.padded_half_length(n), np.float16)
+    bx, bs, bo = d.CreateBuffer(np.ones(n, np.int32)), d.CreateBuffer(s), d.CreateBuffer(out)
+    run(d, lambda e: k.Encode(e, bx, 0, [n], 0, True, bs, 0, None, 0, bo, 0))
+    got = bo.Read().view(np.uint16)[:n]
+    with np.errstate(over="ignore"):
+        want = s.astype(np.float16).view(np.uint16).copy()
+    isnan = np.isnan(s)
+    want[isnan] = (s.view(np.uint32)[isnan] >> 16).astype(np.uint16) & 0x8000 | 0x7E00
+    assert np.array_equal(got, want), [(float(s[i]), hex(got[i]), hex(want[i])) for i in np.nonzero(got != want)[0][:8]]
+    assert np.array_equal(want, np.array([oracle.f2h(float(v)) for v in s], np.uint16))
+
+
+def _quant_case(d, k, signed, shape, axis, per_axis, with_zero, half_in, scales, seed, offs=UNALIGNED):
     """DequantizeTests.QuantizeCase (DequantizeTests.cs:179-255)."""
+    OffX, OffS, OffZ, OffO = offs
     n, axis_len, inner = cases.axis_split(shape, axis, per_axis)
     x = oracle.quantize_input(n + OffX, seed, True)
     xh = x.astype(np.float16)
@@ -78,7 +129,11 @@ def _quant_case(d, k, signed, shape, axis, per_axis, with_zero, half_in, scales,
     xin[:xh.size] = xh
     bx = d.CreateBuffer(xin if half_in else x)
     bs, bz, bo = d.CreateBuffer(scale), d.CreateBuffer(zeros), d.CreateBuffer(out)
-    run(d, lambda e: k.EncodeQuantize(e, bx, OffX, shape, axis, per_axis, bs, OffS, bz if with_zero else None, OffZ, bo, OffO))
+    names = run_named(d, lambda e: k.EncodeQuantize(e, bx, OffX, shape, axis, per_axis, bs, OffS, bz if with_zero else None,
+                                                     OffZ, bo, OffO))
+    want_kernel = ("quantize4-" if offs == ALIGNED else "quantize-") + ("f16-" if half_in else "f32-") + \
+        ("i8" if signed else "u8")
+    assert names == [want_kernel], names
     got = bo.Read().view(np.uint8)
     init = out.view(np.uint8)
     bad = int(np.count_nonzero(got[OffO:OffO + n] != want))
@@ -86,18 +141,20 @@ def _quant_case(d, k, signed, shape, axis, per_axis, with_zero, half_in, scales,
     return bad
 
 
-def test_quantize_is_exact():
-    # QuantizeIsExact (DequantizeTests.cs:257-289)
+@pytest.mark.parametrize("offs", [UNALIGNED, ALIGNED], ids=["unaligned", "aligned"])
+def test_quantize_is_exact(offs):
+    # QuantizeIsExact (DequantizeTests.cs:257-289), at the reference's offsets and at aligned ones
     d = device()
     k = og.DequantizeKernels(d)
     bad = count = 0
     seed = 1
-    for shape, axis, per_axis in cases.DEQUANT_SHAPES:
+    for shape, axis, per_axis in cases.DEQUANT_SHAPES + cases.DEQUANT_SHAPES_BLOCKS:
         for with_zero in (True, False):
             scales = cases.QUANT_SCALE_SETS[count % len(cases.QUANT_SCALE_SETS)]
             for signed, half_in in ((False, False), (True, False), (False, True), (True, True)):
-                say(f"quantize {shape} axis {axis} per {per_axis} zero {with_zero} signed {signed} f16 {half_in}")
-                bad += _quant_case(d, k, signed, shape, axis, per_axis, with_zero, half_in, scales, seed)
+                say(f"quantize {shape} axis {axis} per {per_axis} zero {with_zero} signed {signed} f16 {half_in} "
+                    f"offsets {offs}")
+                bad += _quant_case(d, k, signed, shape, axis, per_axis, with_zero, half_in, scales, seed, offs)
                 seed += 1
                 count += 1
     assert bad == 0
