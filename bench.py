@@ -407,6 +407,7 @@ def elementwise_c5(d, steps, warmup, which, check=True):
     res = {"elements": n, "bytes": bytes_, "wall_s": wall, "step_mean_us": step_us, "per_kernel": per,
            "gbs": bytes_ / (step_us * 1e-6) / 1e9}
     res["hbm_frac"] = res["gbs"] / PEAK_HBM_GBS
+    res["traffic"] = {k: traffic_of(k, which) for k in per}
     if which == "dq":
         per["dq-minmax"]["bytes"], per["dq-quantize"]["bytes"] = 4 * n, 5 * n + 5
         for kk in per:
