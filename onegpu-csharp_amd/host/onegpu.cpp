@@ -322,8 +322,34 @@ static void CheckRange(const std::string &operand, int offset, int stride, int r
                                                                      " but its buffer holds " + std::to_string(length));
 }
 
+// ------------------------------------------------------------------ ArgumentBlocks
+
+ArgumentBlocks::ArgumentBlocks(int capacity) : capacity_(capacity < 1 ? 1 : capacity) {}
+
+void ArgumentBlocks::Note(uint64_t kind, std::initializer_list<const GpuBuffer *> buffers)
+{
+    std::vector<uintptr_t> key;
+    key.reserve(buffers.size() + 1);
+    key.push_back((uintptr_t)kind);
+    for (const GpuBuffer *b : buffers) key.push_back((uintptr_t)(b && b->Valid() ? b->impl().get() : nullptr));
+    ++clock_;
+    for (auto &entry : blocks_)
+        if (entry.first == key) {
+            entry.second = clock_;
+            return;
+        }
+    ++created_;
+    if ((int)blocks_.size() >= capacity_) {
+        auto oldest = blocks_.begin();
+        for (auto it = blocks_.begin(); it != blocks_.end(); ++it)
+            if (it->second < oldest->second) oldest = it;
+        blocks_.erase(oldest);
+    }
+    blocks_.emplace_back(std::move(key), clock_);
+}
+
 Int8Gemm::Int8Gemm(std::shared_ptr<GpuDevice> device, Int8GemmOptions options, int maxCachedBindGroups)
-    : device_(std::move(device)), options_(options)
+    : device_(std::move(device)), options_(options), blocks_(maxCachedBindGroups)
 {
     if (!device_) throw std::invalid_argument("device");
     if (maxCachedBindGroups < 1) throw std::out_of_range("maxCachedBindGroups");
@@ -547,6 +573,7 @@ void Int8Gemm::EncodeRequantized(GpuCommandEncoder &encoder, const Int8GemmProbl
     w.OffScale = (uint32_t)multiplier.Offset;
     w.ZeroPoint = zeroPointY;
     GpuBuffer mult = multiplier.Buffer;
+    blocks_.Note(4, {&sums, &y, &biasBuf, &mult});
     encoder.Record(
         [w, sums, y, biasBuf, mult](og_ctx *ctx) {
             ThrowIfFailed(ctx, og_int8_epilogue(ctx, &w, bind(sums), bind(y), bind(biasBuf), bind(mult), og_buffer{nullptr, 0}), kGemm);
@@ -644,6 +671,7 @@ void Int8Gemm::Multiply(GpuCommandEncoder &encoder, const Int8GemmProblem &p, co
     if (epi.Requantized) {
         const int32_t zy = epi.ZeroPointY;
         const uint32_t ys = epi.SignedY ? 1u : 0u;
+        blocks_.Note(3, {&A, &B, &C, &zaBuf, &zbBuf, &ib, &sc});
         encoder.Record(
             [w, batch, A, B, C, zaBuf, zbBuf, ib, sc, zy, ys](og_ctx *ctx) {
                 ThrowIfFailed(ctx, og_int8_gemm_requantized(ctx, &w, batch, bind(A), bind(B), bind(C), bind(zaBuf), bind(zbBuf), bind(ib), bind(sc), zy, ys), kGemm);
@@ -654,6 +682,7 @@ void Int8Gemm::Multiply(GpuCommandEncoder &encoder, const Int8GemmProblem &p, co
     if (epi.ActScale.Valid()) {
         GpuBuffer as = epi.ActScale;
         const uint32_t aoff = epi.OffActScale;
+        blocks_.Note(2, {&A, &B, &C, &zaBuf, &zbBuf, &ib, &as, &sc, &fb});
         encoder.Record(
             [w, batch, A, B, C, zaBuf, zbBuf, ib, as, aoff, sc, fb](og_ctx *ctx) {
                 ThrowIfFailed(ctx, og_int8_gemm_float_scaled(ctx, &w, batch, bind(A), bind(B), bind(C), bind(zaBuf), bind(zbBuf), bind(ib), bind(as), aoff, bind(sc), bind(fb)), kGemm);
@@ -661,6 +690,7 @@ void Int8Gemm::Multiply(GpuCommandEncoder &encoder, const Int8GemmProblem &p, co
             keep_of({&A, &B, &C, &zaBuf, &zbBuf, &ib, &as, &sc, &fb}));
         return;
     }
+    blocks_.Note(1, {&A, &B, &C, &zaBuf, &zbBuf, &ib, &sc, &fb});
     encoder.Record(
         [w, batch, A, B, C, zaBuf, zbBuf, ib, sc, fb](og_ctx *ctx) {
             ThrowIfFailed(ctx, og_int8_gemm(ctx, &w, batch, bind(A), bind(B), bind(C), bind(zaBuf), bind(zbBuf), bind(ib), bind(sc), bind(fb)), kGemm);
@@ -671,7 +701,7 @@ void Int8Gemm::Multiply(GpuCommandEncoder &encoder, const Int8GemmProblem &p, co
 // ------------------------------------------------------------------ DynamicQuantizeKernels
 
 DynamicQuantizeKernels::DynamicQuantizeKernels(std::shared_ptr<GpuDevice> device, int maxCachedBindGroups)
-    : device_(std::move(device))
+    : device_(std::move(device)), blocks_(maxCachedBindGroups)
 {
     if (!device_) throw std::invalid_argument("device");
     if (maxCachedBindGroups < 1) throw std::out_of_range("maxCachedBindGroups");
@@ -702,6 +732,8 @@ void DynamicQuantizeKernels::Encode(GpuCommandEncoder &encoder, const GpuBuffer 
     w.OffScale = (uint32_t)offsetScale;
     w.OffZero = (uint32_t)offsetZeroPoint;
     GpuBuffer X = x, Y = y, S = scale, Z = zeroPoint;
+    blocks_.Note(1, {&X});                 // the range pass
+    blocks_.Note(2, {&X, &Y, &S, &Z});     // the quantize pass
     encoder.Record(
         [w, X, Y, S, Z](og_ctx *ctx) {
             ThrowIfFailed(ctx, og_dynamic_quantize(ctx, &w, bind(X), bind(Y), bind(S), bind(Z)), "DynamicQuantizeLinear");
@@ -711,7 +743,8 @@ void DynamicQuantizeKernels::Encode(GpuCommandEncoder &encoder, const GpuBuffer 
 
 // ------------------------------------------------------------------ DequantizeKernels
 
-DequantizeKernels::DequantizeKernels(std::shared_ptr<GpuDevice> device, int maxCachedBindGroups) : device_(std::move(device))
+DequantizeKernels::DequantizeKernels(std::shared_ptr<GpuDevice> device, int maxCachedBindGroups)
+    : device_(std::move(device)), blocks_(maxCachedBindGroups)
 {
     if (!device_) throw std::invalid_argument("device");
     if (maxCachedBindGroups < 1) throw std::out_of_range("maxCachedBindGroups");
@@ -789,6 +822,7 @@ void DequantizeKernels::Encode(GpuCommandEncoder &encoder, const GpuBuffer &x, i
     w.AxisLen = (uint32_t)axisLen;
     w.Inner = (uint32_t)std::max<int64_t>(inner, 1);
     GpuBuffer X = x, S = scale, Z = zeroPoint ? *zeroPoint : GpuBuffer(), O = output;
+    blocks_.Note(1 + 2 * (uint64_t)kind + (half ? 1 : 0), {&X, &S, &Z, &O});
     encoder.Record(
         [w, kind, half, X, S, Z, O](og_ctx *ctx) {
             ThrowIfFailed(ctx, og_dequantize(ctx, kind, half ? 1 : 0, &w, bind(X), bind(S), bind(Z), bind(O)), "DequantizeLinear");
@@ -837,6 +871,7 @@ void DequantizeKernels::EncodeQuantize(GpuCommandEncoder &encoder, const GpuBuff
     w.AxisLen = (uint32_t)axisLen;
     w.Inner = (uint32_t)std::max<int64_t>(inner, 1);
     GpuBuffer X = x, S = scale, Z = zeroPoint ? *zeroPoint : GpuBuffer(), O = output;
+    blocks_.Note(16 + 2 * (isSigned ? 1 : 0) + (half ? 1 : 0), {&X, &S, &Z, &O});
     encoder.Record(
         [w, isSigned, half, X, S, Z, O](og_ctx *ctx) {
             ThrowIfFailed(ctx, og_quantize(ctx, isSigned ? 1 : 0, half ? 1 : 0, &w, bind(X), bind(S), bind(Z), bind(O)), "QuantizeLinear");
@@ -867,7 +902,8 @@ void GpuIndexStatus::ThrowIfFailed()
     if (word != 0xFFFFFFFFu) throw GpuKernelIndexException(operation_.empty() ? "index operation" : operation_, word);
 }
 
-GatherKernels::GatherKernels(std::shared_ptr<GpuDevice> device, int maxCachedBindGroups) : device_(std::move(device))
+GatherKernels::GatherKernels(std::shared_ptr<GpuDevice> device, int maxCachedBindGroups)
+    : device_(std::move(device)), blocks_(maxCachedBindGroups)
 {
     if (!device_) throw std::invalid_argument("device");
     if (maxCachedBindGroups < 1) throw std::out_of_range("maxCachedBindGroups");
@@ -940,6 +976,7 @@ void GatherKernels::EncodeGather(GpuCommandEncoder &encoder, const GpuBuffer &da
     w.AxisLen = (uint32_t)axisLength;
     const uint32_t eb = (uint32_t)ElementSize(data.Type());
     GpuBuffer D = data, I = indices, O = output, S = status ? status->Buffer() : GpuBuffer();
+    blocks_.Note(eb, {&D, &I, &O, &S});
     encoder.Record(
         [w, eb, D, I, O, S](og_ctx *ctx) {
             ThrowIfFailed(ctx, og_gather(ctx, eb, &w, bind(D), bind(I), bind(O), bind(S)), "Gather");
@@ -1010,7 +1047,7 @@ static void ConvGeometry(const ConvProblem &p, int &oh, int &ow, int64_t &k, int
 }
 
 ConvIntegerKernels::ConvIntegerKernels(std::shared_ptr<GpuDevice> device, Int8GemmOptions options, int maxCachedBindGroups)
-    : device_(device), options_(options), gemm_(device, options, maxCachedBindGroups)
+    : device_(device), options_(options), gemm_(device, options, maxCachedBindGroups), blocks_(maxCachedBindGroups)
 {
     if (!device_) throw std::invalid_argument("device");
 }
@@ -1152,6 +1189,7 @@ void ConvIntegerKernels::Encode(GpuCommandEncoder &encoder, const ConvProblem &p
     GpuBuffer X = x, W = w, Y = y, XZ = xZeroPoint ? xZeroPoint->Buffer : GpuBuffer(),
               WZ = wZeroPoint ? wZeroPoint->Buffer : GpuBuffer(), S = columns;
     const uint64_t off = (uint64_t)columnBase;
+    blocks_.Note(1, {&X, &W, &Y, &XZ, &WZ, &S});
     encoder.Record(
         [c, X, W, Y, XZ, WZ, S, off](og_ctx *ctx) {
             ThrowIfFailed(ctx, og_conv_integer(ctx, &c, bind(X), bind(W), bind(Y), bind(XZ), bind(WZ), bind(S), off), kConv);

@@ -4,12 +4,14 @@
 //
 // Names, argument meaning, validation order and the exception raised for each bad argument follow the C# sources cited
 // at each member, so code written against the reference API reads the same here. What differs is only what HIP makes
-// moot: there are no bind groups (BindGroupsCreated stays 0), and buffers carry their element type at run time where
-// the C# API has a generic parameter, so the type checks the C# compiler or RequireInt8 makes happen at the call.
+// moot: a kernel's arguments travel by value in the launch packet, so the bind groups become argument blocks that are
+// only counted (ArgumentBlocks), and buffers carry their element type at run time where the C# API has a generic
+// parameter, so the type checks the C# compiler or RequireInt8 makes happen at the call.
 #pragma once
 
 #include <cstdint>
 #include <functional>
+#include <initializer_list>
 #include <memory>
 #include <optional>
 #include <stdexcept>
@@ -202,6 +204,26 @@ struct Int8Scratch {
     int Offset = 0;
 };
 
+// What a kernel family's bind groups (Int8Gemm.cs:365-375; BindingCacheTests.cs:141-197) become on HIP. Nothing is
+// bound: a dispatch's arguments travel by value in its launch packet. A family instead remembers the argument blocks it
+// has recorded, one per dispatch kind and set of buffers (offsets and sizes are launch arguments, as they are uniforms
+// in the reference), at most maxCachedBindGroups of them, the least recently recorded dropped first. Created() counts
+// the blocks added since the family was made: recording a call again with buffers it has seen adds none, and after
+// Release() (ReleaseBindings: the cache emptied, the count kept) the same call adds its blocks again.
+class ArgumentBlocks {
+public:
+    explicit ArgumentBlocks(int capacity);
+    void Note(uint64_t kind, std::initializer_list<const GpuBuffer *> buffers);
+    int Created() const { return created_; }
+    void Release() { blocks_.clear(); }
+
+private:
+    int capacity_;
+    int created_ = 0;
+    uint64_t clock_ = 0;
+    std::vector<std::pair<std::vector<uintptr_t>, uint64_t>> blocks_;   // (kind and buffer identities, last use)
+};
+
 // Int8Gemm.cs:39-95.
 struct Int8GemmProblem {
     Int8GemmProblem() = default;
@@ -248,8 +270,8 @@ public:
     static int64_t ScratchElements(const Int8GemmProblem &problem);   // Int8Gemm.cs:525-531
     void ReserveScratch(int64_t elements);                            // Int8Gemm.cs:533-549
     const std::string &Variant() const { return variant_; }           // Int8Gemm.cs:214-215
-    int BindGroupsCreated() const { return 0; }                       // nothing is bound on HIP
-    void ReleaseBindings() {}
+    int BindGroupsCreated() const { return blocks_.Created(); }       // Int8Gemm.cs:365-366
+    void ReleaseBindings() { blocks_.Release(); }                     // Int8Gemm.cs:368-375
     void Dispose();
 
 private:
@@ -288,6 +310,7 @@ private:
     Int8GemmOptions options_;
     std::string variant_;
     std::vector<GpuBuffer> scratch_;
+    ArgumentBlocks blocks_;
 };
 
 // ------------------------------------------------------------------ DynamicQuantizeKernels (DynamicQuantizeKernels.cs)
@@ -298,12 +321,13 @@ public:
     // DynamicQuantizeKernels.cs:47-90.
     void Encode(GpuCommandEncoder &encoder, const GpuBuffer &x, int offsetX, int count, const GpuBuffer &y, int offsetY,
                 const GpuBuffer &scale, int offsetScale, const GpuBuffer &zeroPoint, int offsetZeroPoint);
-    int BindGroupsCreated() const { return 0; }
-    void ReleaseBindings() {}
+    int BindGroupsCreated() const { return blocks_.Created(); }
+    void ReleaseBindings() { blocks_.Release(); }
     void Dispose() {}
 
 private:
     std::shared_ptr<GpuDevice> device_;
+    ArgumentBlocks blocks_;
 };
 
 // ------------------------------------------------------------------ DequantizeKernels (DequantizeKernels.cs)
@@ -320,12 +344,13 @@ public:
                         int axis, bool perAxis, const GpuBuffer &scale, int offsetScale,
                         const std::optional<GpuBuffer> &zeroPoint, int offsetZeroPoint, const GpuBuffer &output,
                         int offsetOutput);
-    int BindGroupsCreated() const { return 0; }
-    void ReleaseBindings() {}
+    int BindGroupsCreated() const { return blocks_.Created(); }
+    void ReleaseBindings() { blocks_.Release(); }
     void Dispose() {}
 
 private:
     std::shared_ptr<GpuDevice> device_;
+    ArgumentBlocks blocks_;
 };
 
 // The geometry of a convolution (src/RecursiveAI.OneGpu.Kernels/ConvProblem.cs:107-235): NCHW input, OIHW weights,
@@ -356,14 +381,18 @@ public:
     explicit ConvIntegerKernels(std::shared_ptr<GpuDevice> device, Int8GemmOptions options = {},
                                 int maxCachedBindGroups = 1024);
     std::string Variant() const { return gemm_.Variant(); }
-    int BindGroupsCreated() const { return 0; }
+    int BindGroupsCreated() const { return blocks_.Created() + gemm_.BindGroupsCreated(); }
     static int64_t ScratchBytesPerImage(const ConvProblem &problem);
     // ConvIntegerKernels.cs:97-253.
     void Encode(GpuCommandEncoder &encoder, const ConvProblem &problem, const GpuBuffer &x, const GpuBuffer &w,
                 const GpuBuffer &y, const std::optional<Int8Operand> &xZeroPoint = std::nullopt,
                 const std::optional<Int8Operand> &wZeroPoint = std::nullopt,
                 const std::optional<GpuBuffer> &scratch = std::nullopt, int scratchOffset = 0);
-    void ReleaseBindings() {}
+    void ReleaseBindings()
+    {
+        blocks_.Release();
+        gemm_.ReleaseBindings();
+    }
     void Dispose();
     // This library's own: convolutions with one input channel a group run on the direct kernel (true, the default)
     // or through the column matrix and the products like the others (false; a test hook).
@@ -376,6 +405,7 @@ private:
     Int8Gemm gemm_;
     GpuBuffer own_u8_, own_i8_;
     std::vector<GpuBuffer> retired_;   // smaller columns buffers that recorded commands may still name
+    ArgumentBlocks blocks_;
 };
 
 // Where a gather records the position of an invalid index (GpuIndexStatus.cs:13-63): one uint32 on the device, reset to
@@ -405,12 +435,13 @@ public:
     void EncodeGather(GpuCommandEncoder &encoder, const GpuBuffer &data, int offsetData, const std::vector<int> &dataShape,
                       int axis, const GpuBuffer &indices, int offsetIndices, int indexCount, const GpuBuffer &output,
                       int offsetOutput, GpuIndexStatus *status = nullptr);
-    int BindGroupsCreated() const { return 0; }
-    void ReleaseBindings() {}
+    int BindGroupsCreated() const { return blocks_.Created(); }
+    void ReleaseBindings() { blocks_.Release(); }
     void Dispose() {}
 
 private:
     std::shared_ptr<GpuDevice> device_;
+    ArgumentBlocks blocks_;
 };
 
 // ------------------------------------------------------------------ shared checks (KernelSupport.cs:68-131)

@@ -113,6 +113,52 @@ def test_variants(d):
     assert og.Int8Gemm(d).BindGroupsCreated == 0
 
 
+def test_argument_blocks_follow_the_binding_cache_contract(d):
+    # BindingCacheTests.cs:141-197 on this backend's argument blocks: a family's first call with a buffer set adds
+    # blocks, the same call again adds none, and after ReleaseBindings the same call adds them again (the count is kept);
+    # a cache size below 1 is refused. Recording is enough: the count changes when work is recorded, not when it runs.
+    f, f2 = buf(d, og.ElementType.Float32, 4096), buf(d, og.ElementType.Float32, 4096)
+    u8, i8 = buf(d, og.ElementType.UInt8, 4096), buf(d, og.ElementType.Int8, 4096)
+    i32 = buf(d, og.ElementType.Int32, 4096)
+    zero = buf(d, og.ElementType.UInt8, 8)
+    int8, dq = og.Int8Gemm(d, None, 8), og.DynamicQuantizeKernels(d, 8)
+    dequantize, quantizer, gather = og.DequantizeKernels(d, 8), og.DequantizeKernels(d, 8), og.GatherKernels(d, 8)
+    conv = og.ConvIntegerKernels(d, None, 8)
+    families = [
+        ("int8 gemm", lambda e: int8.EncodeInt32(e, og.Int8GemmProblem(16, 16, 16), u8, i8, i32), int8),
+        ("dynamic quantize", lambda e: dq.Encode(e, f, 0, 1000, u8, 0, f2, 0, zero, 0), dq),
+        ("dequantize", lambda e: dequantize.Encode(e, u8, 0, [16, 16], 0, False, f, 0, None, 0, f2, 0), dequantize),
+        ("quantize", lambda e: quantizer.EncodeQuantize(e, f, 0, [16, 16], 0, False, f2, 0, None, 0, u8, 0), quantizer),
+        ("gather", lambda e: gather.EncodeGather(e, f, 0, [64, 8], 0, i32, 0, 20, f2, 0), gather),
+        ("conv", lambda e: conv.Encode(e, og.ConvProblem(1, 1, 8, 8, 4, 3, 3), u8, i8, i32), conv),
+    ]
+    for name, record, family in families:
+        record(d.BeginCommands())
+        first = family.BindGroupsCreated
+        record(d.BeginCommands())
+        second = family.BindGroupsCreated
+        family.ReleaseBindings()
+        record(d.BeginCommands())
+        third = family.BindGroupsCreated
+        assert first > 0 and second == first and third == 2 * first, (name, first, second, third)
+    # A new buffer set adds blocks; the cache keeps at most maxCachedBindGroups of them, the least recent dropped.
+    small = og.DequantizeKernels(d, 2)
+    outs = [buf(d, og.ElementType.Float32, 256) for _ in range(3)]
+    rec = lambda o: small.Encode(d.BeginCommands(), u8, 0, [256], 0, False, f, 0, None, 0, o, 0)  # noqa: E731
+    for o in outs:
+        rec(o)
+    assert small.BindGroupsCreated == 3
+    rec(outs[2])
+    rec(outs[1])
+    assert small.BindGroupsCreated == 3
+    rec(outs[0])   # dropped when the third set came in
+    assert small.BindGroupsCreated == 4
+    for make in (lambda: og.Int8Gemm(d, None, 0), lambda: og.DynamicQuantizeKernels(d, 0),
+                 lambda: og.DequantizeKernels(d, 0), lambda: og.GatherKernels(d, 0)):
+        with pytest.raises((IndexError, ValueError, OverflowError)):
+            make()
+
+
 def test_dynamic_quantize_bad_arguments(d):
     k = og.DynamicQuantizeKernels(d)
     x, y = buf(d, og.ElementType.Float32, 16), buf(d, og.ElementType.UInt8, 16)
