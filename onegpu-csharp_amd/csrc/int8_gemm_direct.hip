@@ -31,7 +31,7 @@ hipError_t launch_gemm_direct(const GemmArgs &g, hipStream_t s, const char **ker
     const dim3 grid((uint32_t)blocks);
     if (!large) launch_direct128(g, s, grid, tn, tm, 1, g.K);
     else if (g.flags & OG_GEMM_TRANSPOSE_B) launch_direct_nk256(g, s, grid, tn, tm);
-    else launch_direct_t<256, false>(g, s, grid, tn, tm, 1, g.K);
+    else launch_direct_t<256, false, 8>(g, s, grid, tn, tm, 1, g.K);
     return hipGetLastError();
 }
 

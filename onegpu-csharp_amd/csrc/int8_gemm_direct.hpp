@@ -2,14 +2,16 @@
 // no staging registers), and B stored K x N is read in its own layout with the gfx950 transpose read
 // ds_read_b64_tr_b8, so no VALU transposition is needed.
 //
-//  - Tile 256 x 256 per workgroup (large products) or 128 x 128 (medium ones), 64 deep per stage, 4 waves (2 x 2) of
-//    128 x 128 (4 x 4 blocks of v_mfma_i32_32x32x32_i8) or 64 x 64 (2 x 2 blocks), a ring of 5 stages filling the
-//    160 KB of LDS (half of it at 128, two workgroups a CU). K must be a multiple of 64 (other products take the
-//    register-staged kernel).
-//  - One wave per SIMD, so the wave's own instruction stream has to keep the matrix core busy. The 32 x 32 x 32 MFMA
-//    (32 cycles) does the work of two 16 x 16 x 64 ones with the same fragment reads, and leaves room for about
-//    seven other instructions: the DMA of a later stage (2 instructions a load), the fragment reads, one flip per
-//    unsigned fragment, and the operands' byte sums (v_sad_u8, which issues beside an MFMA where v_dot4 does not).
+//  - Tile 256 x 256 per workgroup (large products) or 128 x 128 (medium ones), 64 deep per stage, a ring of 5 stages
+//    filling the 160 KB of LDS (half of it at 128, two workgroups a CU). K must be a multiple of 64 (other products
+//    take the register-staged kernel). At 256, 8 waves (4 x 2) of 64 x 128 (2 x 4 blocks of v_mfma_i32_32x32x32_i8):
+//    two waves a SIMD, so while one waits (at the stage barrier, for a fragment read) the other keeps the matrix core
+//    busy; 128 accumulator registers a wave leave room for both in the SIMD's register file. At 128, 4 waves (2 x 2)
+//    of 64 x 64 (2 x 2 blocks), one a SIMD.
+//  - The 32 x 32 x 32 MFMA (32 cycles) does the work of two 16 x 16 x 64 ones with the same fragment reads, and leaves
+//    room for about seven other instructions: the DMA of a later stage (2 instructions a load), the fragment reads,
+//    one flip per unsigned fragment, and the operands' byte sums (v_sad_u8, which issues beside an MFMA where v_dot4
+//    does not).
 //  - Operands stay as stored in LDS; each MFMA fragment of an unsigned operand is moved to the signed domain
 //    (s = u ^ 0x80) after it is read, and the zero points are applied at the store from the byte sums:
 //        sum (s - z')(t - w') = sum s t - w' sum s - z' sum t + K z' w'   (mod 2^32; Int8GemmDot.hlsl:1-11 rearranges the same)
@@ -40,18 +42,22 @@ typedef uint32_t u4w __attribute__((ext_vector_type(4)));
 
 namespace {
 
-constexpr int DBK = 64, DTHREADS = 256;
+constexpr int DBK = 64;
 constexpr int NS = 5;                                   // stages in the ring
 
-// The shape of a BT x BT tile (BT = 256 or 128): 2 x 2 waves of WT x WT, each F x F blocks of 32 x 32; a stage of 64
-// k in NB blocks of 2 row blocks x F column blocks (HB blocks per 32-deep half).
-template <int BT>
+// The shape of a BT x BT tile (BT = 256 or 128) on WAVES waves (4: one a SIMD; 8: two a SIMD, at 256): WAVES / 2 x 2
+// waves of WTM x WTN, each FM x FN blocks of 32 x 32; a stage of 64 k in NB blocks of 2 row blocks x FN column blocks
+// (HB blocks per 32-deep half).
+template <int BT, int WAVES>
 struct DCfg {
+    static constexpr int THREADS = 64 * WAVES;
     static constexpr int A_STAGE = BT * DBK, B_STAGE = DBK * BT, STAGE = A_STAGE + B_STAGE;   // bytes
-    static constexpr int LOADS_A = A_STAGE / 16 / DTHREADS, LOADS_B = B_STAGE / 16 / DTHREADS;   // 16-byte loads a thread
+    static constexpr int LOADS_A = A_STAGE / 16 / THREADS, LOADS_B = B_STAGE / 16 / THREADS;   // 16-byte loads a thread
     static constexpr int LOADS = LOADS_A + LOADS_B;
-    static constexpr int WT = BT / 2, F = WT / 32, HB = F / 2, NB = 2 * HB, BPB = F / HB;
+    static constexpr int WTM = BT / (WAVES / 2), WTN = BT / 2, FM = WTM / 32, FN = WTN / 32;
+    static constexpr int HB = FM / 2, NB = 2 * HB, BPB = FN / HB;
     static_assert(BT == 256 || BT == 128, "tile");
+    static_assert(WAVES == 4 || (WAVES == 8 && BT == 256), "waves");
 };
 
 // Buffer resource words for `bytes` bytes at `base` (raw buffer: no stride, no swizzle; reads past the range
@@ -169,17 +175,18 @@ __device__ __forceinline__ void sched_block()
 
 // FLIP_A / FLIP_B: the operand is unsigned (moved to the signed domain fragment by fragment). SUM_A / SUM_B: the row
 // sums of A / column sums of B are needed (the other operand's zero point in the signed domain can be non-zero).
-template <int BT, bool TRANS_B, bool SUM_A, bool SUM_B, bool FLIP_A, bool FLIP_B>
+template <int BT, bool TRANS_B, bool SUM_A, bool SUM_B, bool FLIP_A, bool FLIP_B, int WAVES = 4>
 // ksplit > 1: the product is cut along K into slices of kslice bytes (a multiple of 64); g.batch counts batch entries
 // times slices, and slice kc of batch entry b computes the int32 sums of its k range with the zero points applied
 // (every correction term is linear in the slice) into batch entry b * ksplit + kc of C, which is then a dense int32
 // partial buffer (the caller adds the slices and applies the epilogue). ksplit = 1: the whole product.
-__global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t tiles_n, int32_t tiles_m, int32_t ksplit,
+__global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t tiles_n, int32_t tiles_m, int32_t ksplit,
                                                           int32_t kslice)
 {
-    using D = DCfg<BT>;
+    using D = DCfg<BT, WAVES>;
     constexpr int DBM = BT, DBN = BT, A_STAGE = D::A_STAGE, STAGE = D::STAGE, LOADS_A = D::LOADS_A;
-    constexpr int LOADS_B = D::LOADS_B, LOADS = D::LOADS, WT = D::WT, F = D::F, HB = D::HB, NB = D::NB, BPB = D::BPB;
+    constexpr int LOADS_B = D::LOADS_B, LOADS = D::LOADS, WTM = D::WTM, WTN = D::WTN, FM = D::FM, FN = D::FN;
+    constexpr int HB = D::HB, NB = D::NB, BPB = D::BPB;
     // The ring of NS stages, A (BT x 64) then B (64 x BT) each: all 160 KB of LDS at BT = 256, half at 128 (two
     // workgroups a CU). After the loop its start holds the epilogue's per-row and per-column arrays.
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
@@ -242,16 +249,16 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
     }
 
     // Per-thread global offsets of the chunks that land in this thread's LDS slots (the same at every stage): load i
-    // of a wave fills 1 KB at i * 4 KB + wave * 1 KB of the operand's tile.
+    // of a wave fills 1 KB at i * WAVES KB + wave * 1 KB of the operand's tile.
     uint32_t off_a[LOADS_A], off_b[LOADS_B];
 #pragma unroll
     for (int i = 0; i < LOADS_A; i++) {
-        const int s = (i * 4 + wave) * 64 + lane, r = s >> 2, p = s & 3;
+        const int s = (i * WAVES + wave) * 64 + lane, r = s >> 2, p = s & 3;
         off_a[i] = (uint32_t)r * (uint32_t)lda + 16u * (uint32_t)a_pos(r, p);
     }
 #pragma unroll
     for (int i = 0; i < LOADS_B; i++) {
-        const int s = (i * 4 + wave) * 64 + lane;
+        const int s = (i * WAVES + wave) * 64 + lane;
         if constexpr (TRANS_B) {
             const int r = s >> 2, p = s & 3;
             off_b[i] = (uint32_t)r * (uint32_t)ldb + 16u * (uint32_t)a_pos(r, p);
@@ -262,7 +269,7 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
     }
     const uint32_t wave_lds = lds_addr(smem) + (uint32_t)wave * 1024u;
 
-    // The DMA of the stage at depth k0 into ring buffer U: load I < 4 is A's, the rest B's. A k0 past K (the loads
+    // The DMA of the stage at depth k0 into ring buffer U: load I < LOADS_A is A's, the rest B's. A k0 past K (the loads
     // beyond the last stage) is clamped to K, which keeps the offsets in range; those loads are never used.
     struct StageRsrc {
         u4w a, b;
@@ -273,26 +280,26 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
     };
     auto dma = [&](auto u_tag, auto i_tag, const StageRsrc &rr) {
         constexpr int U = decltype(u_tag)::value, I = decltype(i_tag)::value;
-        if constexpr (I < LOADS_A) dma16<U * STAGE + I * 4096>(rr.a, wave_lds, off_a[I]);
-        else dma16<U * STAGE + A_STAGE + (I - LOADS_A) * 4096>(rr.b, wave_lds, off_b[I - LOADS_A]);
+        if constexpr (I < LOADS_A) dma16<U * STAGE + I * WAVES * 1024>(rr.a, wave_lds, off_a[I]);
+        else dma16<U * STAGE + A_STAGE + (I - LOADS_A) * WAVES * 1024>(rr.b, wave_lds, off_b[I - LOADS_A]);
     };
 
     // Fragments as stored (unsigned operands not yet flipped) from ring buffer u. A: row block i (32 rows) at k half
     // ks; lane l holds row 32 i + l % 32, k 32 ks + 16 (l / 32) .. + 15: one ds_read_b128.
     auto read_a = [&](int u, int i, int ks) {
-        const int r = wm * WT + 32 * i + i32;
+        const int r = wm * WTM + 32 * i + i32;
         return *reinterpret_cast<const v4i *>(smem + u * STAGE + r * 64 + 16 * a_pos(r, 2 * ks + h2));
     };
     // B: column block j (32 columns) at k half ks; lane l holds column 32 j + l % 32 and the same 16 k as A.
     auto read_b = [&](int u, int j, int ks) -> v4i {
         const uint8_t *bs = smem + u * STAGE + A_STAGE;
         if constexpr (TRANS_B) {
-            const int r = wn * WT + 32 * j + i32;
+            const int r = wn * WTN + 32 * j + i32;
             return *reinterpret_cast<const v4i *>(bs + r * 64 + 16 * a_pos(r, 2 * ks + h2));
         } else {
             // Each 16-lane group g transposes 16 columns (16 (g & 1) .. + 15 of the block) x 8 rows per read; groups
             // 2 and 3 take the second 16 k.
-            const int c = (wn * WT + 32 * j + 16 * (g4 & 1)) >> 4;   // 16-byte chunk of the group's columns
+            const int c = (wn * WTN + 32 * j + 16 * (g4 & 1)) >> 4;   // 16-byte chunk of the group's columns
             v2i h[2];
 #pragma unroll
             for (int hh = 0; hh < 2; hh++) {
@@ -303,21 +310,22 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
         }
     };
 
-    v16i acc[F][F];
+    v16i acc[FM][FN];
 #pragma unroll
-    for (int i = 0; i < F; i++)
+    for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int j = 0; j < F; j++)
+        for (int j = 0; j < FN; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
     // This lane's biased byte sums (its k half, 16 bytes per fragment) of the wave's A row blocks / B column blocks.
     // Biased bytes: an unsigned operand's bytes as stored, a signed one's with the top bit flipped.
-    uint32_t rs[F], cs[F];
+    uint32_t rs[FM], cs[FN];
 #pragma unroll
-    for (int i = 0; i < F; i++) { rs[i] = 0; cs[i] = 0; }
+    for (int i = 0; i < FM; i++) rs[i] = 0;
+#pragma unroll
+    for (int j = 0; j < FN; j++) cs[j] = 0;
     // VALU instructions per block beside the MFMAs: byte sums of two A and BPB B fragments, and the flips of the two
     // A and BPB B fragments read in the block.
-    constexpr int VS = (SUM_A ? (FLIP_A ? 8 : 16) : 0) + (SUM_B ? 8 * BPB : 0);
     constexpr int VF = (FLIP_A ? 8 : 0) + (FLIP_B ? 4 * BPB : 0);
     constexpr int DS = 2 + BPB * (TRANS_B ? 1 : 2);
 
@@ -330,9 +338,9 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
     });
     wait_vm_barrier<LOADS * (NS - 2)>();
     // B fragments in the signed domain, [k half][column block]; the current block's A fragments as stored and signed.
-    v4i bf[2][F], a_st[2], a_cur[2];
+    v4i bf[2][FN], a_st[2], a_cur[2];
 #pragma unroll
-    for (int j = 0; j < F; j++) bf[0][j] = to_signed<FLIP_B>(read_b(0, j, 0));
+    for (int j = 0; j < FN; j++) bf[0][j] = to_signed<FLIP_B>(read_b(0, j, 0));
 #pragma unroll
     for (int t = 0; t < 2; t++) {
         a_st[t] = read_a(0, t, 0);
@@ -340,15 +348,18 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
     }
 
     // One stage s in ring buffer U, in NB blocks of 2F MFMAs: block b multiplies A row blocks 2 (b % HB), + 1 at k
-    // half b / HB against the F B column blocks. Block b reads the A fragments of block b + 1 (the last block: the
+    // half b / HB against the FN B column blocks. Block b reads the A fragments of block b + 1 (the last block: the
     // first of stage s + 1) and BPB B fragments: the first half's blocks this stage's second k half, the second half's
     // the next stage's first (whose registers are free once the first half is done). At the first block of the second
     // half the waves wait for stage s + 1 (this wave's loads landed, then everyone's) and meet: from then on nobody
     // reads the buffer of stage s - 1, so the second half's blocks issue the loads of stage s + NS - 1 into it. Stages
     // past the last still wait and read (their loads cover empty or unused ranges and what is read is not used), so
     // every stage is the same.
-    auto run_stage = [&](auto u_tag, int32_t s) {
+    // SA / SB: this wave keeps the row / column byte sums (only the waves whose sums the epilogue reads do).
+    auto run_stage = [&](auto u_tag, int32_t s, auto sa_tag, auto sb_tag) {
         constexpr int U = decltype(u_tag)::value, DU = (U + NS - 1) % NS, NU = (U + 1) % NS;
+        constexpr bool SA = decltype(sa_tag)::value, SB = decltype(sb_tag)::value;
+        constexpr int VS = (SA ? (FLIP_A ? 8 : 16) : 0) + (SB ? 8 * BPB : 0);
         const StageRsrc rr = stage_rsrc((s + NS - 1) * DBK);
         static_for<0, NB>([&](auto b_tag) {
             constexpr int b = decltype(b_tag)::value, ks = b / HB, i0 = 2 * (b % HB);
@@ -364,39 +375,66 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
                     dma(std::integral_constant<int, DU>{}, std::integral_constant<int, LPB * (b - HB) + decltype(q_tag)::value>{}, rr);
                 });
             }
-            const v4i b0 = read_b(RU, rj, rks), b1 = read_b(RU, rj + 1, rks);
+            v4i bn[BPB];
+#pragma unroll
+            for (int q = 0; q < BPB; q++) bn[q] = read_b(RU, rj + q, rks);
             v4i a_nx[2];
             a_nx[0] = read_a(AU, 2 * (nb % HB), nb / HB);
             a_nx[1] = read_a(AU, 2 * (nb % HB) + 1, nb / HB);
-            if constexpr (SUM_A) {
+            if constexpr (SA) {
 #pragma unroll
                 for (int t = 0; t < 2; t++)
                     rs[i0 + t] = FLIP_A ? sad16(a_st[t], rs[i0 + t]) : sad16(a_cur[t] ^ (int32_t)0x80808080, rs[i0 + t]);
             }
-            if constexpr (SUM_B) {
-                cs[rj] = sad16(bf[ks][rj] ^ (int32_t)0x80808080, cs[rj]);
-                cs[rj + 1] = sad16(bf[ks][rj + 1] ^ (int32_t)0x80808080, cs[rj + 1]);
+            if constexpr (SB) {
+#pragma unroll
+                for (int q = 0; q < BPB; q++) cs[rj + q] = sad16(bf[ks][rj + q] ^ (int32_t)0x80808080, cs[rj + q]);
             }
 #pragma unroll
             for (int t = 0; t < 2; t++)
 #pragma unroll
-                for (int j = 0; j < F; j++) acc[i0 + t][j] = mfma32(a_cur[t], bf[ks][j], acc[i0 + t][j]);
-            bf[rks][rj] = to_signed<FLIP_B>(b0);
-            bf[rks][rj + 1] = to_signed<FLIP_B>(b1);
+                for (int j = 0; j < FN; j++) acc[i0 + t][j] = mfma32(a_cur[t], bf[ks][j], acc[i0 + t][j]);
+#pragma unroll
+            for (int q = 0; q < BPB; q++) bf[rks][rj + q] = to_signed<FLIP_B>(bn[q]);
 #pragma unroll
             for (int t = 0; t < 2; t++) {
                 a_st[t] = a_nx[t];
                 a_cur[t] = to_signed<FLIP_A>(a_nx[t]);
             }
-            sched_block<2 * F, VS, VF, DS>();
+            sched_block<2 * FN, VS, VF, DS>();
             __builtin_amdgcn_sched_barrier(0);
         });
     };
     static_assert(NS == 5, "the loop below is unrolled for 5 stages");
-    for (int32_t kt = 0; kt < nk; kt += NS) {
-        static_for<0, NS>([&](auto u_tag) {
-            if (kt + decltype(u_tag)::value < nk) run_stage(u_tag, kt + decltype(u_tag)::value);
-        });
+    auto main_loop = [&](auto sa_tag, auto sb_tag) {
+        for (int32_t kt = 0; kt < nk; kt += NS) {
+            static_for<0, NS>([&](auto u_tag) {
+                if (kt + decltype(u_tag)::value < nk) run_stage(u_tag, kt + decltype(u_tag)::value, sa_tag, sb_tag);
+            });
+        }
+    };
+    // The epilogue takes the row sums from the waves with wn = 0 and the column sums from those with wm = 0, so only
+    // they form them: the loop is instantiated per wave role (the choice is uniform across a wave) and the other waves
+    // spend neither the VALU work nor its energy, which counts in a loop the chip's power limit sets the pace of.
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    const bool sa_here = wn == 0, sb_here = wm == 0;
+    if constexpr (SUM_A && SUM_B) {
+        if (sa_here) {
+            if (sb_here) main_loop(T_{}, T_{});
+            else main_loop(T_{}, F_{});
+        } else {
+            if (sb_here) main_loop(F_{}, T_{});
+            else main_loop(F_{}, F_{});
+        }
+    } else if constexpr (SUM_A) {
+        if (sa_here) main_loop(T_{}, F_{});
+        else main_loop(F_{}, F_{});
+    } else if constexpr (SUM_B) {
+        if (sb_here) main_loop(F_{}, T_{});
+        else main_loop(F_{}, F_{});
+    } else {
+        main_loop(F_{}, F_{});
     }
     // Every DMA landed and every wave done with the stage buffers before the epilogue's arrays take their place.
     wait_vm<0>();
@@ -414,16 +452,16 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
     const uint32_t bias_total = 128u * (uint32_t)DBK * (uint32_t)nk;
     if (SUM_A && wn == 0) {
 #pragma unroll
-        for (int i = 0; i < F; i++) {
+        for (int i = 0; i < FM; i++) {
             const uint32_t v = rs[i] + (uint32_t)__shfl_xor((int32_t)rs[i], 32);
-            if (h2 == 0) RowSum[wm * WT + 32 * i + i32] = (int32_t)(v - bias_total);
+            if (h2 == 0) RowSum[wm * WTM + 32 * i + i32] = (int32_t)(v - bias_total);
         }
     }
     if (SUM_B && wm == 0) {
 #pragma unroll
-        for (int j = 0; j < F; j++) {
+        for (int j = 0; j < FN; j++) {
             const uint32_t v = cs[j] + (uint32_t)__shfl_xor((int32_t)cs[j], 32);
-            if (h2 == 0) ColSum[wn * WT + 32 * j + i32] = (int32_t)(v - bias_total);
+            if (h2 == 0) ColSum[wn * WTN + 32 * j + i32] = (int32_t)(v - bias_total);
         }
     }
     if (tid < BT) {
@@ -440,11 +478,11 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
     // MFMA 32 x 32 output layout: lane l holds column l % 32 and, in register r, row 8 (r / 4) + 4 (l / 32) + r % 4
     // of its block; one store writes two 128-byte row segments.
     const uint32_t Ku = (uint32_t)K;
-    uint32_t wz[F], ct[F], ib[F];
-    float sc[F], fb[F];
+    uint32_t wz[FN], ct[FN], ib[FN];
+    float sc[FN], fb[FN];
 #pragma unroll
-    for (int j = 0; j < F; j++) {
-        const int nl = wn * WT + 32 * j + i32;
+    for (int j = 0; j < FN; j++) {
+        const int nl = wn * WTN + 32 * j + i32;
         wz[j] = SUM_A ? (uint32_t)ColW[nl] : 0u;
         ct[j] = SUM_B ? (uint32_t)ColSum[nl] - Ku * wz[j] : 0u;
         ib[j] = (uint32_t)ColIB[nl];
@@ -454,12 +492,12 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
     // int32 and float32 results are 4-byte elements, requantized ones bytes; strideC counts elements either way.
     int32_t *const Cb = static_cast<int32_t *>(g.C) + bsplit * g.strideC;
     uint8_t *const Yb = static_cast<uint8_t *>(g.C) + bsplit * g.strideC;
-    const int32_t ncol0 = n0 + wn * WT + i32;
+    const int32_t ncol0 = n0 + wn * WTN + i32;
     const int32_t M = g.M, N = g.N, zp_y = g.zp_y;
     // MODE 0: int32 (+ bias); 1: float32, `opt` = float bias present; 2: requantized bytes, `opt` = uint8 output.
     auto store_all = [&](auto mode_tag, bool opt) {
         constexpr int MODE = decltype(mode_tag)::value;
-        if constexpr (BT == 128) {
+        if constexpr (BT == 128 && WAVES == 4) {
             // Staged through LDS: one store instruction per thread then writes four neighbouring columns (16 bytes, or
             // 4 bytes of a requantized row) where the accumulator layout gives it one column per lane, so a tile takes
             // a quarter of the store instructions, whose issue rate bounds this epilogue. Needs N % 4 == 0 and an
@@ -472,14 +510,14 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
                 static_assert(T_OFF >= (2 * DBM + 5 * DBN) * 4 && T_OFF + BT * LDT * 4 <= NS * STAGE, "staging space");
                 int32_t *const T = reinterpret_cast<int32_t *>(smem + T_OFF);
 #pragma unroll
-                for (int i = 0; i < F; i++)
+                for (int i = 0; i < FM; i++)
 #pragma unroll
                     for (int q = 0; q < 4; q++)
 #pragma unroll
                         for (int r = 0; r < 4; r++)
 #pragma unroll
-                            for (int j = 0; j < F; j++)
-                                T[(wm * WT + 32 * i + 8 * q + 4 * h2 + r) * LDT + wn * WT + 32 * j + i32] = acc[i][j][4 * q + r];
+                            for (int j = 0; j < FN; j++)
+                                T[(wm * WTM + 32 * i + 8 * q + 4 * h2 + r) * LDT + wn * WTN + 32 * j + i32] = acc[i][j][4 * q + r];
                 wait_lgkm_barrier();
                 // Thread t: columns 4 (t % 32) .. + 3 of the tile, rows t / 32 + 8 jj.
                 const int c4 = 4 * (tid & 31), r0 = tid >> 5;
@@ -527,10 +565,10 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
             }
         }
 #pragma unroll
-        for (int i = 0; i < F; i++) {
+        for (int i = 0; i < FM; i++) {
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                const int ml = wm * WT + 32 * i + 8 * q + 4 * h2;
+                const int ml = wm * WTM + 32 * i + 8 * q + 4 * h2;
                 const v4i ssv = SUM_A ? *reinterpret_cast<const v4i *>(&RowSum[ml]) : (v4i){0, 0, 0, 0};
                 const v4i zzv = SUM_B ? *reinterpret_cast<const v4i *>(&RowZ[ml]) : (v4i){0, 0, 0, 0};
 #pragma unroll
@@ -541,7 +579,7 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
                     uint8_t *const yrow = Yb + m * N;
                     const uint32_t ss = (uint32_t)ssv[r], zz = (uint32_t)zzv[r];
 #pragma unroll
-                    for (int j = 0; j < F; j++) {
+                    for (int j = 0; j < FN; j++) {
                         const int32_t n = ncol0 + 32 * j;
                         if (n >= N) continue;
                         const uint32_t v = (uint32_t)acc[i][j][4 * q + r] - wz[j] * ss - zz * ct[j] + ib[j];
@@ -570,12 +608,12 @@ __global__ __launch_bounds__(DTHREADS) void k_gemm_direct(GemmArgs g, int32_t ti
 }
 
 // One instantiation per operand signedness and needed byte sums (an unsigned operand always needs the other's sums).
-template <int BT, bool T, bool FA, bool FB>
+template <int BT, bool T, bool FA, bool FB, int WAVES>
 inline void launch_direct_flips(const GemmArgs &g, hipStream_t s, dim3 grid, int32_t tn, int32_t tm, int32_t ks,
                                 int32_t kslice, bool sa, bool sb)
 {
 #define OG_D(SA, SB) \
-    hipLaunchKernelGGL((k_gemm_direct<BT, T, SA, SB, FA, FB>), grid, dim3(DTHREADS), 0, s, g, tn, tm, ks, kslice)
+    hipLaunchKernelGGL((k_gemm_direct<BT, T, SA, SB, FA, FB, WAVES>), grid, dim3(64 * WAVES), 0, s, g, tn, tm, ks, kslice)
     if constexpr (FA && FB) {
         OG_D(true, true);
     } else if constexpr (FA) {
@@ -593,16 +631,16 @@ inline void launch_direct_flips(const GemmArgs &g, hipStream_t s, dim3 grid, int
 #undef OG_D
 }
 
-template <int BT, bool T>
+template <int BT, bool T, int WAVES = 4>
 inline void launch_direct_t(const GemmArgs &g, hipStream_t s, dim3 grid, int32_t tn, int32_t tm, int32_t ks,
                             int32_t kslice)
 {
     const bool fa = !(g.flags & OG_GEMM_A_INT8), fb = !(g.flags & OG_GEMM_B_INT8);
     const bool sa = (g.flags & OG_GEMM_ZB) || fb, sb = (g.flags & OG_GEMM_ZA) || fa;
-    if (fa && fb) launch_direct_flips<BT, T, true, true>(g, s, grid, tn, tm, ks, kslice, sa, sb);
-    else if (fa) launch_direct_flips<BT, T, true, false>(g, s, grid, tn, tm, ks, kslice, sa, sb);
-    else if (fb) launch_direct_flips<BT, T, false, true>(g, s, grid, tn, tm, ks, kslice, sa, sb);
-    else launch_direct_flips<BT, T, false, false>(g, s, grid, tn, tm, ks, kslice, sa, sb);
+    if (fa && fb) launch_direct_flips<BT, T, true, true, WAVES>(g, s, grid, tn, tm, ks, kslice, sa, sb);
+    else if (fa) launch_direct_flips<BT, T, true, false, WAVES>(g, s, grid, tn, tm, ks, kslice, sa, sb);
+    else if (fb) launch_direct_flips<BT, T, false, true, WAVES>(g, s, grid, tn, tm, ks, kslice, sa, sb);
+    else launch_direct_flips<BT, T, false, false, WAVES>(g, s, grid, tn, tm, ks, kslice, sa, sb);
 }
 
 // Instantiated in translation units of their own (compiled in parallel): B stored N x K at 256, both layouts at 128.

@@ -6,7 +6,7 @@ namespace og {
 
 void launch_direct_nk256(const GemmArgs &g, hipStream_t s, dim3 grid, int32_t tn, int32_t tm)
 {
-    launch_direct_t<256, true>(g, s, grid, tn, tm, 1, g.K);
+    launch_direct_t<256, true, 8>(g, s, grid, tn, tm, 1, g.K);
 }
 
 }  // namespace og

@@ -517,13 +517,25 @@ def test_scratch_semantics():
     need = og.Int8Gemm.ScratchElements(og.Int8GemmProblem(Large, N, K))
     assert need == Large * N
     scratch = d.CreateBufferOf(og.ElementType.Int32, need)
-    gemm = og.Int8Gemm(d)
-    for m in (Small, Large):
-        run(d, lambda e: gemm.EncodeRequantized(e, og.Int8GemmProblem(m, N, K), a, b, y, mult, 3, scratch=og.Int8Scratch(scratch)))
-    assert gemm.BindGroupsCreated == 0
-    gemm.ReserveScratch(need)
-    run(d, lambda e: gemm.EncodeRequantized(e, og.Int8GemmProblem(Large, N, K), a, b, y, mult, 3))
-    assert y.Read()[:Large * N].tolist() == [3] * (Large * N)   # B = 0: every sum is 0, so y = zeroPointY
+
+    def pair(gemm, given):
+        # The argument blocks the larger product adds after the smaller one (Int8ScratchTests.Pair).
+        run(d, lambda e: gemm.EncodeRequantized(e, og.Int8GemmProblem(Small, N, K), a, b, y, mult, 3, scratch=given))
+        first = gemm.BindGroupsCreated
+        run(d, lambda e: gemm.EncodeRequantized(e, og.Int8GemmProblem(Large, N, K), a, b, y, mult, 3, scratch=given))
+        return gemm.BindGroupsCreated - first
+
+    for fused in (True, False):
+        opts = og.Int8GemmOptions(FusedRequantize=fused)
+        # The caller's scratch, sized once for the largest product: nothing new for the larger one.
+        assert pair(og.Int8Gemm(d, opts), og.Int8Scratch(scratch)) == 0
+        # Reserving the instance's own scratch up front does the same.
+        gemm = og.Int8Gemm(d, opts)
+        gemm.ReserveScratch(need)
+        assert pair(gemm, None) == 0
+        assert y.Read()[:Large * N].tolist() == [3] * (Large * N)   # B = 0: every sum is 0, so y = zeroPointY
+        # Without either, the two-pass form's sums buffer grows and the larger product needs a new block.
+        assert pair(og.Int8Gemm(d, opts), None) >= 0
     small = d.CreateBufferOf(og.ElementType.Int32, 100)
     with pytest.raises(og.GpuKernelShapeException) as ex:
         gemm.EncodeRequantized(d.BeginCommands(), og.Int8GemmProblem(64, 64, 8), a, b, y, mult, 0, scratch=og.Int8Scratch(small))
