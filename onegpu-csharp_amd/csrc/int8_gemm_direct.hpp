@@ -4,10 +4,10 @@
 //
 //  - Tile 256 x 256 per workgroup (large products) or 128 x 128 (medium ones), 64 deep per stage, a ring of 5 stages
 //    filling the 160 KB of LDS (half of it at 128, two workgroups a CU). K must be a multiple of 64 (other products
-//    take the register-staged kernel). At 256, 8 waves (4 x 2) of 64 x 128 (2 x 4 blocks of v_mfma_i32_32x32x32_i8):
-//    two waves a SIMD, so while one waits (at the stage barrier, for a fragment read) the other keeps the matrix core
-//    busy; 128 accumulator registers a wave leave room for both in the SIMD's register file. At 128, 4 waves (2 x 2)
-//    of 64 x 64 (2 x 2 blocks), one a SIMD.
+//    take the register-staged kernel). 8 waves, two a SIMD, so while one waits (at the stage barrier, for a fragment
+//    read) the other keeps the matrix core busy: at 256, 4 x 2 waves of 64 x 128 (2 x 4 blocks of
+//    v_mfma_i32_32x32x32_i8; 128 accumulator registers a wave leave room for both in the SIMD's register file), at
+//    128, 2 x 4 waves of 64 x 32 (2 x 1 blocks). A 4-wave form (2 x 2 waves, one a SIMD) is kept in the template.
 //  - The 32 x 32 x 32 MFMA (32 cycles) does the work of two 16 x 16 x 64 ones with the same fragment reads, and leaves
 //    room for about seven other instructions: the DMA of a later stage (2 instructions a load), the fragment reads,
 //    one flip per unsigned fragment, and the operands' byte sums (v_sad_u8, which issues beside an MFMA where v_dot4
@@ -45,19 +45,21 @@ namespace {
 constexpr int DBK = 64;
 constexpr int NS = 5;                                   // stages in the ring
 
-// The shape of a BT x BT tile (BT = 256 or 128) on WAVES waves (4: one a SIMD; 8: two a SIMD, at 256): WAVES / 2 x 2
-// waves of WTM x WTN, each FM x FN blocks of 32 x 32; a stage of 64 k in NB blocks of 2 row blocks x FN column blocks
-// (HB blocks per 32-deep half).
+// The shape of a BT x BT tile (BT = 256 or 128) on WAVES waves (4: one a SIMD; 8: two a SIMD): WGM x WGN waves of
+// WTM x WTN (4 x 2 at 256 on 8 waves, 2 x 4 at 128 on 8 waves, else 2 x 2), each FM x FN blocks of 32 x 32; a stage of
+// 64 k in NB blocks of 2 row blocks x FN column blocks (HB blocks per 32-deep half).
 template <int BT, int WAVES>
 struct DCfg {
     static constexpr int THREADS = 64 * WAVES;
     static constexpr int A_STAGE = BT * DBK, B_STAGE = DBK * BT, STAGE = A_STAGE + B_STAGE;   // bytes
     static constexpr int LOADS_A = A_STAGE / 16 / THREADS, LOADS_B = B_STAGE / 16 / THREADS;   // 16-byte loads a thread
     static constexpr int LOADS = LOADS_A + LOADS_B;
-    static constexpr int WTM = BT / (WAVES / 2), WTN = BT / 2, FM = WTM / 32, FN = WTN / 32;
+    static constexpr int WGN = (WAVES == 8 && BT == 128) ? 4 : 2, WGM = WAVES / WGN;
+    static constexpr int WTM = BT / WGM, WTN = BT / WGN, FM = WTM / 32, FN = WTN / 32;
     static constexpr int HB = FM / 2, NB = 2 * HB, BPB = FN / HB;
     static_assert(BT == 256 || BT == 128, "tile");
-    static_assert(WAVES == 4 || (WAVES == 8 && BT == 256), "waves");
+    static_assert(WAVES == 4 || WAVES == 8, "waves");
+    static_assert(FM >= 2 && FN >= 1 && LOADS_A >= 1 && LOADS_B >= 1, "shape");
 };
 
 // Buffer resource words for `bytes` bytes at `base` (raw buffer: no stride, no swizzle; reads past the range
@@ -156,21 +158,6 @@ __device__ __forceinline__ void static_for(F &&f)
     }
 }
 
-// Scheduling pattern of one block of NM MFMAs: its DS reads first, then each MFMA followed by its share of the VALU
-// work (the byte sums VS over the first NM - 2, the flips VF, which wait for a read, over the last two).
-template <int NM, int VS, int VF, int DS>
-__device__ __forceinline__ void sched_block()
-{
-    constexpr int NS1 = NM - 2;
-    __builtin_amdgcn_sched_group_barrier(0x100, DS, 0);
-    static_for<0, NM>([](auto m_tag) {
-        constexpr int m = decltype(m_tag)::value;
-        constexpr int v = m < NS1 ? (VS * (m + 1) / NS1 - VS * m / NS1) : (VF * (m - NS1 + 1) / 2 - VF * (m - NS1) / 2);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x002, v, 0);
-    });
-}
-
 }  // namespace
 
 // FLIP_A / FLIP_B: the operand is unsigned (moved to the signed domain fragment by fragment). SUM_A / SUM_B: the row
@@ -186,7 +173,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
     using D = DCfg<BT, WAVES>;
     constexpr int DBM = BT, DBN = BT, A_STAGE = D::A_STAGE, STAGE = D::STAGE, LOADS_A = D::LOADS_A;
     constexpr int LOADS_B = D::LOADS_B, LOADS = D::LOADS, WTM = D::WTM, WTN = D::WTN, FM = D::FM, FN = D::FN;
-    constexpr int HB = D::HB, NB = D::NB, BPB = D::BPB;
+    constexpr int HB = D::HB, NB = D::NB, BPB = D::BPB, WGN = D::WGN, THREADS = D::THREADS;
     // The ring of NS stages, A (BT x 64) then B (64 x BT) each: all 160 KB of LDS at BT = 256, half at 128 (two
     // workgroups a CU). After the loop its start holds the epilogue's per-row and per-column arrays.
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
@@ -194,7 +181,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int i32 = lane & 31, h2 = lane >> 5;   // MFMA roles: row / column within a 32-block, k half
     const int i16 = lane & 15, g4 = lane >> 4;   // transpose-read roles
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WGN, wn = wave % WGN;
 
     // Tile order: the hardware deals workgroups round-robin to the 8 XCDs; remap so that each XCD gets one contiguous
     // run of tiles, walked in groups of 8 row tiles, and the A and B tiles the run reuses stay in its L2.
@@ -324,11 +311,6 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
     for (int i = 0; i < FM; i++) rs[i] = 0;
 #pragma unroll
     for (int j = 0; j < FN; j++) cs[j] = 0;
-    // VALU instructions per block beside the MFMAs: byte sums of two A and BPB B fragments, and the flips of the two
-    // A and BPB B fragments read in the block.
-    constexpr int VF = (FLIP_A ? 8 : 0) + (FLIP_B ? 4 * BPB : 0);
-    constexpr int DS = 2 + BPB * (TRANS_B ? 1 : 2);
-
     const int32_t nk = K / DBK;   // K is a multiple of DBK here
 
     // Prologue: stages 0 .. NS - 2 in flight; stage 0 landed, its first k half of B and the first block's A read.
@@ -359,7 +341,6 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
     auto run_stage = [&](auto u_tag, int32_t s, auto sa_tag, auto sb_tag) {
         constexpr int U = decltype(u_tag)::value, DU = (U + NS - 1) % NS, NU = (U + 1) % NS;
         constexpr bool SA = decltype(sa_tag)::value, SB = decltype(sb_tag)::value;
-        constexpr int VS = (SA ? (FLIP_A ? 8 : 16) : 0) + (SB ? 8 * BPB : 0);
         const StageRsrc rr = stage_rsrc((s + NS - 1) * DBK);
         static_for<0, NB>([&](auto b_tag) {
             constexpr int b = decltype(b_tag)::value, ks = b / HB, i0 = 2 * (b % HB);
@@ -401,7 +382,8 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
                 a_st[t] = a_nx[t];
                 a_cur[t] = to_signed<FLIP_A>(a_nx[t]);
             }
-            sched_block<2 * FN, VS, VF, DS>();
+            // Blocks stay in order; within one the compiler interleaves freely (with two waves a SIMD the other wave
+            // fills what one wave's order leaves idle; a fixed MFMA / VALU interleave measured slower).
             __builtin_amdgcn_sched_barrier(0);
         });
     };
@@ -497,7 +479,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
     // MODE 0: int32 (+ bias); 1: float32, `opt` = float bias present; 2: requantized bytes, `opt` = uint8 output.
     auto store_all = [&](auto mode_tag, bool opt) {
         constexpr int MODE = decltype(mode_tag)::value;
-        if constexpr (BT == 128 && WAVES == 4) {
+        if constexpr (BT == 128) {
             // Staged through LDS: one store instruction per thread then writes four neighbouring columns (16 bytes, or
             // 4 bytes of a requantized row) where the accumulator layout gives it one column per lane, so a tile takes
             // a quarter of the store instructions, whose issue rate bounds this epilogue. Needs N % 4 == 0 and an
@@ -519,7 +501,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
                             for (int j = 0; j < FN; j++)
                                 T[(wm * WTM + 32 * i + 8 * q + 4 * h2 + r) * LDT + wn * WTN + 32 * j + i32] = acc[i][j][4 * q + r];
                 wait_lgkm_barrier();
-                // Thread t: columns 4 (t % 32) .. + 3 of the tile, rows t / 32 + 8 jj.
+                // Thread t: columns 4 (t % 32) .. + 3 of the tile, rows t / 32 + (THREADS / 32) jj.
                 const int c4 = 4 * (tid & 31), r0 = tid >> 5;
                 uint32_t wz4[4], ct4[4], ib4[4];
                 float sc4[4], fb4[4];
@@ -533,8 +515,8 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
                 }
                 const int32_t n = n0 + c4;
 #pragma unroll 4
-                for (int jj = 0; jj < BT / 8; jj++) {
-                    const int rl = r0 + 8 * jj;
+                for (int jj = 0; jj < BT / (THREADS / 32); jj++) {
+                    const int rl = r0 + (THREADS / 32) * jj;
                     const int32_t m = m0 + rl;
                     if (m >= M || n >= N) continue;   // N % 4 == 0: the four columns are all in or all out
                     const v4i raw = *reinterpret_cast<const v4i *>(&T[rl * LDT + c4]);
