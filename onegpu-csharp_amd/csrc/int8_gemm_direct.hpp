@@ -7,7 +7,8 @@
 //    take the register-staged kernel). 8 waves, two a SIMD, so while one waits (at the stage barrier, for a fragment
 //    read) the other keeps the matrix core busy: at 256, 4 x 2 waves of 64 x 128 (2 x 4 blocks of
 //    v_mfma_i32_32x32x32_i8; 128 accumulator registers a wave leave room for both in the SIMD's register file), at
-//    128, 2 x 4 waves of 64 x 32 (2 x 1 blocks). A 4-wave form (2 x 2 waves, one a SIMD) is kept in the template.
+//    128, 2 x 4 waves of 64 x 32 (2 x 1 blocks). A 256 tile that needs both operands' byte sums runs on 4 waves
+//    (2 x 2 of 128 x 128, one a SIMD, accumulators in AGPRs): on 8 its registers would spill.
 //  - The 32 x 32 x 32 MFMA (32 cycles) does the work of two 16 x 16 x 64 ones with the same fragment reads, and leaves
 //    room for about seven other instructions: the DMA of a later stage (2 instructions a load), the fragment reads,
 //    one flip per unsigned fragment, and the operands' byte sums (v_sad_u8, which issues beside an MFMA where v_dot4
@@ -173,7 +174,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
     using D = DCfg<BT, WAVES>;
     constexpr int DBM = BT, DBN = BT, A_STAGE = D::A_STAGE, STAGE = D::STAGE, LOADS_A = D::LOADS_A;
     constexpr int LOADS_B = D::LOADS_B, LOADS = D::LOADS, WTM = D::WTM, WTN = D::WTN, FM = D::FM, FN = D::FN;
-    constexpr int HB = D::HB, NB = D::NB, BPB = D::BPB, WGN = D::WGN, THREADS = D::THREADS;
+    constexpr int HB = D::HB, NB = D::NB, BPB = D::BPB, WGM = D::WGM, WGN = D::WGN, THREADS = D::THREADS;
     // The ring of NS stages, A (BT x 64) then B (64 x BT) each: all 160 KB of LDS at BT = 256, half at 128 (two
     // workgroups a CU). After the loop its start holds the epilogue's per-row and per-column arrays.
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
@@ -337,10 +338,12 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
     // reads the buffer of stage s - 1, so the second half's blocks issue the loads of stage s + NS - 1 into it. Stages
     // past the last still wait and read (their loads cover empty or unused ranges and what is read is not used), so
     // every stage is the same.
-    // SA / SB: this wave keeps the row / column byte sums (only the waves whose sums the epilogue reads do).
+    // SAR / SBR: the row / column byte sums this wave forms: those of its row blocks i with i % WGN == SAR and of its
+    // column blocks j with j % WGM == SBR (-1: none). So each row block's sums come from one wave of its row of waves
+    // and each column block's from one wave of its column, spread evenly, and no wave repeats another's.
     auto run_stage = [&](auto u_tag, int32_t s, auto sa_tag, auto sb_tag) {
         constexpr int U = decltype(u_tag)::value, DU = (U + NS - 1) % NS, NU = (U + 1) % NS;
-        constexpr bool SA = decltype(sa_tag)::value, SB = decltype(sb_tag)::value;
+        constexpr int SAR = decltype(sa_tag)::value, SBR = decltype(sb_tag)::value;
         const StageRsrc rr = stage_rsrc((s + NS - 1) * DBK);
         static_for<0, NB>([&](auto b_tag) {
             constexpr int b = decltype(b_tag)::value, ks = b / HB, i0 = 2 * (b % HB);
@@ -362,15 +365,16 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
             v4i a_nx[2];
             a_nx[0] = read_a(AU, 2 * (nb % HB), nb / HB);
             a_nx[1] = read_a(AU, 2 * (nb % HB) + 1, nb / HB);
-            if constexpr (SA) {
-#pragma unroll
-                for (int t = 0; t < 2; t++)
+            static_for<0, 2>([&](auto t_tag) {
+                constexpr int t = decltype(t_tag)::value;
+                if constexpr (SAR >= 0 && (i0 + t) % WGN == SAR)
                     rs[i0 + t] = FLIP_A ? sad16(a_st[t], rs[i0 + t]) : sad16(a_cur[t] ^ (int32_t)0x80808080, rs[i0 + t]);
-            }
-            if constexpr (SB) {
-#pragma unroll
-                for (int q = 0; q < BPB; q++) cs[rj + q] = sad16(bf[ks][rj + q] ^ (int32_t)0x80808080, cs[rj + q]);
-            }
+            });
+            static_for<0, BPB>([&](auto q_tag) {
+                constexpr int q = decltype(q_tag)::value;
+                if constexpr (SBR >= 0 && (rj + q) % WGM == SBR)
+                    cs[rj + q] = sad16(bf[ks][rj + q] ^ (int32_t)0x80808080, cs[rj + q]);
+            });
 #pragma unroll
             for (int t = 0; t < 2; t++)
 #pragma unroll
@@ -395,28 +399,23 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
             });
         }
     };
-    // The epilogue takes the row sums from the waves with wn = 0 and the column sums from those with wm = 0, so only
-    // they form them: the loop is instantiated per wave role (the choice is uniform across a wave) and the other waves
-    // spend neither the VALU work nor its energy, which counts in a loop the chip's power limit sets the pace of.
-    using T_ = std::true_type;
-    using F_ = std::false_type;
-    const bool sa_here = wn == 0, sb_here = wm == 0;
-    if constexpr (SUM_A && SUM_B) {
-        if (sa_here) {
-            if (sb_here) main_loop(T_{}, T_{});
-            else main_loop(T_{}, F_{});
+    // The loop is instantiated per wave role (wm, wn are uniform across a wave), so each wave carries only its own share
+    // of the byte sums: no wave waits at the stage barrier for another's extra VALU work, and none is spent twice.
+    auto with_roles = [&](auto sa_tag) {
+        if constexpr (SUM_B) {
+            static_for<0, D::WGM>([&](auto r_tag) {
+                if (wm == decltype(r_tag)::value) main_loop(sa_tag, r_tag);
+            });
         } else {
-            if (sb_here) main_loop(F_{}, T_{});
-            else main_loop(F_{}, F_{});
+            main_loop(sa_tag, std::integral_constant<int, -1>{});
         }
-    } else if constexpr (SUM_A) {
-        if (sa_here) main_loop(T_{}, F_{});
-        else main_loop(F_{}, F_{});
-    } else if constexpr (SUM_B) {
-        if (sb_here) main_loop(F_{}, T_{});
-        else main_loop(F_{}, F_{});
+    };
+    if constexpr (SUM_A) {
+        static_for<0, D::WGN>([&](auto r_tag) {
+            if (wn == decltype(r_tag)::value) with_roles(r_tag);
+        });
     } else {
-        main_loop(F_{}, F_{});
+        with_roles(std::integral_constant<int, -1>{});
     }
     // Every DMA landed and every wave done with the stage buffers before the epilogue's arrays take their place.
     wait_vm<0>();
@@ -432,16 +431,18 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
     // Byte sums: the two k halves of a row / column sit in lanes l and l + 32. The biased sums cover 64 bytes per
     // stage; the signed sums are 128 less per byte (mod 2^32).
     const uint32_t bias_total = 128u * (uint32_t)DBK * (uint32_t)nk;
-    if (SUM_A && wn == 0) {
+    if (SUM_A) {
 #pragma unroll
         for (int i = 0; i < FM; i++) {
+            if (i % WGN != wn) continue;   // another wave of this row of waves formed these
             const uint32_t v = rs[i] + (uint32_t)__shfl_xor((int32_t)rs[i], 32);
             if (h2 == 0) RowSum[wm * WTM + 32 * i + i32] = (int32_t)(v - bias_total);
         }
     }
-    if (SUM_B && wm == 0) {
+    if (SUM_B) {
 #pragma unroll
         for (int j = 0; j < FN; j++) {
+            if (j % WGM != wm) continue;   // another wave of this column of waves formed these
             const uint32_t v = cs[j] + (uint32_t)__shfl_xor((int32_t)cs[j], 32);
             if (h2 == 0) ColSum[wn * WTN + 32 * j + i32] = (int32_t)(v - bias_total);
         }
@@ -589,13 +590,22 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
     }
 }
 
+// The waves a 256 tile runs on: 8 (two a SIMD) when a wave's registers fit in half the SIMD's file; a product that
+// needs both operands' byte sums does not fit (the compiler spills inside the loop), so it keeps 4.
+template <int BT, bool SA, bool SB, int WAVES>
+constexpr int direct_waves()
+{
+    return (BT == 256 && SA && SB) ? 4 : WAVES;
+}
+
 // One instantiation per operand signedness and needed byte sums (an unsigned operand always needs the other's sums).
 template <int BT, bool T, bool FA, bool FB, int WAVES>
 inline void launch_direct_flips(const GemmArgs &g, hipStream_t s, dim3 grid, int32_t tn, int32_t tm, int32_t ks,
                                 int32_t kslice, bool sa, bool sb)
 {
 #define OG_D(SA, SB) \
-    hipLaunchKernelGGL((k_gemm_direct<BT, T, SA, SB, FA, FB, WAVES>), grid, dim3(64 * WAVES), 0, s, g, tn, tm, ks, kslice)
+    hipLaunchKernelGGL((k_gemm_direct<BT, T, SA, SB, FA, FB, direct_waves<BT, SA, SB, WAVES>()>), grid, \
+                       dim3(64 * direct_waves<BT, SA, SB, WAVES>()), 0, s, g, tn, tm, ks, kslice)
     if constexpr (FA && FB) {
         OG_D(true, true);
     } else if constexpr (FA) {
