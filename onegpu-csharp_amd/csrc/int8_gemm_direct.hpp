@@ -149,6 +149,15 @@ __device__ __forceinline__ uint32_t sad16(v4i v, uint32_t acc)
     return __builtin_amdgcn_sad_u8((uint32_t)v.w, 0u, acc);
 }
 
+// a * b mod 2^32 for the epilogue's corrections (a zero point times a byte sum): with SMALL both are under 2^23 in
+// magnitude, so the 24-bit multiply (full rate) gives the exact product; otherwise the 32-bit one (quarter rate).
+template <bool SMALL>
+__device__ __forceinline__ uint32_t zmul(uint32_t a, uint32_t b)
+{
+    if constexpr (SMALL) return (uint32_t)__mul24((int32_t)a, (int32_t)b);
+    else return a * b;
+}
+
 // Calls f(integral_constant<I>) for I = B .. E - 1.
 template <int B, int E, typename F>
 __device__ __forceinline__ void static_for(F &&f)
@@ -461,6 +470,9 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
     // MFMA 32 x 32 output layout: lane l holds column l % 32 and, in register r, row 8 (r / 4) + 4 (l / 32) + r % 4
     // of its block; one store writes two 128-byte row segments.
     const uint32_t Ku = (uint32_t)K;
+    // Below 2^15 k a byte sum (and a column sum less K times a zero point) stays under 2^23 in magnitude, so the
+    // correction products fit the full-rate 24-bit multiply exactly.
+    const bool small_k = K < 32768;
     uint32_t wz[FN], ct[FN], ib[FN];
     float sc[FN], fb[FN];
 #pragma unroll
@@ -524,7 +536,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
                     const uint32_t ss = SUM_A ? (uint32_t)RowSum[rl] : 0u, zz = SUM_B ? (uint32_t)RowZ[rl] : 0u;
                     uint32_t v[4];
 #pragma unroll
-                    for (int e = 0; e < 4; e++) v[e] = (uint32_t)raw[e] - wz4[e] * ss - zz * ct4[e] + ib4[e];
+                    for (int e = 0; e < 4; e++) v[e] = (uint32_t)raw[e] - wz4[e] * ss - zz * ct4[e] + ib4[e];   // once a 16 bytes
                     const int64_t at = (int64_t)m * N + n;
                     if constexpr (MODE == 1) {
                         float f[4];
@@ -547,37 +559,50 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
                 return;
             }
         }
+        // WHOLE: every row and column of the tile is in range (all tiles but the last row and column of tiles), so
+        // no store needs a bounds check: a lane's row address once per row, its column blocks at immediate offsets.
+        auto store_rows = [&](auto whole_tag, auto small_tag) {
+            constexpr bool WHOLE = decltype(whole_tag)::value, SMALL = decltype(small_tag)::value;
 #pragma unroll
-        for (int i = 0; i < FM; i++) {
+            for (int i = 0; i < FM; i++) {
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int ml = wm * WTM + 32 * i + 8 * q + 4 * h2;
-                const v4i ssv = SUM_A ? *reinterpret_cast<const v4i *>(&RowSum[ml]) : (v4i){0, 0, 0, 0};
-                const v4i zzv = SUM_B ? *reinterpret_cast<const v4i *>(&RowZ[ml]) : (v4i){0, 0, 0, 0};
+                for (int q = 0; q < 4; q++) {
+                    const int ml = wm * WTM + 32 * i + 8 * q + 4 * h2;
+                    const v4i ssv = SUM_A ? *reinterpret_cast<const v4i *>(&RowSum[ml]) : (v4i){0, 0, 0, 0};
+                    const v4i zzv = SUM_B ? *reinterpret_cast<const v4i *>(&RowZ[ml]) : (v4i){0, 0, 0, 0};
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int32_t m = m0 + ml + r;
-                    if (m >= M) continue;
-                    int32_t *const row = Cb + m * N;   // batch * M * N < 2^31 (checked at the boundary)
-                    uint8_t *const yrow = Yb + m * N;
-                    const uint32_t ss = (uint32_t)ssv[r], zz = (uint32_t)zzv[r];
+                    for (int r = 0; r < 4; r++) {
+                        const int32_t m = m0 + ml + r;
+                        if (!WHOLE && m >= M) continue;
+                        int32_t *const row = Cb + m * N + ncol0;   // batch * M * N < 2^31 (checked at the boundary)
+                        uint8_t *const yrow = Yb + m * N + ncol0;
+                        const uint32_t ss = (uint32_t)ssv[r], zz = (uint32_t)zzv[r];
 #pragma unroll
-                    for (int j = 0; j < FN; j++) {
-                        const int32_t n = ncol0 + 32 * j;
-                        if (n >= N) continue;
-                        const uint32_t v = (uint32_t)acc[i][j][4 * q + r] - wz[j] * ss - zz * ct[j] + ib[j];
-                        if constexpr (MODE == 1) {
-                            float f = __fmul_rn((float)(int32_t)v, sc[j]);
-                            if (opt) f = __fadd_rn(f, fb[j]);
-                            row[n] = __float_as_int(f);
-                        } else if constexpr (MODE == 2) {
-                            yrow[n] = (uint8_t)requantize_byte(v, sc[j], zp_y, opt);
-                        } else {
-                            row[n] = (int32_t)v;
+                        for (int j = 0; j < FN; j++) {
+                            if (!WHOLE && ncol0 + 32 * j >= N) continue;
+                            const uint32_t v = (uint32_t)acc[i][j][4 * q + r] - zmul<SMALL>(wz[j], ss) -
+                                               zmul<SMALL>(zz, ct[j]) + ib[j];
+                            if constexpr (MODE == 1) {
+                                float f = __fmul_rn((float)(int32_t)v, sc[j]);
+                                if (opt) f = __fadd_rn(f, fb[j]);
+                                row[32 * j] = __float_as_int(f);
+                            } else if constexpr (MODE == 2) {
+                                yrow[32 * j] = (uint8_t)requantize_byte(v, sc[j], zp_y, opt);
+                            } else {
+                                row[32 * j] = (int32_t)v;
+                            }
                         }
                     }
                 }
             }
+        };
+        const bool whole = m0 + DBM <= M && n0 + DBN <= N;
+        if (whole) {
+            if (small_k) store_rows(std::true_type{}, std::true_type{});
+            else store_rows(std::true_type{}, std::false_type{});
+        } else {
+            if (small_k) store_rows(std::false_type{}, std::true_type{});
+            else store_rows(std::false_type{}, std::false_type{});
         }
     };
     if (epi & EPI_REQUANT) {
