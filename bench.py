@@ -501,6 +501,16 @@ def traffic_of(kernel, workload):
     return None if e is None else e.get("hbm_bytes_per_launch")
 
 
+def clock_of(kernel, workload):
+    """The clock the chip held and the MFMA-busy fraction for `kernel` on `workload`, from profiles/clock.json
+    (rocprofv3 GRBM_GUI_ACTIVE and SQ_VALU_MFMA_BUSY_CYCLES per dispatch), or None when not measured."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "clock.json")) as f:
+            return json.load(f).get("kernels", {}).get(f"{kernel} {workload}")
+    except (OSError, ValueError):
+        return None
+
+
 def copy_workload(d, steps, warmup, mib=256):
     """A device-to-device copy of a known size (the counters' calibration for the traffic figures)."""
     n = mib << 20
@@ -814,6 +824,14 @@ def main():
             "note": "int8 ops (a multiply-add counts 2), 2*M*N*K per launch over the average launch duration (one HIP "
                     "event pair on the library's stream around the back-to-back timed launches, / steps); unit is "
                     "tera-ops/s"}
+    clk = clock_of(c4["kernel"], "c4")
+    if clk:
+        # The nominal peak assumes 2.4 GHz; on random int8 operands the chip's power limit holds a lower clock
+        # (measured with rocprofv3 on the same kernel and workload), and the peak at that clock is the reachable one.
+        peak_adj = PEAK_INT8_TOPS * clk["held_clock_ghz"] / 2.4
+        roof["clock_adjusted"] = {"held_clock_ghz": round(clk["held_clock_ghz"], 3), "peak": round(peak_adj, 1),
+                                  "frac": kern_tops / peak_adj, "mfma_busy_profiled": round(clk["mfma_busy"], 3),
+                                  "source": "profiles/clock.json (GRBM_GUI_ACTIVE / duration; MfmaUtil)"}
     cpu = None if args.no_cpu else cpu_baseline_c4(c4["host_operands"])
     g1 = gemv.get(1)
     line = {
