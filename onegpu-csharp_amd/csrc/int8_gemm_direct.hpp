@@ -323,12 +323,17 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
     for (int j = 0; j < FN; j++) cs[j] = 0;
     const int32_t nk = K / DBK;   // K is a multiple of DBK here
 
-    // Prologue: stages 0 .. NS - 2 in flight; stage 0 landed, its first k half of B and the first block's A read.
-    static_for<0, NS - 1>([&](auto u_tag) {
+    // How far ahead the DMA runs. With one block a k half (HB = 1) a stage's buffer is read only in its first block,
+    // so once the waves meet in stage s (each having finished its LDS reads) the buffer of stage s itself can take stage
+    // s + NS: every buffer of the ring holds a stage in flight. With more blocks a k half, the second half's first
+    // blocks still read stage s's A, so the refill goes one stage later, into the buffer of stage s - 1.
+    constexpr int AHEAD = HB == 1 ? NS : NS - 1;
+    // Prologue: stages 0 .. AHEAD - 1 in flight; stage 0 landed, its first k half of B and the first block's A read.
+    static_for<0, AHEAD>([&](auto u_tag) {
         const StageRsrc r = stage_rsrc(decltype(u_tag)::value * DBK);
         static_for<0, LOADS>([&](auto i_tag) { dma(u_tag, i_tag, r); });
     });
-    wait_vm_barrier<LOADS * (NS - 2)>();
+    wait_vm_barrier<LOADS * (AHEAD - 1)>();
     // B fragments in the signed domain, [k half][column block]; the current block's A fragments as stored and signed.
     v4i bf[2][FN], a_st[2], a_cur[2];
 #pragma unroll
@@ -344,23 +349,23 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
     // first of stage s + 1) and BPB B fragments: the first half's blocks this stage's second k half, the second half's
     // the next stage's first (whose registers are free once the first half is done). At the first block of the second
     // half the waves wait for stage s + 1 (this wave's loads landed, then everyone's) and meet: from then on nobody
-    // reads the buffer of stage s - 1, so the second half's blocks issue the loads of stage s + NS - 1 into it. Stages
+    // reads the buffer DU, so the second half's blocks issue the loads of stage s + AHEAD into it. Stages
     // past the last still wait and read (their loads cover empty or unused ranges and what is read is not used), so
     // every stage is the same.
     // SAR / SBR: the row / column byte sums this wave forms: those of its row blocks i with i % WGN == SAR and of its
     // column blocks j with j % WGM == SBR (-1: none). So each row block's sums come from one wave of its row of waves
     // and each column block's from one wave of its column, spread evenly, and no wave repeats another's.
     auto run_stage = [&](auto u_tag, int32_t s, auto sa_tag, auto sb_tag) {
-        constexpr int U = decltype(u_tag)::value, DU = (U + NS - 1) % NS, NU = (U + 1) % NS;
+        constexpr int U = decltype(u_tag)::value, DU = (U + AHEAD) % NS, NU = (U + 1) % NS;
         constexpr int SAR = decltype(sa_tag)::value, SBR = decltype(sb_tag)::value;
-        const StageRsrc rr = stage_rsrc((s + NS - 1) * DBK);
+        const StageRsrc rr = stage_rsrc((s + AHEAD) * DBK);
         static_for<0, NB>([&](auto b_tag) {
             constexpr int b = decltype(b_tag)::value, ks = b / HB, i0 = 2 * (b % HB);
             constexpr int rks = b < HB ? 1 : 0, rj = BPB * (b % HB), RU = b < HB ? U : NU;
             constexpr int nb = (b + 1) % NB, AU = b < NB - 1 ? U : NU;
             constexpr int LPB = LOADS / HB;   // loads per second-half block
             if constexpr (b == HB) {
-                wait_vm_lgkm_barrier<LOADS * (NS - 3)>();   // stages s + 2 .. s + NS - 2 may still be in flight
+                wait_vm_lgkm_barrier<LOADS * (AHEAD - 2)>();   // stages s + 2 .. s + AHEAD - 1 may still be in flight
                 __builtin_amdgcn_sched_barrier(0);
             }
             if constexpr (b >= HB) {
