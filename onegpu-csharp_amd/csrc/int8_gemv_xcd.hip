@@ -275,37 +275,63 @@ __global__ __launch_bounds__(GX_THREADS) void k_gemv_xcd(GemmArgs g, int32_t sla
     __syncthreads();
     if (!s_ok) return;
 
-    // The other parts, read with agent-scope loads (past the L1, from the XCD's L2), all in flight, added in part
-    // order to the tile's own sums.
+    // The other parts (slices 0 .. nkc - 2), read with agent-scope loads (sc1: past the vector L1, from the XCD's L2)
+    // and added in part order to the tile's own sums. A thread serves POS 16-byte positions (POS = 1 up to 256
+    // positions, M < 8; else 3) and takes the parts in groups of G (8, or 4 with 3 positions, which keeps the
+    // registers of the whole kernel within three waves a SIMD): every load of a group is issued before any is used, so
+    // a group costs one round trip. Reads past the parts return zero.
     const int32_t *pq = parts + (int64_t)q * nkc * pstride;
-    for (int it = tid; it < R * (GX_COLS / 4); it += GX_THREADS) {
-        const int r = it / (GX_COLS / 4), c4 = it % (GX_COLS / 4);
-        const int32_t *src = pq + r * GX_COLS + 4 * c4;
-        v4i s = *reinterpret_cast<const v4i *>(smem + r * GX_COLS + 4 * c4);
-        for (int p0 = 0; p0 < nkc; p0 += 8) {
-            unsigned long long t[8][2];
+    const __amdgpu_buffer_rsrc_t rp =
+        __builtin_amdgcn_make_buffer_rsrc((void *)pq, (short)0, (nkc - 1) * (int32_t)pstride * 4, 0x00020000);
+    constexpr int GX_SC1 = 16;   // cache policy: sc1
+    static_assert(GX_COLS / 4 == 32 && 17 * 32 <= 3 * GX_THREADS, "position it: row it / 32, columns 4 (it % 32) ..");
+    const int npos = R * (GX_COLS / 4);
+    auto add_parts = [&](auto pos_tag, auto group_tag) {
+        constexpr int POS = decltype(pos_tag)::value, G = decltype(group_tag)::value;
+        v4i tot[POS];
+        uint32_t at[POS];
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                t[e][0] = t[e][1] = 0;
-                if (p0 + e < nkc && p0 + e != kc) {
-                    const unsigned long long *pp = reinterpret_cast<const unsigned long long *>(src + (int64_t)(p0 + e) * pstride);
-                    t[e][0] = __hip_atomic_load(pp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    t[e][1] = __hip_atomic_load(pp + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int u = 0; u < POS; u++) {
+            const int it = tid + GX_THREADS * u;
+            at[u] = (uint32_t)((it >> 5) * GX_COLS + 4 * (it & 31)) * 4u;
+            tot[u] = it < npos ? *reinterpret_cast<const v4i *>(reinterpret_cast<const uint8_t *>(smem) + at[u])
+                               : (v4i){0, 0, 0, 0};
+        }
+        for (int p0 = 0; p0 < nkc - 1; p0 += G) {
+            v4i t[POS][G];
+#pragma unroll
+            for (int u = 0; u < POS; u++)
+#pragma unroll
+                for (int e = 0; e < G; e++) {
+                    const bool in = tid + GX_THREADS * u < npos && p0 + e < nkc - 1;
+                    t[u][e] = __builtin_amdgcn_raw_buffer_load_b128(
+                        rp, in ? (uint32_t)(p0 + e) * (uint32_t)pstride * 4u + at[u] : 0x80000000u, 0, GX_SC1);
                 }
-            }
+#pragma unroll
+            for (int u = 0; u < POS; u++)
+#pragma unroll
+                for (int e = 0; e < G; e++) tot[u] += t[u][e];
+        }
+#pragma unroll
+        for (int u = 0; u < POS; u++)
+            if (tid + GX_THREADS * u < npos)
+                *reinterpret_cast<v4i *>(reinterpret_cast<uint8_t *>(smem) + at[u]) = tot[u];
+    };
+    if (npos <= GX_THREADS) add_parts(std::integral_constant<int, 1>{}, std::integral_constant<int, 8>{});
+    else add_parts(std::integral_constant<int, 3>{}, std::integral_constant<int, 4>{});
+    if (SUM_A && tid < 16) {
+        uint32_t rs = (uint32_t)smem[R * GX_COLS + tid];
+        for (int p0 = 0; p0 < nkc - 1; p0 += 8) {
+            uint32_t t[8];
 #pragma unroll
             for (int e = 0; e < 8; e++)
-                s += (v4i){(int32_t)t[e][0], (int32_t)(t[e][0] >> 32), (int32_t)t[e][1], (int32_t)(t[e][1] >> 32)};
+                t[e] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                    rp, p0 + e < nkc - 1 ? ((uint32_t)(p0 + e) * (uint32_t)pstride + (uint32_t)(R * GX_COLS + tid)) * 4u : 0x80000000u,
+                    0, GX_SC1);
+#pragma unroll
+            for (int e = 0; e < 8; e++) rs += t[e];
         }
-        *reinterpret_cast<v4i *>(smem + r * GX_COLS + 4 * c4) = s;
-    }
-    if (SUM_A && tid < 16) {
-        uint32_t s = (uint32_t)smem[R * GX_COLS + tid];
-        for (int p = 0; p < nkc; p++)
-            if (p != kc)
-                s += __hip_atomic_load(reinterpret_cast<const uint32_t *>(pq + (int64_t)p * pstride + R * GX_COLS + tid),
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        smem[R * GX_COLS + tid] = (int32_t)s;
+        smem[R * GX_COLS + tid] = (int32_t)rs;
     }
     __syncthreads();
 
