@@ -360,7 +360,10 @@ def c5_chain(d, steps, warmup, check=True, c5=None):
     n_act, n_out = c5.Bt * c5.M * c5.K, c5.Bt * c5.M * c5.N
     kbytes = {"dq-minmax": 4 * n_act, "dq-quantize": 5 * n_act + 5, "scale-product": 8 * c5.Bt * c5.N + 4}
     for k in per:
-        per[k]["bytes"] = kbytes.get(k, c5.product_bytes if k.startswith("mfma") else 8 * n_out // c5.Bt)
+        # A rescale dispatch moves one batch's int32 in and float32 out, a batched one (every batch's pass in one
+        # launch) all of them.
+        per[k]["bytes"] = kbytes.get(k, c5.product_bytes if k.startswith("mfma") else
+                                     8 * n_out if k.endswith("-batch") else 8 * n_out // c5.Bt)
         per[k]["gbs_median"] = per[k]["bytes"] / (per[k]["median_us"] * 1e-6) / 1e9
         per[k]["hbm_frac_median"] = per[k]["gbs_median"] / PEAK_HBM_GBS
     # The chain's operands once: x read, B and the weight scales read, y written.

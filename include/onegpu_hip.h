@@ -239,6 +239,15 @@ typedef struct og_dequant_params {
 int og_dequantize(og_ctx *ctx, int kind, int f16_out, const og_dequant_params *params, og_buffer X, og_buffer scale,
                   og_buffer zero, og_buffer out);
 
+/* n DequantizeLinear passes of one count, axis and zero-point form (buffers and offsets their own) in one launch:
+ * no counterpart in the reference, where each pass is a dispatch of its own. For recorders that see consecutive
+ * passes, such as the per-batch rescale after a batched product whose batches have their own column scales; the
+ * host mirror's encoder batches consecutive passes through it. Passes run together, so a pass's output may not
+ * overlap another pass's operands (OG_ERR_INVALID_ARG, argument "output"); at most OG_DEQUANT_BATCH_MAX a call. */
+#define OG_DEQUANT_BATCH_MAX 256u
+int og_dequantize_batch(og_ctx *ctx, int kind, int f16_out, uint32_t n, const og_dequant_params *params,
+                        const og_buffer *X, const og_buffer *scale, const og_buffer *zero, const og_buffer *out);
+
 /* y = saturate(rne(x / scale[a]) + zp) with correctly rounded division, NaN to the lowest value; f16_in widens binary16
  * input exactly. Replaces DequantizeKernels.EncodeQuantize<TIn, TOut> (DequantizeKernels.cs:204-272). */
 int og_quantize(og_ctx *ctx, int is_signed, int f16_in, const og_dequant_params *params, og_buffer X, og_buffer scale,

@@ -1142,8 +1142,9 @@ static int check_axis(og_ctx *ctx, const og_dequant_params *p)
     return OG_OK;
 }
 
-int og_dequantize(og_ctx *ctx, int kind, int f16_out, const og_dequant_params *p, og_buffer X, og_buffer scale,
-                  og_buffer zero, og_buffer out)
+// Checks one DequantizeLinear pass and forms its kernel arguments.
+static int dequant_args(og_ctx *ctx, int kind, int f16_out, const og_dequant_params *p, og_buffer X, og_buffer scale,
+                        og_buffer zero, og_buffer out, og::DequantArgs *d)
 {
     if (!p) return fail(ctx, OG_ERR_INVALID_ARG, "params", "null parameter block");
     if (kind < OG_KIND_U8 || kind > OG_KIND_I32) return fail(ctx, OG_ERR_INVALID_ARG, "TIn", "unknown input kind %d", kind);
@@ -1157,19 +1158,67 @@ int og_dequantize(og_ctx *ctx, int kind, int f16_out, const og_dequant_params *p
         if ((p->Flags & 2u) && (!zero.ptr || (esz == 4 && ((uintptr_t)zero.ptr & 3)) || !fits(p->OffZ * esz, params * esz, zero))) return fail(ctx, OG_ERR_INVALID_ARG, "zeroPoint", "elements %u..%llu reach past the buffer", p->OffZ, (unsigned long long)(p->OffZ + params));
         if (!out.ptr || ((uintptr_t)out.ptr & (osz - 1)) || !fits(p->OffO * osz, cnt * osz, out)) return fail(ctx, OG_ERR_INVALID_ARG, "output", "elements %u..%llu reach past the buffer", p->OffO, (unsigned long long)(p->OffO + cnt));
     }
+    *d = og::DequantArgs{};
+    d->x = static_cast<const uint8_t *>(X.ptr) + p->OffX * esz;
+    d->scale = static_cast<const float *>(scale.ptr) + p->OffS;
+    d->zero = (p->Flags & 2u) ? static_cast<const uint8_t *>(zero.ptr) + p->OffZ * esz : nullptr;
+    d->out = static_cast<uint8_t *>(out.ptr) + p->OffO * osz;
+    d->count = p->Count;
+    d->axis_len = p->AxisLen ? p->AxisLen : 1;
+    d->inner = p->Inner ? p->Inner : 1;
+    d->per_axis = p->Flags & 1u;
+    d->has_zero = p->Flags & 2u;
+    return OG_OK;
+}
+
+int og_dequantize(og_ctx *ctx, int kind, int f16_out, const og_dequant_params *p, og_buffer X, og_buffer scale,
+                  og_buffer zero, og_buffer out)
+{
+    og::DequantArgs d;
+    int st = dequant_args(ctx, kind, f16_out, p, X, scale, zero, out, &d);
+    if (st != OG_OK) return st;
     if (!ctx) return fail(ctx, OG_ERR_NO_DEVICE, "ctx", "no context: the arguments are valid but there is no device to run on");
-    og::DequantArgs d{};
-    d.x = static_cast<const uint8_t *>(X.ptr) + p->OffX * esz;
-    d.scale = static_cast<const float *>(scale.ptr) + p->OffS;
-    d.zero = (p->Flags & 2u) ? static_cast<const uint8_t *>(zero.ptr) + p->OffZ * esz : nullptr;
-    d.out = static_cast<uint8_t *>(out.ptr) + p->OffO * osz;
-    d.count = p->Count;
-    d.axis_len = p->AxisLen ? p->AxisLen : 1;
-    d.inner = p->Inner ? p->Inner : 1;
-    d.per_axis = p->Flags & 1u;
-    d.has_zero = p->Flags & 2u;
     (void)hipSetDevice(ctx->device);
     st = launch(ctx, "og_dequantize", [&](const char **k) { return og::launch_dequantize(d, kind, f16_out != 0, ctx->stream, k); });
+    return st == OG_OK ? ok(ctx) : st;
+}
+
+int og_dequantize_batch(og_ctx *ctx, int kind, int f16_out, uint32_t n, const og_dequant_params *params,
+                        const og_buffer *X, const og_buffer *scale, const og_buffer *zero, const og_buffer *out)
+{
+    if (n == 0) return ok(ctx);
+    if (!params || !X || !scale || !zero || !out) return fail(ctx, OG_ERR_INVALID_ARG, "params", "null array");
+    if (n > OG_DEQUANT_BATCH_MAX) return fail(ctx, OG_ERR_INVALID_ARG, "n", "%u passes; at most %u a call", n, (unsigned)OG_DEQUANT_BATCH_MAX);
+    std::vector<og::DequantArgs> d(n);
+    for (uint32_t i = 0; i < n; i++) {
+        const og_dequant_params &a = params[0], &b = params[i];
+        if (b.Count != a.Count || b.Flags != a.Flags || ((b.Flags & 1u) && (b.AxisLen != a.AxisLen || b.Inner != a.Inner)))
+            return fail(ctx, OG_ERR_INVALID_ARG, "params", "pass %u's count, flags or axis differ from pass 0's", i);
+        const int st = dequant_args(ctx, kind, f16_out, &b, X[i], scale[i], zero[i], out[i], &d[i]);
+        if (st != OG_OK) return st;
+    }
+    // Passes run together, so no pass may write what another reads or writes.
+    const uint64_t esz = kind == OG_KIND_I32 ? 4 : 1, osz = f16_out ? 2 : 4;
+    const uint64_t pbytes = (params[0].Flags & 1u) ? (uint64_t)params[0].AxisLen * 4 : 4;
+    const uint64_t zbytes = (params[0].Flags & 1u) ? (uint64_t)params[0].AxisLen * esz : esz;
+    auto overlap = [](const void *a, uint64_t an, const void *b, uint64_t bn) {
+        const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+        return an && bn && x < y + bn && y < x + an;
+    };
+    const uint64_t cnt = params[0].Count;
+    for (uint32_t i = 0; i < n; i++)
+        for (uint32_t j = 0; j < n; j++) {
+            if (i == j) continue;
+            const bool hit = overlap(d[i].out, cnt * osz, d[j].x, cnt * esz) || overlap(d[i].out, cnt * osz, d[j].scale, pbytes) ||
+                             (d[j].has_zero && overlap(d[i].out, cnt * osz, d[j].zero, zbytes)) ||
+                             overlap(d[i].out, cnt * osz, d[j].out, cnt * osz);
+            if (hit) return fail(ctx, OG_ERR_INVALID_ARG, "output", "pass %u's output overlaps pass %u's operands", i, j);
+        }
+    if (!ctx) return fail(ctx, OG_ERR_NO_DEVICE, "ctx", "no context: the arguments are valid but there is no device to run on");
+    (void)hipSetDevice(ctx->device);
+    int st = launch(ctx, "og_dequantize_batch", [&](const char **k) {
+        return og::launch_dequantize_batch(d.data(), (int)n, kind, f16_out != 0, ctx->stream, k);
+    });
     return st == OG_OK ? ok(ctx) : st;
 }
 

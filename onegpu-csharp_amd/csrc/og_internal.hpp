@@ -139,6 +139,10 @@ struct DequantArgs {
     bool per_axis, has_zero;
 };
 hipError_t launch_dequantize(const DequantArgs &d, int kind, bool f16_out, hipStream_t s, const char **kernel);
+// n passes of one count, axis and zero-point form (their buffers independent) in ceil(n / kDqBatch) launches.
+constexpr int kDqBatch = 64;   // 64 argument blocks of 48 bytes: within the 4 KB of kernel arguments
+hipError_t launch_dequantize_batch(const DequantArgs *d, int n, int kind, bool f16_out, hipStream_t s,
+                                   const char **kernel);
 hipError_t launch_quantize(const DequantArgs &d, bool is_signed, bool f16_in, hipStream_t s, const char **kernel);
 
 // ONNX Gather along one axis as a copy of byte rows: output row (o, i) of row_bytes bytes is data row

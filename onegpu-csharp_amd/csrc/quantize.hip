@@ -6,6 +6,8 @@
 // Division is IEEE float32 division (correctly rounded: built with -fhip-fp32-correctly-rounded-divide-sqrt and
 // denormals kept), rounding is rintf (half to even), and no multiply is contracted into an add (-ffp-contract=off),
 // which reproduces the reference's CPU definitions bit for bit.
+#include <algorithm>
+
 #include "og_internal.hpp"
 
 namespace og {
@@ -289,14 +291,14 @@ __device__ __forceinline__ void column_params(const DequantArgs &d, uint32_t a, 
 
 // PER: 0 one scale for the tensor, 1 per axis, 2 per column in runs of four (column_params' conditions).
 template <int KIND, bool F16, int PER, bool VEC>
-__global__ __launch_bounds__(kEwThreads) void k_dequantize(DequantArgs d)
+__device__ __forceinline__ void dequant_block(const DequantArgs &d, uint32_t blk)
 {
     constexpr bool PER_AXIS = PER != 0;
-    if (VEC && ((uint64_t)blockIdx.x + 1) * kEwBlock <= d.count) {
+    if (VEC && ((uint64_t)blk + 1) * kEwBlock <= d.count) {
         int32_t q[4][4];
 #pragma unroll
         for (int c = 0; c < 4; c++) {   // all loads first, so that the four are in flight together
-            const uint32_t j = ew_run(blockIdx.x, c);
+            const uint32_t j = ew_run(blk, c);
             if constexpr (KIND == OG_KIND_I32) {
                 const i4v v = __builtin_nontemporal_load(reinterpret_cast<const i4v *>(static_cast<const int32_t *>(d.x) + j));
                 q[c][0] = v.x; q[c][1] = v.y; q[c][2] = v.z; q[c][3] = v.w;
@@ -312,7 +314,7 @@ __global__ __launch_bounds__(kEwThreads) void k_dequantize(DequantArgs d)
         const DequantParam<KIND> p0(d, 0);   // the one scale and zero point of a per-tensor pass
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            const uint32_t j = ew_run(blockIdx.x, c);
+            const uint32_t j = ew_run(blk, c);
             float y[4];
             if constexpr (PER == 2) {
                 DequantParam<KIND> p[4] = {p0, p0, p0, p0};
@@ -334,7 +336,7 @@ __global__ __launch_bounds__(kEwThreads) void k_dequantize(DequantArgs d)
     } else {
 #pragma unroll 4
         for (int e = 0; e < kEwBlock / kEwThreads; e++) {
-            const uint64_t j = (uint64_t)blockIdx.x * kEwBlock + (uint64_t)e * kEwThreads + threadIdx.x;
+            const uint64_t j = (uint64_t)blk * kEwBlock + (uint64_t)e * kEwThreads + threadIdx.x;
             if (j < d.count) {
                 const AxisWalk<PER_AXIS> w(d, (uint32_t)j);
                 store_y<F16>(d.out, (uint32_t)j, dequant_one<KIND>(load_q<KIND>(d.x, (uint32_t)j), DequantParam<KIND>(d, w.a)));
@@ -343,39 +345,90 @@ __global__ __launch_bounds__(kEwThreads) void k_dequantize(DequantArgs d)
     }
 }
 
+template <int KIND, bool F16, int PER, bool VEC>
+__global__ __launch_bounds__(kEwThreads) void k_dequantize(DequantArgs d)
+{
+    dequant_block<KIND, F16, PER, VEC>(d, blockIdx.x);
+}
+
+// Up to kDqBatch dequantize passes of one shape in one launch: pass blockIdx.y over its blocks blockIdx.x.
+struct DequantBatch {
+    DequantArgs d[kDqBatch];
+};
+
+template <int KIND, bool F16, int PER, bool VEC>
+__global__ __launch_bounds__(kEwThreads) void k_dequantize_batch(DequantBatch b)
+{
+    dequant_block<KIND, F16, PER, VEC>(b.d[blockIdx.y], blockIdx.x);
+}
+
 static bool ew_aligned(const void *a, const void *b) { return (((uintptr_t)a | (uintptr_t)b) & 15) == 0; }
 
 static dim3 ew_grid(uint32_t count) { return dim3((uint32_t)(((uint64_t)count + kEwBlock - 1) / kEwBlock)); }
 
-template <int KIND, bool F16>
-static void launch_dequantize_as(const DequantArgs &d, bool vec, hipStream_t s)
+// The variant a pass takes: PER 2 (per column in runs of four) when the scale and zero point are aligned for it.
+template <int KIND>
+static int dequant_per(const DequantArgs &d)
 {
-    const dim3 grid = ew_grid(d.count), block(kEwThreads);
     const uintptr_t zero_align = KIND == OG_KIND_I32 ? 15 : 3;
     const bool columns = d.per_axis && d.inner == 1 && d.axis_len % 4 == 0 && ((uintptr_t)d.scale & 15) == 0 &&
                          (!d.has_zero || ((uintptr_t)d.zero & zero_align) == 0);
-    if (vec && columns) hipLaunchKernelGGL((k_dequantize<KIND, F16, 2, true>), grid, block, 0, s, d);
-    else if (d.per_axis) {
-        if (vec) hipLaunchKernelGGL((k_dequantize<KIND, F16, 1, true>), grid, block, 0, s, d);
-        else hipLaunchKernelGGL((k_dequantize<KIND, F16, 1, false>), grid, block, 0, s, d);
-    } else {
-        if (vec) hipLaunchKernelGGL((k_dequantize<KIND, F16, 0, true>), grid, block, 0, s, d);
-        else hipLaunchKernelGGL((k_dequantize<KIND, F16, 0, false>), grid, block, 0, s, d);
-    }
+    return columns ? 2 : d.per_axis ? 1 : 0;
+}
+
+// n passes (n = 1: d[0] alone, k_dequantize; else k_dequantize_batch over the first n), all taking variant (per, vec).
+template <int KIND, bool F16>
+static void launch_dequantize_as(const DequantArgs *d, int n, int per, bool vec, hipStream_t s)
+{
+    const dim3 block(kEwThreads);
+#define OG_DQ(P, V)                                                                                                   \
+    do {                                                                                                              \
+        if (n == 1) {                                                                                                 \
+            hipLaunchKernelGGL((k_dequantize<KIND, F16, P, V>), ew_grid(d[0].count), block, 0, s, d[0]);              \
+        } else {                                                                                                      \
+            DequantBatch b{};                                                                                         \
+            for (int i = 0; i < n; i++) b.d[i] = d[i];                                                                \
+            hipLaunchKernelGGL((k_dequantize_batch<KIND, F16, P, V>), dim3(ew_grid(d[0].count).x, (uint32_t)n), block, \
+                               0, s, b);                                                                              \
+        }                                                                                                             \
+    } while (0)
+    if (per == 2) OG_DQ(2, true);
+    else if (per == 1) { if (vec) OG_DQ(1, true); else OG_DQ(1, false); }
+    else { if (vec) OG_DQ(0, true); else OG_DQ(0, false); }
+#undef OG_DQ
 }
 
 hipError_t launch_dequantize(const DequantArgs &d, int kind, bool f16_out, hipStream_t s, const char **kernel)
 {
-    const bool vec = ew_aligned(d.x, d.out);
-    *kernel = f16_out ? (vec ? "dequantize4-f16" : "dequantize-f16") : (vec ? "dequantize4-f32" : "dequantize-f32");
-    if (d.count == 0) return hipSuccess;
-    switch (kind * 2 + (f16_out ? 1 : 0)) {
-    case 0: launch_dequantize_as<OG_KIND_U8, false>(d, vec, s); break;
-    case 1: launch_dequantize_as<OG_KIND_U8, true>(d, vec, s); break;
-    case 2: launch_dequantize_as<OG_KIND_I8, false>(d, vec, s); break;
-    case 3: launch_dequantize_as<OG_KIND_I8, true>(d, vec, s); break;
-    case 4: launch_dequantize_as<OG_KIND_I32, false>(d, vec, s); break;
-    default: launch_dequantize_as<OG_KIND_I32, true>(d, vec, s); break;
+    return launch_dequantize_batch(&d, 1, kind, f16_out, s, kernel);
+}
+
+hipError_t launch_dequantize_batch(const DequantArgs *d, int n, int kind, bool f16_out, hipStream_t s,
+                                   const char **kernel)
+{
+    // Every pass of a batch has the count, axis and zero-point form of the first (the caller checks); the batch takes
+    // the variant every pass can take.
+    bool vec = true;
+    int per = 2;
+    for (int i = 0; i < n; i++) {
+        vec = vec && ew_aligned(d[i].x, d[i].out);
+        const int p = kind == OG_KIND_I32 ? dequant_per<OG_KIND_I32>(d[i]) : dequant_per<OG_KIND_U8>(d[i]);
+        per = std::min(per, p);
+    }
+    if (per == 2 && !vec) per = 1;
+    *kernel = n > 1 ? (f16_out ? (vec ? "dequantize4-f16-batch" : "dequantize-f16-batch") : (vec ? "dequantize4-f32-batch" : "dequantize-f32-batch"))
+                    : (f16_out ? (vec ? "dequantize4-f16" : "dequantize-f16") : (vec ? "dequantize4-f32" : "dequantize-f32"));
+    if (n <= 0 || d[0].count == 0) return hipSuccess;
+    for (int i0 = 0; i0 < n; i0 += kDqBatch) {
+        const int m = std::min(n - i0, kDqBatch);
+        switch (kind * 2 + (f16_out ? 1 : 0)) {
+        case 0: launch_dequantize_as<OG_KIND_U8, false>(d + i0, m, per, vec, s); break;
+        case 1: launch_dequantize_as<OG_KIND_U8, true>(d + i0, m, per, vec, s); break;
+        case 2: launch_dequantize_as<OG_KIND_I8, false>(d + i0, m, per, vec, s); break;
+        case 3: launch_dequantize_as<OG_KIND_I8, true>(d + i0, m, per, vec, s); break;
+        case 4: launch_dequantize_as<OG_KIND_I32, false>(d + i0, m, per, vec, s); break;
+        default: launch_dequantize_as<OG_KIND_I32, true>(d + i0, m, per, vec, s); break;
+        }
     }
     return hipGetLastError();
 }

@@ -109,7 +109,19 @@ void GpuBuffer::Dispose() { impl_.reset(); }
 void GpuCommandEncoder::Record(Command c, std::vector<std::shared_ptr<GpuBuffer::Impl>> keep)
 {
     if (submitted_) throw GpuException("GpuCommandEncoder: already submitted");
-    commands_.push_back(Entry{std::move(c), std::move(keep)});
+    commands_.push_back(Entry{std::move(c), std::move(keep), nullptr});
+}
+
+void GpuCommandEncoder::RecordDequant(DequantCommand c, std::vector<std::shared_ptr<GpuBuffer::Impl>> keep)
+{
+    if (submitted_) throw GpuException("GpuCommandEncoder: already submitted");
+    auto dq = std::make_shared<const DequantCommand>(std::move(c));
+    Command run = [dq](og_ctx *ctx) {
+        ThrowIfFailed(ctx, og_dequantize(ctx, dq->kind, dq->half ? 1 : 0, &dq->params, dq->x.Binding(), dq->scale.Binding(),
+                                         dq->zero.Binding(), dq->out.Binding()),
+                      "DequantizeLinear");
+    };
+    commands_.push_back(Entry{std::move(run), std::move(keep), std::move(dq)});
 }
 
 void GpuCommandEncoder::BeginPassTiming(int max_passes)
@@ -146,6 +158,7 @@ std::shared_ptr<GpuDevice> GpuDevice::Create(int ordinal, GpuDeviceOptions optio
     og_device_limits(ctx, &maxbuf, &cus, &lds);
     d->caps_.ComputeUnits = cus;
     d->caps_.MaxStorageBufferBindingBytes = options.MaxStorageBufferBindingBytes;
+    d->batch_ = options.BatchDispatches;
     return d;
 }
 
@@ -184,6 +197,53 @@ GpuBuffer GpuDevice::CreateBuffer(ElementType type, int length)
     return GpuBuffer(impl);
 }
 
+namespace {
+
+// The device bytes of a pass's operand: [begin, end).
+struct Span {
+    uintptr_t begin = 0, end = 0;
+};
+
+bool overlaps(const Span &a, const Span &b) { return a.begin < a.end && b.begin < b.end && a.begin < b.end && b.begin < a.end; }
+
+// Pass c's input spans (x, scale, zero point) and its output span.
+void dequant_spans(const DequantCommand &c, Span in[3], Span &out)
+{
+    const og_dequant_params &p = c.params;
+    const uint64_t esz = c.kind == OG_KIND_I32 ? 4 : 1, osz = c.half ? 2 : 4, params = (p.Flags & 1u) ? p.AxisLen : 1;
+    auto span = [](const GpuBuffer &b, uint64_t off, uint64_t bytes) {
+        const uintptr_t base = (uintptr_t)b.Binding().ptr + (uintptr_t)off;
+        return Span{base, base + (uintptr_t)bytes};
+    };
+    in[0] = span(c.x, (uint64_t)p.OffX * esz, (uint64_t)p.Count * esz);
+    in[1] = span(c.scale, (uint64_t)p.OffS * 4, params * 4);
+    in[2] = (p.Flags & 2u) ? span(c.zero, (uint64_t)p.OffZ * esz, params * esz) : Span{};
+    out = span(c.out, (uint64_t)p.OffO * osz, (uint64_t)p.Count * osz);
+}
+
+}  // namespace
+
+// Whether pass j can join the run of passes first .. j - 1: the same kind, output type, count, flags and axis as the
+// first, and no output overlapping another pass's operands or output.
+bool GpuDevice::dequant_joins(const DequantCommand &first, const std::vector<GpuCommandEncoder::Entry> &cmds, int begin,
+                              int j)
+{
+    const DequantCommand &c = *cmds[j].dq;
+    const og_dequant_params &a = first.params, &b = c.params;
+    if (c.kind != first.kind || c.half != first.half || b.Count != a.Count || b.Flags != a.Flags || b.Count == 0) return false;
+    if ((b.Flags & 1u) && (b.AxisLen != a.AxisLen || b.Inner != a.Inner)) return false;
+    Span cin[3], cout;
+    dequant_spans(c, cin, cout);
+    for (int k = begin; k < j; k++) {
+        Span kin[3], kout;
+        dequant_spans(*cmds[k].dq, kin, kout);
+        if (overlaps(cout, kout)) return false;
+        for (int t = 0; t < 3; t++)
+            if (overlaps(cout, kin[t]) || overlaps(kout, cin[t])) return false;
+    }
+    return true;
+}
+
 void GpuDevice::Submit(GpuCommandEncoder &encoder)
 {
     if (encoder.submitted_) throw GpuException("GpuDevice.Submit: encoder already submitted");
@@ -191,12 +251,40 @@ void GpuDevice::Submit(GpuCommandEncoder &encoder)
     if (encoder.commands_.empty()) return;
     if (!ctx_) throw GpuUnsupportedException("GpuDevice.Submit: a host-only device cannot run work", "Device", "a HIP device", "none");
     timed_ = 0;
-    const int start = encoder.timing_start_, stop = encoder.timing_stop_;
-    for (int i = 0; i < (int)encoder.commands_.size(); i++) {
+    const int start = encoder.timing_start_, stop = encoder.timing_stop_, n = (int)encoder.commands_.size();
+    const auto &cmds = encoder.commands_;
+    for (int i = 0; i < n;) {
         // A command may launch more than one kernel (a split product, the two passes of a quantizer): 4 slots each.
         if (i == start && stop >= start) ThrowIfFailed(ctx_, og_timing_begin(ctx_, std::max(encoder.timing_slots_, stop - start + 1) * 4), "BeginPassTiming");
-        encoder.commands_[i].run(ctx_);
-        if (i == stop && stop >= start) ThrowIfFailed(ctx_, og_timing_end(ctx_, &timed_), "EndPassTiming");
+        // Consecutive DequantizeLinear passes of one shape run as one launch when no pass writes what another reads or
+        // writes (in order they would be independent too, so the result is the same); a run does not cross the start
+        // or the end of pass timing.
+        int j = i + 1;
+        if (batch_ && cmds[i].dq) {
+            while (j < n && j - i < (int)OG_DEQUANT_BATCH_MAX && j != start && j - 1 != stop && cmds[j].dq &&
+                   dequant_joins(*cmds[i].dq, cmds, i, j))
+                j++;
+        }
+        if (j - i >= 2) {
+            std::vector<og_dequant_params> p;
+            std::vector<og_buffer> x, sc, z, o;
+            for (int k = i; k < j; k++) {
+                const DequantCommand &c = *cmds[k].dq;
+                p.push_back(c.params);
+                x.push_back(c.x.Binding());
+                sc.push_back(c.scale.Binding());
+                z.push_back(c.zero.Binding());
+                o.push_back(c.out.Binding());
+            }
+            const DequantCommand &c0 = *cmds[i].dq;
+            ThrowIfFailed(ctx_, og_dequantize_batch(ctx_, c0.kind, c0.half ? 1 : 0, (uint32_t)(j - i), p.data(), x.data(),
+                                                     sc.data(), z.data(), o.data()),
+                          "DequantizeLinear");
+        } else {
+            cmds[i].run(ctx_);
+        }
+        if (stop >= start && i <= stop && stop < j) ThrowIfFailed(ctx_, og_timing_end(ctx_, &timed_), "EndPassTiming");
+        i = j;
     }
 }
 
@@ -823,11 +911,15 @@ void DequantizeKernels::Encode(GpuCommandEncoder &encoder, const GpuBuffer &x, i
     w.Inner = (uint32_t)std::max<int64_t>(inner, 1);
     GpuBuffer X = x, S = scale, Z = zeroPoint ? *zeroPoint : GpuBuffer(), O = output;
     blocks_.Note(1 + 2 * (uint64_t)kind + (half ? 1 : 0), {&X, &S, &Z, &O});
-    encoder.Record(
-        [w, kind, half, X, S, Z, O](og_ctx *ctx) {
-            ThrowIfFailed(ctx, og_dequantize(ctx, kind, half ? 1 : 0, &w, bind(X), bind(S), bind(Z), bind(O)), "DequantizeLinear");
-        },
-        keep_of({&X, &S, &Z, &O}));
+    DequantCommand c;
+    c.kind = kind;
+    c.half = half;
+    c.params = w;
+    c.x = X;
+    c.scale = S;
+    c.zero = Z;
+    c.out = O;
+    encoder.RecordDequant(std::move(c), keep_of({&X, &S, &Z, &O}));
 }
 
 void DequantizeKernels::EncodeQuantize(GpuCommandEncoder &encoder, const GpuBuffer &x, int offsetX,

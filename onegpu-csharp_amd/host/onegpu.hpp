@@ -91,6 +91,9 @@ struct GpuComputeCapabilities {
 struct GpuDeviceOptions {
     // Lower than the hardware's, to run a product the way a device with small bindings (llvmpipe: 128 MB) refuses it.
     uint64_t MaxStorageBufferBindingBytes = 0;
+    // This library's own: Submit runs consecutive DequantizeLinear passes of one shape whose buffers are independent
+    // as one launch (og_dequantize_batch). false keeps a launch a pass. The results are the same either way.
+    bool BatchDispatches = true;
 };
 
 class GpuDevice;
@@ -117,11 +120,20 @@ private:
     std::shared_ptr<Impl> impl_;
 };
 
+// A recorded DequantizeLinear pass, kept whole so that Submit can run consecutive passes of one shape together.
+struct DequantCommand {
+    int kind = 0;
+    bool half = false;
+    og_dequant_params params{};
+    GpuBuffer x, scale, zero, out;
+};
+
 // Records work; nothing runs until GpuDevice::Submit (src/RecursiveAI.OneGpu/GpuDevice.cs:155-161; Resources.cs:148-316).
 class GpuCommandEncoder {
 public:
     using Command = std::function<void(og_ctx *)>;
     void Record(Command c, std::vector<std::shared_ptr<GpuBuffer::Impl>> keep);
+    void RecordDequant(DequantCommand c, std::vector<std::shared_ptr<GpuBuffer::Impl>> keep);
     int DispatchCount() const { return (int)commands_.size(); }
     // Per-dispatch timing of the commands recorded between the two calls (Resources.cs:216-222).
     void BeginPassTiming(int max_passes);
@@ -132,6 +144,7 @@ private:
     struct Entry {
         Command run;
         std::vector<std::shared_ptr<GpuBuffer::Impl>> keep;
+        std::shared_ptr<const DequantCommand> dq;   // set for a DequantizeLinear pass
     };
     std::vector<Entry> commands_;
     int timing_start_ = -1;  // first timed command
@@ -164,10 +177,13 @@ public:
 
 private:
     GpuDevice() = default;
+    static bool dequant_joins(const DequantCommand &first, const std::vector<GpuCommandEncoder::Entry> &cmds, int begin,
+                              int j);
     og_ctx *ctx_ = nullptr;
     GpuComputeCapabilities caps_;
     std::string name_;
     int timed_ = 0;
+    bool batch_ = true;
 };
 
 // Maps a C-ABI status to the reference's exception (operation names the family).

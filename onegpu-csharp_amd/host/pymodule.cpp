@@ -150,8 +150,13 @@ PYBIND11_MODULE(_onegpu_host, m)
         }, py::arg("a"), py::arg("b"), py::arg("n"), py::arg("out"));
 
     py::class_<GpuDevice, std::shared_ptr<GpuDevice>>(m, "GpuDevice")
-        .def_static("Create", [](int ordinal, uint64_t max_binding) { GpuDeviceOptions o; o.MaxStorageBufferBindingBytes = max_binding; return GpuDevice::Create(ordinal, o); },
-                    py::arg("ordinal") = 0, py::arg("max_binding_bytes") = 0)
+        .def_static("Create", [](int ordinal, uint64_t max_binding, bool batch) {
+                        GpuDeviceOptions o;
+                        o.MaxStorageBufferBindingBytes = max_binding;
+                        o.BatchDispatches = batch;
+                        return GpuDevice::Create(ordinal, o);
+                    },
+                    py::arg("ordinal") = 0, py::arg("max_binding_bytes") = 0, py::arg("BatchDispatches") = true)
         .def_static("CreateHostOnly", [](uint64_t max_binding) { GpuDeviceOptions o; o.MaxStorageBufferBindingBytes = max_binding; return GpuDevice::CreateHostOnly(o); },
                     py::arg("max_binding_bytes") = 0)
         .def("CreateBuffer", [](GpuDevice &d, py::array data) { return create_from(d, data); }, py::arg("data"),

@@ -323,6 +323,45 @@ class GemmParams(ctypes.Structure):
                                                "OffFBias", "GridX")]
 
 
+class DequantParams(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in ("Count", "OffX", "OffO", "OffS", "OffZ", "GridX", "Flags", "AxisLen",
+                                               "Inner")]
+
+
+def test_dequantize_batch_validates_before_touching_a_device():
+    # og_dequantize_batch: every pass checked as og_dequantize checks one; the passes must share count, flags and axis,
+    # and no pass's output may meet another pass's operands (they run together). Host addresses stand in for device
+    # ones: nothing is dereferenced.
+    lib = ctypes.CDLL(og.LIB_PATH)
+    lib.og_dequantize_batch.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_uint32,
+                                        ctypes.POINTER(DequantParams)] + [ctypes.POINTER(Buf)] * 4
+    lib.og_last_error_argument.restype = ctypes.c_char_p
+    lib.og_last_error_argument.argtypes = [ctypes.c_void_p]
+    host = (ctypes.c_uint8 * 65536)()
+    addr = ctypes.addressof(host)
+    n, cols = 3, 16
+
+    def call(params, outs=None, xs=None):
+        k = len(params)
+        P = (DequantParams * k)(*params)
+        X = (Buf * k)(*(xs or [Buf(addr + 1024 * i, 256) for i in range(k)]))
+        S = (Buf * k)(*[Buf(addr + 8192 + 256 * i, 64) for i in range(k)])
+        Z = (Buf * k)(*[Buf(None, 0)] * k)
+        O = (Buf * k)(*(outs or [Buf(addr + 16384 + 1024 * i, 256) for i in range(k)]))
+        st = lib.og_dequantize_batch(None, 2, 0, k, P, X, S, Z, O)   # int32 -> float32
+        return st, lib.og_last_error_argument(None).decode()
+
+    good = DequantParams(Count=64, Flags=1, AxisLen=cols, Inner=1)
+    assert call([good] * n) == (6, "ctx")                                                    # valid: no device
+    assert call([good, DequantParams(Count=60, Flags=1, AxisLen=cols, Inner=1), good])[1] == "params"
+    assert call([good, DequantParams(Count=64, Flags=0), good])[1] == "params"
+    assert call([good] * n, outs=[Buf(addr + 16384, 256)] * n)[1] == "output"                # one output for all
+    assert call([good] * 2, outs=[Buf(addr + 16384, 256), Buf(addr, 256)])[1] == "output"   # pass 1 writes pass 0's x
+    assert call([good] * 2, outs=[Buf(addr + 16384, 256), Buf(addr + 1024, 256)]) == (6, "ctx")   # in place: its own
+    assert call([good] * n, xs=[Buf(addr, 255)] + [Buf(addr + 1024, 256)] * 2)[1] == "x"     # x one byte short
+    assert call([good] * 300)[1] == "n"
+
+
 def test_abi_validates_before_touching_a_device():
     # The C ABI re-checks ranges itself: with no context it reports the bad argument, or, when every argument is
     # valid, that there is no device. Host addresses stand in for device ones: nothing is dereferenced.

@@ -179,3 +179,68 @@ def test_dynamic_quantize_golden_fixture():
             say(f"MISMATCH dq fixture vector {i}: {here}")
         bad += here
     assert bad == 0
+
+
+def _batch_passes(d, k, n_pass, rows, cols, seed, half=False, aligned=True):
+    """n_pass DequantizeLinear passes of int32 [rows x cols] with per-column scales, each its own input, scale and
+    output (the per-batch rescale after a batched product whose batches have their own column scales), recorded in
+    one encoder. Returns (mismatching elements against the oracle, the dispatches' kernel names)."""
+    n = rows * cols
+    xs = [oracle.dequant_input_i32(n, seed + 3 * p) for p in range(n_pass)]
+    ss = [oracle.rig_random(cols, seed + 3 * p + 1, 0.001, 2.0) for p in range(n_pass)]
+    off = 0 if aligned else 1
+    length = og.padded_half_length(n + off) if half else n + off
+    outs = [np.full(length, -77, np.float16 if half else np.float32) for _ in range(n_pass)]
+    bx = [d.CreateBuffer(x) for x in xs]
+    bs = [d.CreateBuffer(s) for s in ss]
+    bo = [d.CreateBuffer(o) for o in outs]
+    names = run_named(d, lambda e: [k.Encode(e, bx[p], 0, [rows, cols], 1, True, bs[p], 0, None, 0, bo[p], off)
+                                    for p in range(n_pass)])
+    bad = 0
+    for p in range(n_pass):
+        want = oracle.dequantize(xs[p], ss[p], True, cols, 1, None, f16_out=half)
+        got = bo[p].Read()
+        bits = np.uint16 if half else np.uint32
+        bad += int(np.count_nonzero(got[off:off + n].view(bits) != want.view(bits)))
+    return bad, names
+
+
+@pytest.mark.parametrize("half", [False, True])
+def test_consecutive_dequantize_passes_run_as_one_launch(half):
+    # 40 passes of one shape: one batch of 40 (the recorder batches up to 256, a launch takes up to 64), bit-exact, and
+    # the same bits with batching off (a launch a pass).
+    d = device()
+    k = og.DequantizeKernels(d)
+    say(f"dequantize batch: 40 passes of 64 x 256, f16 {half}")
+    bad, names = _batch_passes(d, k, 40, 64, 256, 500, half)
+    assert bad == 0
+    assert names == ["dequantize4-" + ("f16" if half else "f32") + "-batch"], names
+    d1 = og.GpuDevice.Create(0, 0, BatchDispatches=False)
+    bad1, names1 = _batch_passes(d1, og.DequantizeKernels(d1), 40, 64, 256, 500, half)
+    assert bad1 == 0 and len(names1) == 40, names1
+    say("  unaligned outputs (the scalar form, batched)")
+    bad, names = _batch_passes(d, k, 5, 33, 100, 900, half, aligned=False)
+    assert bad == 0 and names == ["dequantize-" + ("f16" if half else "f32") + "-batch"], names
+
+
+def test_dependent_dequantize_passes_stay_in_order():
+    # Passes whose buffers meet are not batched: the second of two passes into the same output wins, as in order; a
+    # pass of another shape ends a batch.
+    d = device()
+    k = og.DequantizeKernels(d)
+    rows, cols = 16, 64
+    n = rows * cols
+    x1, x2 = oracle.dequant_input_i32(n, 7), oracle.dequant_input_i32(n, 8)
+    s1, s2 = oracle.rig_random(cols, 9, 0.001, 2.0), oracle.rig_random(cols, 10, 0.001, 2.0)
+    b1, b2, c1, c2 = d.CreateBuffer(x1), d.CreateBuffer(x2), d.CreateBuffer(s1), d.CreateBuffer(s2)
+    out = d.CreateBuffer(np.zeros(n, np.float32))
+    other = d.CreateBuffer(np.zeros(n, np.float32))
+    say("dequantize batch: two passes into one output, then a pass of another shape")
+    names = run_named(d, lambda e: [k.Encode(e, b1, 0, [rows, cols], 1, True, c1, 0, None, 0, out, 0),
+                                    k.Encode(e, b2, 0, [rows, cols], 1, True, c2, 0, None, 0, out, 0),
+                                    k.Encode(e, b1, 0, [rows * cols], 0, False, c1, 0, None, 0, other, 0)])
+    assert names == ["dequantize4-f32"] * 3, names
+    want = oracle.dequantize(x2, s2, True, cols, 1, None)
+    assert np.array_equal(out.Read().view(np.uint32), want.view(np.uint32))
+    want_other = oracle.dequantize(x1, s1, False, 1, 1, None)
+    assert np.array_equal(other.Read().view(np.uint32), want_other.view(np.uint32))
