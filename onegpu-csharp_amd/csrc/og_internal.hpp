@@ -48,7 +48,7 @@ struct Workspace {
     float *dq_ranges;        // 2 * kDqMaxGroups floats: the dynamic quantizer's per-workgroup ranges
 };
 
-constexpr int kDqMaxGroups = 1024;
+constexpr int kDqMaxGroups = 256;
 
 // og_int8_gemm_noalloc's fixed scratch (one array a device): the few-rows kernel's count words, then partial sums.
 constexpr uint64_t kNoAllocScratchBytes = 16ull << 20, kNoAllocWordBytes = 64ull << 10;

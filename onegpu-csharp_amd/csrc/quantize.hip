@@ -1,7 +1,8 @@
 // The element-wise and reduction kernels around the int8 product, for gfx950:
 //  - DynamicQuantizeLinear: a min/max pass writing one range per workgroup, then a quantize pass in which every
-//    workgroup combines those ranges into the scale and zero point and streams x again with 16-byte loads, writing 16
-//    output bytes per thread (no host round trip, no counters or fences: the kernel boundary orders the passes).
+//    workgroup combines those ranges into the scale and zero point and quantizes one block of x with 16-byte loads,
+//    writing 16 output bytes per thread (no host round trip, no counters or fences: the kernel boundary orders the
+//    passes).
 //  - DequantizeLinear / QuantizeLinear and the QLinearMatMul requantization (the int8 epilogue's mode 2).
 // Division is IEEE float32 division (correctly rounded: built with -fhip-fp32-correctly-rounded-divide-sqrt and
 // denormals kept), rounding is rintf (half to even), and no multiply is contracted into an add (-ffp-contract=off),
@@ -18,7 +19,8 @@ __device__ __forceinline__ bool is_nan_bits(float x) { return (__float_as_uint(x
 
 // ------------------------------------------------------------------ DynamicQuantizeLinear
 
-constexpr int DQ_THREADS = 256;
+constexpr int DQ_THREADS = 256;    // pass 2 (and the element-wise kernels' block of 4096 elements)
+constexpr int DQ1_THREADS = 1024;  // pass 1: 16 waves a workgroup, at most kDqMaxGroups workgroups, one per CU
 
 __device__ __forceinline__ void minmax_acc(float v, float &mn, float &mx)
 {
@@ -27,6 +29,7 @@ __device__ __forceinline__ void minmax_acc(float v, float &mn, float &mx)
     mx = (v > mx) ? v : mx;
 }
 
+template <int NT>
 __device__ __forceinline__ void block_minmax(float &mn, float &mx, float *smin, float *smax)
 {
 #pragma unroll
@@ -39,7 +42,7 @@ __device__ __forceinline__ void block_minmax(float &mn, float &mx, float *smin, 
     if (lane == 0) { smin[wave] = mn; smax[wave] = mx; }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < DQ_THREADS / 64; w++) {
+        for (int w = 1; w < NT / 64; w++) {
             mn = (smin[w] < mn) ? smin[w] : mn;
             mx = (smax[w] > mx) ? smax[w] : mx;
         }
@@ -64,11 +67,11 @@ __device__ void dq_params(float mn, float mx, float &scale, uint32_t &zp)
 }
 
 // Pass 1: each workgroup's range (NaN-ignoring min and max) over its grid-stride share of x.
-__global__ __launch_bounds__(DQ_THREADS) void k_dq_minmax(const float *x, uint32_t count, float *ranges)
+__global__ __launch_bounds__(DQ1_THREADS) void k_dq_minmax(const float *x, uint32_t count, float *ranges)
 {
-    __shared__ float smin[DQ_THREADS / 64], smax[DQ_THREADS / 64];
+    __shared__ float smin[DQ1_THREADS / 64], smax[DQ1_THREADS / 64];
     float mn = __int_as_float(0x7F800000), mx = __int_as_float(0xFF800000);
-    const uint32_t tid = blockIdx.x * DQ_THREADS + threadIdx.x, nthreads = gridDim.x * DQ_THREADS;
+    const uint32_t tid = blockIdx.x * DQ1_THREADS + threadIdx.x, nthreads = gridDim.x * DQ1_THREADS;
     if (((uintptr_t)x & 15) == 0) {
         const uint32_t n4 = count / 4;
         const f4 *x4 = reinterpret_cast<const f4 *>(x);
@@ -92,7 +95,7 @@ __global__ __launch_bounds__(DQ_THREADS) void k_dq_minmax(const float *x, uint32
     } else {
         for (uint32_t i = tid; i < count; i += nthreads) minmax_acc(x[i], mn, mx);
     }
-    block_minmax(mn, mx, smin, smax);
+    block_minmax<DQ1_THREADS>(mn, mx, smin, smax);
     if (threadIdx.x == 0) {
         ranges[2 * blockIdx.x] = mn;
         ranges[2 * blockIdx.x + 1] = mx;
@@ -105,24 +108,33 @@ __device__ __forceinline__ uint32_t dq_one(float x, float scale, float zp)
     return is_nan_bits(v) ? 0u : (uint32_t)fminf(fmaxf(v, 0.0f), 255.0f);
 }
 
-// Pass 2: every workgroup combines pass 1's ranges (the kernel boundary orders them; min and max are order-free, so
-// every workgroup derives the same scale and zero point) and quantizes blocks of 4096 elements, grid-stride. In a
-// whole block with x and y 16-byte aligned, lane l of wave w takes elements 1024 w + 256 c + 4 l .. + 3 (c = 0..3)
-// with one 16-byte load and one 4-byte store each, so every instruction covers one contiguous span across the wave;
-// otherwise lane t takes elements t, t + 256, ... Workgroup 0 writes the scale and the zero point (one byte, its
-// neighbours untouched).
-__global__ __launch_bounds__(DQ_THREADS) void k_dq_quantize(const float *x, uint8_t *y, uint32_t count,
-                                                            const float *ranges, uint32_t groups, float *scale_out,
-                                                            uint8_t *zero_out)
+// Pass 2's scale and zero point, in every workgroup: pass 1's ranges combined (the kernel boundary orders them; min and
+// max are order-free, so every workgroup derives the same values). Each thread loads kDqMaxGroups / DQ_THREADS of the
+// (min, max) pairs before the caller's block of x, unconditionally (the workspace always holds kDqMaxGroups pairs, so
+// no load waits on a branch), and ignores the pairs from `groups` on; workgroup 0 also writes the scale and zero point
+// out (the zero point one byte, its neighbours untouched).
+typedef float f2 __attribute__((ext_vector_type(2)));
+constexpr int DQ_PAIRS = kDqMaxGroups / DQ_THREADS;
+static_assert(kDqMaxGroups % DQ_THREADS == 0, "the ranges split evenly over the threads");
+
+__device__ __forceinline__ void dq_load_ranges(const float *ranges, f2 (&r)[DQ_PAIRS])
 {
-    __shared__ float smin[DQ_THREADS / 64], smax[DQ_THREADS / 64], sparam[2];
+#pragma unroll
+    for (int q = 0; q < DQ_PAIRS; q++) r[q] = reinterpret_cast<const f2 *>(ranges)[threadIdx.x + q * DQ_THREADS];
+}
+
+__device__ __forceinline__ void dq_combine(const f2 (&r)[DQ_PAIRS], uint32_t groups, float *smin, float *smax,
+                                           float *sparam, float *scale_out, uint8_t *zero_out, float &scale, float &zpf)
+{
     float mn = __int_as_float(0x7F800000), mx = __int_as_float(0xFF800000);
-    for (uint32_t g = threadIdx.x; g < groups; g += DQ_THREADS) {
-        const float a = ranges[2 * g], b = ranges[2 * g + 1];
-        mn = (a < mn) ? a : mn;
-        mx = (b > mx) ? b : mx;
+#pragma unroll
+    for (int q = 0; q < DQ_PAIRS; q++) {
+        if (threadIdx.x + q * DQ_THREADS < groups) {
+            mn = (r[q].x < mn) ? r[q].x : mn;
+            mx = (r[q].y > mx) ? r[q].y : mx;
+        }
     }
-    block_minmax(mn, mx, smin, smax);
+    block_minmax<DQ_THREADS>(mn, mx, smin, smax);
     if (threadIdx.x == 0) {
         float sc;
         uint32_t zp;
@@ -135,29 +147,44 @@ __global__ __launch_bounds__(DQ_THREADS) void k_dq_quantize(const float *x, uint
         }
     }
     __syncthreads();
-    const float scale = sparam[0], zp = sparam[1];
-    const bool vec = (((uintptr_t)x | (uintptr_t)y) & 15) == 0;
-    const uint32_t lane_off = (threadIdx.x >> 6) * 1024u + (threadIdx.x & 63u) * 4u;
-    for (uint64_t blk = (uint64_t)blockIdx.x * 4096; blk < count; blk += (uint64_t)gridDim.x * 4096) {
-        if (vec && blk + 4096 <= count) {
-            f4 v[4];
+    scale = sparam[0];
+    zpf = sparam[1];
+}
+
+// Pass 2: workgroup b quantizes elements 4096 b .. 4096 b + 4095. It requests the ranges, then its block of x, and
+// combines the ranges while x is still on its way from HBM. In a whole block with x and y 16-byte aligned, lane l of
+// wave w takes elements 1024 w + 256 c + 4 l .. + 3 (c = 0..3) with one 16-byte load and one 4-byte store each, so
+// every instruction covers one contiguous span across the wave; otherwise lane t takes elements t, t + 256, ...
+__global__ __launch_bounds__(DQ_THREADS) void k_dq_quantize(const float *x, uint8_t *y, uint32_t count,
+                                                            const float *ranges, uint32_t groups, float *scale_out,
+                                                            uint8_t *zero_out)
+{
+    __shared__ float smin[DQ_THREADS / 64], smax[DQ_THREADS / 64], sparam[2];
+    f2 r[DQ_PAIRS];
+    dq_load_ranges(ranges, r);
+    const uint64_t blk = (uint64_t)blockIdx.x * 4096;
+    float scale, zp;
+    if ((((uintptr_t)x | (uintptr_t)y) & 15) == 0 && blk + 4096 <= count) {
+        const uint32_t lane_off = (threadIdx.x >> 6) * 1024u + (threadIdx.x & 63u) * 4u;
+        f4 v[4];
 #pragma unroll
-            for (int c = 0; c < 4; c++) v[c] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(x + blk + lane_off + 256 * c));
+        for (int c = 0; c < 4; c++) v[c] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(x + blk + lane_off + 256 * c));
+        dq_combine(r, groups, smin, smax, sparam, scale_out, zero_out, scale, zp);
 #pragma unroll
-            for (int c = 0; c < 4; c++)
-                *reinterpret_cast<uint32_t *>(y + blk + lane_off + 256 * c) =
-                    dq_one(v[c].x, scale, zp) | (dq_one(v[c].y, scale, zp) << 8) | (dq_one(v[c].z, scale, zp) << 16) |
-                    (dq_one(v[c].w, scale, zp) << 24);
-        } else {
-            for (uint64_t i = blk + threadIdx.x; i < blk + 4096 && i < count; i += DQ_THREADS) y[i] = (uint8_t)dq_one(x[i], scale, zp);
-        }
+        for (int c = 0; c < 4; c++)
+            *reinterpret_cast<uint32_t *>(y + blk + lane_off + 256 * c) =
+                dq_one(v[c].x, scale, zp) | (dq_one(v[c].y, scale, zp) << 8) | (dq_one(v[c].z, scale, zp) << 16) |
+                (dq_one(v[c].w, scale, zp) << 24);
+    } else {
+        dq_combine(r, groups, smin, smax, sparam, scale_out, zero_out, scale, zp);
+        for (uint64_t i = blk + threadIdx.x; i < blk + 4096 && i < count; i += DQ_THREADS) y[i] = (uint8_t)dq_one(x[i], scale, zp);
     }
 }
 
 static uint32_t dq_groups(uint32_t count)
 {
-    // About 16 KB of x per workgroup, at most kDqMaxGroups.
-    uint32_t g = (count + 4095) / 4096;
+    // About 64 KB of x per workgroup, at most kDqMaxGroups.
+    uint32_t g = (count + 16383) / 16384;
     return g < 1 ? 1 : (g > (uint32_t)kDqMaxGroups ? (uint32_t)kDqMaxGroups : g);
 }
 
@@ -166,13 +193,12 @@ hipError_t launch_dynamic_quantize(const DqArgs &d, const Workspace &ws, hipStre
     const uint32_t groups = dq_groups(d.count);
     if (step == 0) {
         *kernel = "dq-minmax";
-        hipLaunchKernelGGL(k_dq_minmax, dim3(groups), dim3(DQ_THREADS), 0, s, d.x, d.count, ws.dq_ranges);
+        hipLaunchKernelGGL(k_dq_minmax, dim3(groups), dim3(DQ1_THREADS), 0, s, d.x, d.count, ws.dq_ranges);
     } else {
         *kernel = "dq-quantize";
-        // One block of 4096 elements a workgroup, at most 2048 workgroups (each re-reads the ranges).
-        uint64_t wgs = ((uint64_t)d.count + 4095) / 4096;
-        wgs = wgs > 2048 ? 2048 : (wgs < 1 ? 1 : wgs);
-        hipLaunchKernelGGL(k_dq_quantize, dim3((uint32_t)wgs), dim3(DQ_THREADS), 0, s, d.x, d.y, d.count,
+        // One block of 4096 elements a workgroup (at most 2^20 workgroups for a 32-bit count).
+        const uint32_t wgs = d.count == 0 ? 1u : (uint32_t)(((uint64_t)d.count + 4095) / 4096);
+        hipLaunchKernelGGL(k_dq_quantize, dim3(wgs), dim3(DQ_THREADS), 0, s, d.x, d.y, d.count,
                            (const float *)ws.dq_ranges, groups, d.scale, d.zero);
     }
     return hipGetLastError();

@@ -309,9 +309,12 @@ def test_dynamic_quantize_large_inputs():
 def test_dynamic_quantize_in_sequence():
     # Consecutive launches of different sizes and ranges on one device, each checked against the oracle: nothing of
     # one launch's ranges may leak into the next (the per-workgroup ranges live in a workspace the launches share).
+    # Large and small launches alternate, so a larger launch's ranges past a smaller one's groups are still in the
+    # workspace when the smaller one runs.
     d = device()
     k = og.DynamicQuantizeKernels(d)
-    counts = [2_097_152, 1, 4097, 786_432, 2_097_153, 65_536, 2_000_001, 3, 1_048_577, 2_097_152, 257, 786_432]
+    counts = [2_097_152, 1, 4097, 786_432, 2_097_153, 65_536, 2_000_001, 3, 1_048_577, 2_097_152, 257, 786_432,
+              4_194_304, 4_194_303, 6_000_007, 6_000_007, 5, 4_194_305, 8_388_608]
     for i, count in enumerate(counts):
         kind = i % 7
         x = oracle.dq_input(count, 900 + i, kind)
