@@ -223,6 +223,17 @@ def test_consecutive_dequantize_passes_run_as_one_launch(half):
     assert bad == 0 and names == ["dequantize-" + ("f16" if half else "f32") + "-batch"], names
 
 
+def test_long_runs_of_dequantize_passes_split_into_batches():
+    # 300 passes of one shape: the recorder takes at most 256 passes a call (OG_DEQUANT_BATCH_MAX), so two calls (256 +
+    # 44), and a call launches at most 64 passes at once (four launches for the first); every pass bit-exact.
+    d = device()
+    k = og.DequantizeKernels(d)
+    say("dequantize batch: 300 passes of 4 x 64")
+    bad, names = _batch_passes(d, k, 300, 4, 64, 1300)
+    assert bad == 0
+    assert names == ["dequantize4-f32-batch"] * 2, names
+
+
 def test_dependent_dequantize_passes_stay_in_order():
     # Passes whose buffers meet are not batched: the second of two passes into the same output wins, as in order; a
     # pass of another shape ends a batch.
