@@ -76,6 +76,46 @@ def test_dequantize_is_exact(dtype, seed0, offs):
     assert bad == 0
 
 
+@pytest.mark.parametrize("offs", [UNALIGNED, ALIGNED], ids=["unaligned", "aligned"])
+@pytest.mark.parametrize("dtype,seed0", [(np.uint8, 3001), (np.int8, 3100), (np.int32, 3200)])
+def test_batched_dequantize_is_exact(dtype, seed0, offs):
+    # The cases of DequantizeIsExact, each as three passes of one shape with their own buffers recorded together, so
+    # that the recorder runs them as one batched launch: every input kind, zero points per tensor and per axis, both
+    # output types, the vector and the scalar forms.
+    OffX, OffS, OffZ, OffO = offs
+    d = device()
+    k = og.DequantizeKernels(d)
+    seed, bad = seed0, 0
+    for shape, axis, per_axis in cases.DEQUANT_SHAPES + cases.DEQUANT_SHAPES_BLOCKS:
+        n, axis_len, inner = cases.axis_split(shape, axis, per_axis)
+        for with_zero in (True, False):
+            for half in (False, True):
+                say(f"dequantize batch {np.dtype(dtype).name} {shape} axis {axis} per {per_axis} zero {with_zero} "
+                    f"f16 {half} offsets {offs}")
+                passes = []
+                for q in range(3):
+                    x = _quantized(dtype, n + OffX, seed)
+                    scale = oracle.rig_random(axis_len + OffS, seed + 1, 0.001, 2.0)
+                    zeros = _quantized(dtype, axis_len + OffZ, seed + 2)
+                    seed += 3
+                    want = oracle.dequantize(x[OffX:OffX + n], scale[OffS:], per_axis, axis_len, inner,
+                                             zeros[OffZ:OffZ + axis_len] if with_zero else None, f16_out=half)
+                    length = og.padded_half_length(n + OffO + 1) if half else n + OffO + 1
+                    out = np.full(length, -77, np.float16 if half else np.float32)
+                    passes.append((d.CreateBuffer(x), d.CreateBuffer(scale), d.CreateBuffer(zeros), d.CreateBuffer(out),
+                                   want))
+                names = run_named(d, lambda e: [k.Encode(e, bx, OffX, shape, axis, per_axis, bs,
+                                                         OffS, bz if with_zero else None, OffZ, bo, OffO)
+                                                for bx, bs, bz, bo, _ in passes])
+                want_kernel = ("dequantize4-" if offs == ALIGNED else "dequantize-") + ("f16" if half else "f32")
+                assert names == [want_kernel + "-batch"], names
+                for _, _, _, bo, want in passes:
+                    gbits = bo.Read().view(np.uint16 if half else np.uint32)
+                    wbits = want.view(np.uint16) if half else want.view(np.uint32)
+                    bad += int(np.count_nonzero(gbits[OffO:OffO + n] != wbits))
+    assert bad == 0
+
+
 def test_binary16_conversion_is_exact():
     # Every binary32 -> binary16 case the output conversion meets, through DequantizeLinear of int32 ones with one scale
     # per element (y = fl(1 * s) = s): ties to even at the normal/subnormal/zero boundaries, the largest finite value and
