@@ -626,7 +626,7 @@ def test_seeded_random_products_are_bit_exact(config):
     gemm = dict(configs(d, True))[config]
     rng = np.random.default_rng({"default": 11, "tiled only": 12, "large tile": 13}[config])
     bad, kernels = 0, set()
-    for i in range(40):
+    for i in range(120):
         kind = i % 3
         batch = int(rng.choice([1, 1, 1, 2, 3]))
         trans = bool(rng.integers(0, 2))
@@ -648,7 +648,7 @@ def test_seeded_random_products_are_bit_exact(config):
         kernels.add(kern)
         assert here == 0, f"{c.name} [{config}, {kern}]: {here} wrong"
         bad += here
-    say(f"ROW seeded random products [{config}]: 40 cases, mismatches {bad}; kernels {sorted(kernels)}")
+    say(f"ROW seeded random products [{config}]: 120 cases, mismatches {bad}; kernels {sorted(kernels)}")
 
 
 @pytest.mark.parametrize("config", ["default", "large tile"])
