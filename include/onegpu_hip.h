@@ -68,8 +68,10 @@ int og_device_limits(og_ctx *ctx, uint64_t *max_buffer_bytes, uint32_t *compute_
 /* The hipStream_t the context records on, for callers that interleave their own work. */
 int og_stream(og_ctx *ctx, void **hip_stream);
 /* Waits for everything recorded so far (GpuDevice.WaitIdle); reports a failed launch as OG_ERR_LAUNCH_FAILED, and so
- * a one-launch few-rows product whose column slab did not run on one XCD (its output may then be wrong; the context
- * uses the two-launch form from then on). */
+ * a one-launch few-rows product whose column slab did not run on one XCD (its output may then be wrong), that gave up
+ * waiting for a slab's parts (those columns unwritten), or that found the count words left by such a failure and did
+ * not run. It then clears the count words (the context's and the device's fixed ones) and the context uses the
+ * two-launch form from then on. */
 int og_sync(og_ctx *ctx);
 /* Buffers (GpuDevice.CreateBuffer / GpuBuffer<T>.Dispose, GpuBufferOfT.cs:11-89). */
 int og_alloc(og_ctx *ctx, uint64_t bytes, void **dptr);
@@ -205,7 +207,7 @@ int og_int8_gemm_requantized(og_ctx *ctx, const og_int8_gemm_params *params, uin
 
 /* ------------------------------------------------------------------ DynamicQuantizeLinear */
 
-/* DqParams, 7 words (src/RecursiveAI.OneGpu.Kernels/Shaders/DynamicQuantize.hlsl:131-140). GridX and Groups are the
+/* DqParams, 7 words (src/RecursiveAI.OneGpu.Kernels/Shaders/DynamicQuantize.hlsl:13-22). GridX and Groups are the
  * reference's dispatch sizes and are ignored: the library sizes its own grid. */
 typedef struct og_dq_params {
     uint32_t Count;     /* elements, >= 1 */
@@ -224,7 +226,7 @@ int og_dynamic_quantize(og_ctx *ctx, const og_dq_params *params, og_buffer X, og
 
 /* ------------------------------------------------------------------ DequantizeLinear / QuantizeLinear */
 
-/* DequantizeParams / QuantizeParams, 9 words (Dequantize.hlsl:9-20, Quantize.hlsl:99-110). The tensor is seen as
+/* DequantizeParams / QuantizeParams, 9 words (Dequantize.hlsl:9-20, Quantize.hlsl:10-21). The tensor is seen as
  * [outer, AxisLen, Inner]; Flags bit 0 per axis, bit 1 zero point given. GridX is ignored. */
 typedef struct og_dequant_params {
     uint32_t Count, OffX, OffO, OffS, OffZ, GridX, Flags, AxisLen, Inner;
@@ -329,6 +331,18 @@ int og_util_synth(og_ctx *ctx, int kind, uint64_t seed, uint32_t tensor, og_buff
 int og_util_col_absmax_scale(og_ctx *ctx, og_buffer W, uint32_t rows, uint32_t cols, float divisor, og_buffer scale);
 /* out[i] = fl(a[0] * b[i]) for i < n (the on-device scale product of the dynamic int8 chain). */
 int og_util_scale_product(og_ctx *ctx, og_buffer a, og_buffer b, uint32_t n, og_buffer out);
+
+/* ------------------------------------------------------------------ test hooks
+ * (no counterpart in the reference: they let a test drive the failure path of the one-launch few-rows product,
+ * "mfma-i8-rows16-xcd", from the host, with every kernel still ending normally) */
+
+/* Polls of a column slab's part count before that kernel's finishing tile gives up on ctx's later products (default
+ * 4194304). 0: the finishing tile gives up at once, leaving its columns of C unwritten; og_sync then reports
+ * OG_ERR_LAUNCH_FAILED, clears the count words and the context uses the two-launch form. */
+int og_test_set_spin_limit(og_ctx *ctx, uint32_t polls);
+/* How many of the count words are non-zero: ctx's own, and the device's fixed ones (og_int8_gemm_noalloc). Waits for
+ * ctx's stream. */
+int og_test_nonzero_words(og_ctx *ctx, uint64_t *context_words, uint64_t *fixed_words);
 
 #ifdef __cplusplus
 }

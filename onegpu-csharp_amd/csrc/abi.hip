@@ -27,6 +27,8 @@ struct og_ctx {
     uint64_t xcd_word_count = 0;
     uint32_t *xcd_flag = nullptr;
     bool xcd_local = false;
+    // Polls of a slab's count before that kernel's finishing tile gives up (og_test_set_spin_limit changes it).
+    uint32_t spin_limit = og::kGemvSpinLimit;
     // og_int8_gemm_noalloc's fixed scratch on this device (og::noalloc_scratch_setup).
     uint8_t *noalloc_scratch = nullptr;
     std::string error;
@@ -303,16 +305,26 @@ int og_sync(og_ctx *ctx)
     int st = hip_status(ctx, hipStreamSynchronize(ctx->stream), "og_sync");
     if (st == OG_OK && ctx->xcd_flag && __atomic_load_n(ctx->xcd_flag, __ATOMIC_ACQUIRE) != 0) {
         // A one-launch few-rows product found a column slab's tiles on different XCDs (flag 1: its sums may be
-        // wrong) or gave up waiting for a slab's parts (flag 2: that slab's columns of C were not written). The
-        // context stops using that kernel.
+        // wrong), gave up waiting for a slab's parts (flag 2: that slab's columns of C were not written), or found
+        // the words poisoned by such a failure (flag 3: not run). Tiles may have counted into the words after the
+        // failure, so the words this context's products use are cleared, the device's fixed ones too (a product of
+        // og_int8_gemm_noalloc may have been the one that failed), and the context stops using that kernel.
         const uint32_t why = *ctx->xcd_flag;
-        *ctx->xcd_flag = 0;
         ctx->xcd_local = false;
+        hipError_t e = hipSuccess;
+        if (ctx->xcd_words) e = og::launch_fill_bytes(ctx->xcd_words, 0, ctx->xcd_word_count * 8, ctx->stream);
+        if (e == hipSuccess && ctx->noalloc_scratch)
+            e = og::launch_fill_bytes(ctx->noalloc_scratch, 0, og::kNoAllocWordBytes, ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        __atomic_store_n(ctx->xcd_flag, 0u, __ATOMIC_RELEASE);
+        if (e != hipSuccess) return hip_status(ctx, e, "og_sync");
         return fail(ctx, OG_ERR_LAUNCH_FAILED, nullptr,
-                    why == 2 ? "og_sync: a one-launch few-rows product timed out waiting for a column slab's parts; "
-                               "its output is incomplete and the two-launch form is used from now on"
-                             : "og_sync: a one-launch few-rows product ran a column slab's tiles on different XCDs; "
-                               "its output may be wrong and the two-launch form is used from now on");
+                    why == 2   ? "og_sync: a one-launch few-rows product timed out waiting for a column slab's parts; "
+                                 "its output is incomplete and the two-launch form is used from now on"
+                    : why == 3 ? "og_sync: a one-launch few-rows product found its count words left by an earlier "
+                                 "failed product and did not run; the two-launch form is used from now on"
+                               : "og_sync: a one-launch few-rows product ran a column slab's tiles on different XCDs; "
+                                 "its output may be wrong and the two-launch form is used from now on");
     }
     return st == OG_OK ? ok(ctx) : st;
 }
@@ -599,8 +611,11 @@ static int launch_product(og_ctx *ctx, const og::GemmArgs &g, bool fixed = false
     og::GemmKernel k = og::choose_gemm_kernel(g.M, g.N, g.K, g.batch, g.flags);
     if ((k == og::GemmKernel::Skinny || k == og::GemmKernel::SkinnyDirect) && !(g.flags & OG_GEMM_NO_STREAM) &&
         og::gemv_tiles_ok(g))
-        k = ctx->xcd_local && !(g.flags & OG_GEMM_TWO_PASS) && og::gemv_xcd_ok(g) ? og::GemmKernel::RowXcd
-                                                                                 : og::GemmKernel::RowTiles;
+        // A raised flag that og_sync has not seen yet already rules the one-launch form out.
+        k = ctx->xcd_local && __atomic_load_n(ctx->xcd_flag, __ATOMIC_ACQUIRE) == 0 && !(g.flags & OG_GEMM_TWO_PASS) &&
+                    og::gemv_xcd_ok(g)
+                ? og::GemmKernel::RowXcd
+                : og::GemmKernel::RowTiles;
     switch (k) {
     case og::GemmKernel::Portable:
         st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_portable(g, ctx->stream, n); });
@@ -627,7 +642,7 @@ static int launch_product(og_ctx *ctx, const og::GemmArgs &g, bool fixed = false
         st = scratch_for(ctx, sc, og::gemv_xcd_workspace_bytes(g), og::gemv_xcd_words(g));
         if (st != OG_OK) return st;
         st = launch(ctx, "og_int8_gemm", [&](const char **n) {
-            return og::launch_gemv_xcd(g, sc.ws.partials, sc.words, ctx->xcd_flag, ctx->stream, n);
+            return og::launch_gemv_xcd(g, sc.ws.partials, sc.words, ctx->xcd_flag, ctx->spin_limit, ctx->stream, n);
         });
         break;
     case og::GemmKernel::RowTiles:
@@ -1283,6 +1298,31 @@ int og_util_scale_product(og_ctx *ctx, og_buffer a, og_buffer b, uint32_t n, og_
     (void)hipSetDevice(ctx->device);
     int st = launch(ctx, "og_util_scale_product", [&](const char **k) { *k = "scale-product"; return og::launch_scale_product(static_cast<const float *>(a.ptr), static_cast<const float *>(b.ptr), n, static_cast<float *>(out.ptr), ctx->stream); });
     return st == OG_OK ? ok(ctx) : st;
+}
+
+// ------------------------------------------------------------------ test hooks
+
+int og_test_set_spin_limit(og_ctx *ctx, uint32_t polls)
+{
+    if (!ctx) return fail(ctx, OG_ERR_INVALID_ARG, "ctx", "null context");
+    ctx->spin_limit = polls;
+    return ok(ctx);
+}
+
+int og_test_nonzero_words(og_ctx *ctx, uint64_t *context_words, uint64_t *fixed_words)
+{
+    if (!ctx || !context_words || !fixed_words) return fail(ctx, OG_ERR_INVALID_ARG, "ctx", "null context or pointer");
+    (void)hipSetDevice(ctx->device);
+    auto count = [&](const void *dev, uint64_t words, uint64_t *out) {
+        std::vector<unsigned long long> h(words);
+        hipError_t e = words ? hipMemcpyAsync(h.data(), dev, words * 8, hipMemcpyDeviceToHost, ctx->stream) : hipSuccess;
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        *out = (uint64_t)std::count_if(h.begin(), h.end(), [](unsigned long long w) { return w != 0; });
+        return e;
+    };
+    hipError_t e = count(ctx->xcd_words, ctx->xcd_words ? ctx->xcd_word_count : 0, context_words);
+    if (e == hipSuccess) e = count(ctx->noalloc_scratch, ctx->noalloc_scratch ? og::kNoAllocWordBytes / 8 : 0, fixed_words);
+    return e == hipSuccess ? ok(ctx) : hip_status(ctx, e, "og_test_nonzero_words");
 }
 
 }  // extern "C"

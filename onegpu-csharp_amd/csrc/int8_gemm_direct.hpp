@@ -172,7 +172,8 @@ __device__ __forceinline__ void static_for(F &&f)
 
 // FLIP_A / FLIP_B: the operand is unsigned (moved to the signed domain fragment by fragment). SUM_A / SUM_B: the row
 // sums of A / column sums of B are needed (the other operand's zero point in the signed domain can be non-zero).
-template <int BT, bool TRANS_B, bool SUM_A, bool SUM_B, bool FLIP_A, bool FLIP_B, int WAVES = 4>
+// PP: the 256 tile on 8 waves in ping-pong order (below) instead of the block-interleaved stage loop.
+template <int BT, bool TRANS_B, bool SUM_A, bool SUM_B, bool FLIP_A, bool FLIP_B, int WAVES = 4, bool PP = false>
 // ksplit > 1: the product is cut along K into slices of kslice bytes (a multiple of 64); g.batch counts batch entries
 // times slices, and slice kc of batch entry b computes the int32 sums of its k range with the zero points applied
 // (every correction term is linear in the slice) into batch entry b * ksplit + kc of C, which is then a dense int32
@@ -323,6 +324,135 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
     for (int j = 0; j < FN; j++) cs[j] = 0;
     const int32_t nk = K / DBK;   // K is a multiple of DBK here
 
+    if constexpr (PP) {
+        // Ping-pong: waves 0-3 (group 0, rows 0-127 of the tile) and 4-7 (group 1, rows 128-255) put one wave of each
+        // group on every SIMD, and the two groups take turns: while one group's waves issue a stage's 16 MFMAs (512
+        // cycles of the SIMD's matrix core), the other group's read their fragments of the stage they multiply next,
+        // move them to the signed domain, form their byte sums and issue their half of a later stage's DMA. A barrier
+        // ends each such phase, two a stage, so the matrix core of every SIMD always has one wave feeding it.
+        //   phase 2t:     group 0 multiplies stage t;  group 1 issues A of stage t + 4 and reads stage t;
+        //   phase 2t + 1: group 1 multiplies stage t;  group 0 issues B of stage t + 4 and reads stage t + 1.
+        // Stage t + 4 goes into the buffer of stage t - 1, which both groups finished reading by phase 2t - 2. Stage
+        // t + 1 must have landed before phase 2t + 1, where group 0 reads it: at the end of phase 2t, group 1 (A of
+        // stages t + 1 .. t + 4 outstanding) and group 0 (B of t + 1 .. t + 3) each wait for their loads of stage
+        // t + 1, before the barrier that lets group 0 read it.
+        static_assert(BT == 256 && WAVES == 8 && FM == 2 && FN == 4 && WGN == 2, "the ping-pong layout");
+        constexpr int PD = NS - 1;   // stages in flight beyond the one being read
+        constexpr int GL = 4;        // DMA loads of a group's thread a stage: one operand (16 KB) over 256 threads
+        static_assert(A_STAGE / 16 / 256 == GL && B_STAGE / 16 / 256 == GL, "half a stage a group");
+        auto pp = [&](auto wm_tag, auto wn_tag) {
+            constexpr int WM = decltype(wm_tag)::value, WN = decltype(wn_tag)::value, GRP = WM >> 1;
+            // Byte sums: row block WN of this wave's rows, column block WM of its columns (one wave each).
+            constexpr int SAR = SUM_A ? WN : -1, SBR = SUM_B ? WM : -1;
+            const int lw = wave & 3;
+            const uint32_t lds_l = lds_addr(smem) + (uint32_t)lw * 1024u;
+            // The group's operand: load i of local wave lw fills 1 KB at (4 i + lw) KB of its tile (group 1: A;
+            // group 0: B).
+            uint32_t off_g[GL];
+#pragma unroll
+            for (int i = 0; i < GL; i++) {
+                const int s = (i * 4 + lw) * 64 + lane;
+                if constexpr (GRP == 1 || TRANS_B) {
+                    const int r = s >> 2, q = s & 3;
+                    off_g[i] = (uint32_t)r * (uint32_t)(GRP == 1 ? lda : ldb) + 16u * (uint32_t)a_pos(r, q);
+                } else {
+                    const int k = s / (DBN / 16), q = s % (DBN / 16);
+                    off_g[i] = (uint32_t)k * (uint32_t)ldb + 16u * (uint32_t)b_pos<BT>(k, q);
+                }
+            }
+            auto issue = [&](auto u_tag, int32_t st) {
+                constexpr int U = decltype(u_tag)::value;
+                const StageRsrc rr = stage_rsrc(st * DBK);
+                static_for<0, GL>([&](auto i_tag) {
+                    constexpr int I = decltype(i_tag)::value;
+                    if constexpr (GRP == 1) dma16<U * STAGE + I * 4096>(rr.a, lds_l, off_g[I]);
+                    else dma16<U * STAGE + A_STAGE + I * 4096>(rr.b, lds_l, off_g[I]);
+                });
+            };
+            // The fragments of the next stage this wave multiplies, in the signed domain: [k half][block].
+            v4i af[2][2], bf[2][FN];
+            auto fetch = [&](auto u_tag) {
+                constexpr int U = decltype(u_tag)::value;
+                v4i ar[2][2], br[2][FN];
+#pragma unroll
+                for (int ks = 0; ks < 2; ks++) {
+#pragma unroll
+                    for (int i = 0; i < 2; i++) ar[ks][i] = read_a(U, i, ks);
+#pragma unroll
+                    for (int j = 0; j < FN; j++) br[ks][j] = read_b(U, j, ks);
+                }
+#pragma unroll
+                for (int ks = 0; ks < 2; ks++) {
+                    if constexpr (SAR >= 0)
+                        rs[SAR] = sad16(FLIP_A ? ar[ks][SAR] : (ar[ks][SAR] ^ (int32_t)0x80808080), rs[SAR]);
+                    if constexpr (SBR >= 0)
+                        cs[SBR] = sad16(FLIP_B ? br[ks][SBR] : (br[ks][SBR] ^ (int32_t)0x80808080), cs[SBR]);
+#pragma unroll
+                    for (int i = 0; i < 2; i++) af[ks][i] = to_signed<FLIP_A>(ar[ks][i]);
+#pragma unroll
+                    for (int j = 0; j < FN; j++) bf[ks][j] = to_signed<FLIP_B>(br[ks][j]);
+                }
+            };
+            auto multiply = [&]() {
+#pragma unroll
+                for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+                    for (int i = 0; i < 2; i++)
+#pragma unroll
+                        for (int j = 0; j < FN; j++) acc[i][j] = mfma32(af[ks][i], bf[ks][j], acc[i][j]);
+            };
+            auto stage = [&](auto u_tag, int32_t t) {
+                constexpr int U = decltype(u_tag)::value, DU = (U + PD) % NS, NU = (U + 1) % NS;
+                // phase 2t
+                if constexpr (GRP == 0) {
+                    multiply();
+                    __builtin_amdgcn_sched_barrier(0);
+                    wait_vm_lgkm_barrier<GL * (PD - 2)>();   // this wave's B of stage t + 1 landed
+                } else {
+                    issue(std::integral_constant<int, DU>{}, t + PD);
+                    fetch(u_tag);
+                    __builtin_amdgcn_sched_barrier(0);
+                    wait_vm_lgkm_barrier<GL * (PD - 1)>();   // this wave's A of stage t + 1 landed
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                // phase 2t + 1
+                if constexpr (GRP == 1) {
+                    multiply();
+                } else {
+                    issue(std::integral_constant<int, DU>{}, t + PD);
+                    if (t + 1 < nk) fetch(std::integral_constant<int, NU>{});   // (past the last stage: nothing)
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                wait_lgkm_barrier();
+                __builtin_amdgcn_sched_barrier(0);
+            };
+            // Prologue: stages 0 .. PD - 1 in flight (each group its operand); stage 0 landed; group 0 reads it.
+            static_for<0, PD>([&](auto u_tag) { issue(u_tag, decltype(u_tag)::value); });
+            wait_vm_barrier<GL * (PD - 1)>();
+            if constexpr (GRP == 0) fetch(std::integral_constant<int, 0>{});
+            __builtin_amdgcn_sched_barrier(0);
+            wait_lgkm_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            static_assert(NS == 5, "the loop below is unrolled for 5 stages");
+            for (int32_t kt = 0; kt < nk; kt += NS) {
+                static_for<0, NS>([&](auto u_tag) {
+                    if (kt + decltype(u_tag)::value < nk) stage(u_tag, kt + decltype(u_tag)::value);
+                });
+            }
+        };
+        // One instantiation per wave role (wm, and wn when A's row sums are needed), uniform across each wave.
+        static_for<0, 4>([&](auto wm_tag) {
+            if (wm == decltype(wm_tag)::value) {
+                if constexpr (SUM_A) {
+                    static_for<0, 2>([&](auto wn_tag) {
+                        if (wn == decltype(wn_tag)::value) pp(wm_tag, wn_tag);
+                    });
+                } else {
+                    pp(wm_tag, std::integral_constant<int, 0>{});
+                }
+            }
+        });
+    } else {
     // How far ahead the DMA runs. With one block a k half (HB = 1) a stage's buffer is read only in its first block,
     // so once the waves meet in stage s (each having finished its LDS reads) the buffer of stage s itself can take stage
     // s + NS: every buffer of the ring holds a stage in flight. With more blocks a k half, the second half's first
@@ -436,6 +566,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
         });
     } else {
         with_roles(std::integral_constant<int, -1>{});
+    }
     }
     // Every DMA landed and every wave done with the stage buffers before the epilogue's arrays take their place.
     wait_vm<0>();

@@ -23,6 +23,12 @@
 // (HW_REG_XCC_ID), so the finishing tile checks that every tile of its slab shared its L2; if not, it raises a flag in
 // host memory that og_sync reports (og_init runs this kernel only after a probe launch has shown the mapping). The
 // wait is bounded: past the bound the tile raises the flag and leaves its columns of C unwritten.
+//
+// A failed hand-off leaves count words behind (tiles still count after the finishing tile gave up, and a slab split
+// over two XCDs has counted in two L2s). So the finishing tile that fails also sets the poison word (word 0 of
+// `words`, an agent-scope store), and every later launch's finishing tiles read it first (agent scope, coherent
+// across the XCDs; a launch starts after the previous one on the stream has ended) and, finding it set, raise the
+// flag (3) without reading any part. og_sync clears all the words (poison included) once it has seen the flag.
 //        sum (s - z')(t - w') = sum s t - w' sum s - z' sum t + K z' w'   (mod 2^32; Int8GemmDot.hlsl:1-11)
 #include <algorithm>
 #include <type_traits>
@@ -46,7 +52,6 @@ constexpr int GX_LPS = 64 / GX_ROWS_PER_LOAD;                 // loads a step (2
 constexpr int GX_CPW = GX_CPR / 4;                            // chunks a wave computes (2)
 constexpr int GX_STAGE = 64 * GX_COLS;                        // bytes of one step in LDS
 constexpr int GX_RED = 17 * GX_COLS + 16;                     // the finishing tile's sums (ints)
-constexpr uint32_t GX_SPIN_LIMIT = 1u << 22;                  // polls of the part count before giving up
 static_assert(GX_CPR == 8 && GX_LPS * GX_ROWS_PER_LOAD == 64, "the staging layout below is for 128-byte rows");
 
 __device__ __forceinline__ v4i gx_load(__amdgpu_buffer_rsrc_t r, uint32_t off)
@@ -91,10 +96,13 @@ __host__ __device__ inline int64_t gemv_xcd_part(int32_t M) { return (int64_t)(M
 
 // Workgroup id x: XCD x % 8 takes slabs [x8 * Q / 8, (x8 + 1) * Q / 8) of the Q = batch * slabs column slabs; its
 // j-th workgroup (j = x / 8) takes slab j % nq of them (slab-fastest, so the tiles running together cover whole rows
-// of B) and row band j / nq. Word q of `words` counts slab q's stored parts.
+// of B) and row band j / nq. Word 1 + q of `words` counts slab q's stored parts; word 0 is the poison word.
+// spin_limit: polls of the count before the finishing tile gives up (0: it gives up at once, without reading the
+// count; the library's tests use that to drive the recovery path).
 template <bool SUM_A, bool SUM_B, bool FLIP_A, bool FLIP_B, bool ROWS16>
 __global__ __launch_bounds__(GX_THREADS) void k_gemv_xcd(GemmArgs g, int32_t slabs, int32_t nkc, int32_t qtotal,
-                                                         int32_t *parts, unsigned long long *words, uint32_t *flag)
+                                                         int32_t *parts, unsigned long long *words, uint32_t *flag,
+                                                         uint32_t spin_limit)
 {
     __shared__ __attribute__((aligned(1024))) int32_t smem[(2 * GX_STAGE / 4) > GX_RED ? (2 * GX_STAGE / 4) : GX_RED];
     __shared__ uint32_t s_ok;
@@ -207,7 +215,7 @@ __global__ __launch_bounds__(GX_THREADS) void k_gemv_xcd(GemmArgs g, int32_t sla
         }
         if (SUM_A && wave == 0 && g4 == 0) dst[R * GX_COLS + i16] = (int32_t)rowsum;
     };
-    unsigned long long *const word = words + q;
+    unsigned long long *const poison = words, *const word = words + 1 + q;
     if (kc != nkc - 1) {
         put_part(parts + ((int64_t)q * nkc + kc) * pstride);
         // Counted once this wave's stores are in L2 (vmcnt drains) and every wave's are, in the 7-bit field of the
@@ -218,6 +226,9 @@ __global__ __launch_bounds__(GX_THREADS) void k_gemv_xcd(GemmArgs g, int32_t sla
             __hip_atomic_fetch_add(word, 1ull << (7 * gx_xcc_id()), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         return;
     }
+    // Whether an earlier launch failed its hand-off: requested now, used after the epilogue operands are in flight.
+    const unsigned long long poisoned =
+        tid == 0 ? __hip_atomic_load(poison, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
     gx_lds_barrier();   // every wave's MFMAs are done, so their reads of the staging buffers too
     put_part(smem);
 
@@ -255,22 +266,30 @@ __global__ __launch_bounds__(GX_THREADS) void k_gemv_xcd(GemmArgs g, int32_t sla
     // performed in L2: an idempotent read-modify-write may be compiled to a plain load, which the L1 can answer);
     // bits 0 .. 55 are the eight XCDs' 7-bit counts.
     if (tid == 0) {
-        const uint32_t xcc = gx_xcc_id();
-        uint32_t polls = 0, total = 0;
-        unsigned long long now = 0;
-        for (;;) {
-            now = __hip_atomic_fetch_add(word, 1ull << 56, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            total = 0;
+        if (poisoned) {
+            // The words are stale: raise the flag and leave this slab's columns of C unwritten.
+            *flag = 3u;
+            s_ok = 0u;
+        } else {
+            const uint32_t xcc = gx_xcc_id();
+            uint32_t polls = 0, total = 0;
+            unsigned long long now = 0;
+            while (spin_limit != 0) {
+                now = __hip_atomic_fetch_add(word, 1ull << 56, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                total = 0;
 #pragma unroll
-            for (int x = 0; x < 8; x++) total += (uint32_t)(now >> (7 * x)) & 127u;
-            if (total == (uint32_t)(nkc - 1) || ++polls == GX_SPIN_LIMIT) break;
-            __builtin_amdgcn_s_sleep(1);
+                for (int x = 0; x < 8; x++) total += (uint32_t)(now >> (7 * x)) & 127u;
+                if (total == (uint32_t)(nkc - 1) || ++polls >= spin_limit) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+            const bool done = spin_limit != 0 && total == (uint32_t)(nkc - 1);
+            const bool here = (now & ((1ull << 56) - 1)) == ((unsigned long long)(nkc - 1) << (7 * xcc));
+            if (!done) *flag = 2u;
+            else if (!here) *flag = 1u;   // some tile of the slab ran on another XCD: its sums may be wrong
+            if (!done || !here) __hip_atomic_store(poison, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *word = 0ull;   // every other tile of the slab has counted its part: free for the next product
+            s_ok = done ? 1u : 0u;
         }
-        const bool done = total == (uint32_t)(nkc - 1);
-        if (!done) *flag = 2u;
-        else if ((now & ((1ull << 56) - 1)) != ((unsigned long long)(nkc - 1) << (7 * xcc))) *flag = 1u;   // elsewhere
-        *word = 0ull;   // every other tile of the slab has counted its part: free for the next product
-        s_ok = done ? 1u : 0u;
     }
     __syncthreads();
     if (!s_ok) return;
@@ -382,11 +401,11 @@ uint64_t gemv_xcd_workspace_bytes(const GemmArgs &g)
 
 uint64_t gemv_xcd_words(const GemmArgs &g)
 {
-    return (uint64_t)g.batch * ((g.N + GX_COLS - 1) / GX_COLS);
+    return 1 + (uint64_t)g.batch * ((g.N + GX_COLS - 1) / GX_COLS);   // the poison word, then one a slab
 }
 
 hipError_t launch_gemv_xcd(const GemmArgs &g, int32_t *parts, unsigned long long *words, uint32_t *flag,
-                           hipStream_t s, const char **kernel)
+                           uint32_t spin_limit, hipStream_t s, const char **kernel)
 {
     const int32_t slabs = (g.N + GX_COLS - 1) / GX_COLS, nkc = (g.K + GX_KT - 1) / GX_KT;
     const int32_t q = g.batch * slabs;
@@ -398,10 +417,10 @@ hipError_t launch_gemv_xcd(const GemmArgs &g, int32_t *parts, unsigned long long
     do {                                                                                                          \
         if (SB && g.M == 16)                                                                                      \
             hipLaunchKernelGGL((k_gemv_xcd<SA, SB, FA, FB, true>), grid, block, 0, s, g, slabs, nkc, q,           \
-                               parts, words, flag);                                                               \
+                               parts, words, flag, spin_limit);                                                               \
         else                                                                                                      \
             hipLaunchKernelGGL((k_gemv_xcd<SA, SB, FA, FB, false>), grid, block, 0, s, g, slabs, nkc, q,          \
-                               parts, words, flag);                                                               \
+                               parts, words, flag, spin_limit);                                                               \
     } while (0)
     if (fa && fb) OG_GX(true, true, true, true);
     else if (fa) { if (sa) OG_GX(true, true, true, false); else OG_GX(false, true, true, false); }

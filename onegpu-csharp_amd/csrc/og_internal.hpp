@@ -99,13 +99,16 @@ hipError_t launch_gemv_tiles(const GemmArgs &g, const Workspace &ws, hipStream_t
 // The same tiles in one launch: every tile but the last row band of a column slab stores its part into `parts` and
 // counts it in the slab's word of `words`; the last row band's tile waits for the count, adds the parts and stores C.
 // The tiles of a slab run on one XCD (ids equal modulo 8), so the parts pass through that XCD's L2 alone. `words`
-// (gemv_xcd_words 64-bit words) must be zero before the launch and is zero again after it; `flag` is set to 1 if a
-// slab's tiles did not share an XCD, 2 if a slab's parts were never all counted (its columns of C not written).
+// (gemv_xcd_words 64-bit words: a poison word, then one a slab) must be zero before the launch and the slab words are
+// zero again after it; `flag` is set to 1 if a slab's tiles did not share an XCD, 2 if a slab's parts were never all
+// counted within `spin_limit` polls (its columns of C not written), 3 if an earlier launch on these words failed (the
+// poison word was set: nothing was read); after 1 or 2 the poison word is set and every word must be cleared.
+constexpr uint32_t kGemvSpinLimit = 1u << 22;
 bool gemv_xcd_ok(const GemmArgs &g);
 uint64_t gemv_xcd_workspace_bytes(const GemmArgs &g);
 uint64_t gemv_xcd_words(const GemmArgs &g);
 hipError_t launch_gemv_xcd(const GemmArgs &g, int32_t *parts, unsigned long long *words, uint32_t *flag,
-                           hipStream_t s, const char **kernel);
+                           uint32_t spin_limit, hipStream_t s, const char **kernel);
 // out[x] = the XCD (HW_REG_XCC_ID) workgroup x of a `groups`-workgroup launch ran on.
 hipError_t launch_xcc_probe(uint32_t *out, uint32_t groups, hipStream_t s);
 

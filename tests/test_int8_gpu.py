@@ -142,8 +142,12 @@ def test_float_and_requantized_forms_are_bit_exact(config):
 
 # Shapes that reach every kernel: few rows on the tiled few-rows kernel (or split k), the 128 and 256 direct kernels
 # (ragged M included), the register-staged 128 tile (K = 96), the generic kernel (unaligned rows), tiny products.
+# The last three reach the one-launch few-rows kernel with its k-slices handed to the finishing tile (16 to 36 column
+# slabs of 2 to 8 row bands), so its epilogues are checked after a real hand-off.
 REQUANT_KERNEL_SHAPES = [(1, 1, 1), (5, 7, 9), (4, 272, 512), (16, 256, 1024), (64, 64, 96), (33, 257, 77),
-                         (128, 384, 384), (130, 256, 512), (2, 8192, 128), (96, 208, 320), (3, 4608, 272)]
+                         (128, 384, 384), (130, 256, 512), (2, 8192, 128), (96, 208, 320), (3, 4608, 272),
+                         (3, 4608, 1024), (4, 2048, 4096), (16, 2048, 2048)]
+HANDOFF_SHAPES = REQUANT_KERNEL_SHAPES[-3:]
 
 
 @pytest.mark.parametrize("fused", [True, False], ids=["one launch", "two passes"])
@@ -162,6 +166,8 @@ def test_requantized_product_on_every_kernel(config, fused):
             bad += _requant_case(d, gemm, m, n, k, vec, unsigned, zero, (seed & 1) == 0, seed, (seed & 2) != 0,
                                  (seed & 4) != 0)
             kernels.add(d.LastKernel)
+            if fused and config == "default" and (m, n, k) in HANDOFF_SHAPES:
+                assert d.LastKernel == "mfma-i8-rows16-xcd", d.LastKernel
             seed += 1
     say(f"ROW requantized [{config}, {'one launch' if fused else 'two passes'}] wrong bytes {bad}; kernels "
         f"{sorted(kernels)}")
@@ -213,6 +219,8 @@ def test_scaled_float_product_on_every_kernel(config):
             same = np.where(np.isnan(expected), np.isnan(got), got.view(np.uint32) == expected.view(np.uint32))
             bad += int(np.count_nonzero(~same))
             kernels.add(d.LastKernel)
+            if config == "default" and (m, n, k) in HANDOFF_SHAPES:
+                assert d.LastKernel == "mfma-i8-rows16-xcd", d.LastKernel
             seed += 1
     say(f"ROW scaled float [{config}] wrong values {bad}; kernels {sorted(kernels)}")
     assert bad == 0
@@ -586,8 +594,109 @@ def test_few_rows_kernels_are_bit_exact(config):
         bad_total += _float_case(d, gemm, 4, 256, 128, vec, True, True, 77 + vec)
         bad_total += _float_case(d, gemm, 16, 1024, 512, vec, False, True, 79 + vec)
         bad_total += _float_case(d, gemm, 3, 8192, 192, vec, True, True, 81 + vec)
+        # Column slabs of 8, 2 and 4 row bands: the finishing tile's float store after a real hand-off.
+        for j, (m, n, k) in enumerate(HANDOFF_SHAPES):
+            bad_total += _float_case(d, gemm, m, n, k, vec, j != 1, j != 0, 83 + 2 * j + vec)
+            if config == "tiles":
+                assert d.LastKernel == "mfma-i8-rows16-xcd", d.LastKernel
     say(f"ROW int8 gemm | few rows [{config}] | mismatches {bad_total}; kernels {sorted(kernels)}")
     assert bad_total == 0
+
+
+@pytest.mark.parametrize("m", [1, 4, 16])
+def test_c3_matmul_integer_to_float_few_rows(m):
+    # Configuration 3 as the decode layer runs it: DynamicQuantizeLinear of N(0, 1) activations [m x 4096], then
+    # MatMulIntegerToFloat with int8 weights [4096 x 11008] quantized symmetric per column from N(0, 0.02), the column
+    # scale fl(actScale * wScale[n]) made in the product's epilogue (EncodeFloatScaled) and, as the reference chains
+    # it, the scale vector made first (EncodeFloat). The one-launch few-rows kernel hands 8 k-slices of each of 86
+    # column slabs to the slab's finishing tile. Against the oracle: DQ's bytes, scale and zero point, then every
+    # output bit.
+    K, N = 4096, 11008
+    d = device()
+    rng = np.random.default_rng(900 + m)
+    x = rng.standard_normal(m * K).astype(np.float32)
+    w = (rng.standard_normal(K * N) * 0.02).astype(np.float32).reshape(K, N)
+    wscale = (np.abs(w).max(axis=0).astype(np.float32) / np.float32(127)).astype(np.float32)
+    wq = oracle.quantize(w.ravel(), wscale, True, per_axis=True, axis_len=N, inner=1).view(np.int8)
+    y_want, s_want, z_want = oracle.dynamic_quantize(x)
+    bx, bq, bws = d.CreateBuffer(x), d.CreateBuffer(wq), d.CreateBuffer(wscale)
+    by = d.CreateBufferOf(og.ElementType.UInt8, m * K)
+    bs, bz = d.CreateBufferOf(og.ElementType.Float32, 1), d.CreateBufferOf(og.ElementType.UInt8, 4)
+    say(f"c3 float m {m}: DynamicQuantizeLinear")
+    run(d, lambda e: og.DynamicQuantizeKernels(d).Encode(e, bx, 0, m * K, by, 0, bs, 0, bz, 0))
+    y, s, z = by.Read()[:m * K], np.float32(bs.Read()[0]), int(bz.Read()[0])
+    assert np.array_equal(y, y_want) and s == np.float32(s_want) and z == z_want
+    sums = oracle.int8_gemm(cases.problem(m, N, K), y, False, wq.view(np.uint8), True, (np.array([z], np.uint8), False, 0))
+    colscale = (s * wscale).astype(np.float32)
+    want = oracle.float_epilogue(sums, N, colscale, True)
+    gemm = og.Int8Gemm(d)
+    p = og.Int8GemmProblem(m, N, K)
+    for form in ("scaled in the epilogue", "scale vector first"):
+        bc = d.CreateBufferOf(og.ElementType.Float32, m * N)
+        say(f"c3 float m {m}: MatMulIntegerToFloat, {form}")
+        if form == "scaled in the epilogue":
+            run(d, lambda e: gemm.EncodeFloatScaled(e, p, by, bq, bc, og.Int8Operand(bs, 0), og.Int8Operand(bws, 0, True),
+                                                    og.Int8Operand(bz, 0)))
+        else:
+            bsc = d.CreateBufferOf(og.ElementType.Float32, N)
+            run(d, lambda e: (e.RecordScaleProduct(bs, bws, N, bsc),
+                              gemm.EncodeFloat(e, p, by, bq, bc, og.Int8Operand(bsc, 0, True), og.Int8Operand(bz, 0))))
+        d.WaitIdle()
+        assert d.LastKernel == "mfma-i8-rows16-xcd", d.LastKernel
+        got = bc.Read()
+        bad = int(np.count_nonzero(got.view(np.uint32) != want.view(np.uint32)))
+        say(f"ROW c3 MatMulIntegerToFloat m {m} ({form}): {bad} wrong values")
+        assert bad == 0
+
+
+@pytest.mark.parametrize("fused", [True, False], ids=["one launch", "two passes"])
+@pytest.mark.parametrize("shape", [(64, 256, 512, 128), (4, 4096, 2048, 4096)], ids=["tiles", "few rows"])
+def test_chained_qlinear_matmul(shape, fused):
+    # The QLinearMatMul model format (docs/kernels.md:160-162; Int8Tests.cs:375-466 per layer): layer 1's requantized
+    # uint8 output, with its zero point, is layer 2's A operand with that zero point; layer 2 requantizes to int8. The
+    # two-pass form places both layers' int32 sums in one caller scratch buffer (Int8Scratch, at element offsets past
+    # each other). Every byte of both layers against the oracle.
+    m, k1, n1, n2 = shape
+    d = device()
+    rng = np.random.default_rng(950 + m)
+    a = rng.integers(0, 256, m * k1, dtype=np.uint8)
+    za = np.array([rng.integers(90, 160)] * 4, np.uint8)
+    b1 = rng.integers(-127, 128, k1 * n1, dtype=np.int8)
+    b2 = rng.integers(-127, 128, n1 * n2, dtype=np.int8)
+    # Multipliers that spread each layer's bytes over about +-20 around its zero point (a few saturate): a sum of K
+    # products of a - za (RMS ~74) and b (RMS ~73) with random signs spreads over about sqrt(K) * 5400.
+    mult1 = ((rng.random(n1) + 0.5) * 20.0 / (np.sqrt(k1) * 5400.0)).astype(np.float32)
+    mult2 = np.array([15.0 / (np.sqrt(n1) * 25.0 * 73.0)], np.float32)
+    zy1, zy2 = 117, -5
+    s1 = oracle.int8_gemm(cases.problem(m, n1, k1), a, False, b1.view(np.uint8), True, (za[:1], False, 0))
+    y1 = oracle.requant_array(s1, n1, mult1, True, zy1, True)
+    s2 = oracle.int8_gemm(cases.problem(m, n2, n1), y1, False, b2.view(np.uint8), True, (np.array([zy1], np.uint8), False, 0))
+    y2 = oracle.requant_array(s2, n2, mult2, False, zy2, False)
+    assert 10 < len(np.unique(y1)) and 10 < len(np.unique(y2)), "the layers' outputs span many values"
+    ba, bza, bb1, bb2 = d.CreateBuffer(a), d.CreateBuffer(za), d.CreateBuffer(b1), d.CreateBuffer(b2)
+    bm1, bm2 = d.CreateBuffer(mult1), d.CreateBuffer(mult2)
+    by1 = d.CreateBufferOf(og.ElementType.UInt8, m * n1)
+    by2 = d.CreateBufferOf(og.ElementType.Int8, m * n2)
+    bzy1 = d.CreateBuffer(np.full(4, zy1, np.uint8))
+    gemm = og.Int8Gemm(d, og.Int8GemmOptions(FusedRequantize=fused))
+    p1, p2 = og.Int8GemmProblem(m, n1, k1), og.Int8GemmProblem(m, n2, n1)
+    e1 = og.Int8Gemm.ScratchElements(p1)
+    scratch = d.CreateBufferOf(og.ElementType.Int32, e1 + og.Int8Gemm.ScratchElements(p2) + 8)
+    say(f"chained qlinear {shape} {'one launch' if fused else 'two passes'}")
+
+    def record(e):
+        gemm.EncodeRequantized(e, p1, ba, bb1, by1, og.Int8Operand(bm1, 0, True), zy1, og.Int8Operand(bza, 0),
+                               scratch=og.Int8Scratch(scratch, 0))
+        gemm.EncodeRequantized(e, p2, by1, bb2, by2, og.Int8Operand(bm2, 0), zy2, og.Int8Operand(bzy1, 0),
+                               scratch=og.Int8Scratch(scratch, e1 + 8))
+    run(d, record)
+    d.WaitIdle()
+    got1, got2 = by1.Read()[:m * n1], by2.Read().view(np.uint8)[:m * n2]
+    bad1 = int(np.count_nonzero(got1 != y1))
+    bad2 = int(np.count_nonzero(got2 != y2.view(np.uint8)))
+    say(f"ROW chained QLinearMatMul {shape} ({'one launch' if fused else 'two passes'}, {d.LastKernel}): wrong bytes "
+        f"{bad1} + {bad2}")
+    assert bad1 + bad2 == 0
 
 
 def test_golden_fixtures_on_every_kernel():

@@ -83,20 +83,35 @@ def test_noalloc_matches_the_allocating_entry_point(first, second):
         assert np.array_equal(ref, got)
 
 
-def test_noalloc_refuses_a_product_past_its_scratch():
-    # M = 16 rows over K = 65536: the one-launch few-rows kernel's parts need 86 slabs x 128 row bands x 8.8 KB,
-    # beyond the 16 MiB array: refused with OG_ERR_UNSUPPORTED (argument "scratch") before any kernel runs.
+# (label, m, n, k, batch, strideB): products that take the one-launch few-rows kernel ("mfma-i8-rows16-xcd") and need
+# more of the fixed array than it holds. Its parts: 86 column slabs x 24 row bands of 17 x 128 + 32 ints (8,832
+# bytes) = 18.2 MB, past the 16 MiB array. Its count words: one a column slab and the poison word, 1 + 96 x 86 = 8,257,
+# past the 8,192 the array holds (the 96 batch entries share one B, strideB = 0; their parts take 9.5 MB).
+REFUSED = [
+    ("parts past the array", 16, 11008, 12288, 1, 11008 * 12288),
+    ("count words past the array", 1, 11008, 512, 96, 0),
+]
+
+
+@pytest.mark.parametrize("label, m, n, k, batch, stride_b", REFUSED)
+def test_noalloc_refuses_a_product_past_its_scratch(label, m, n, k, batch, stride_b):
+    # Refused with OG_ERR_UNSUPPORTED (argument "scratch") before any kernel runs.
     d = device()
     L = _lib()
-    m, n, k = 16, 11008, 65536
-    a = np.zeros(m * k, np.uint8)
-    ba = d.CreateBuffer(a)
+    L.og_int8_gemm_kernel_name.argtypes = [ctypes.POINTER(L.GemmParams), ctypes.c_uint32, ctypes.c_char_p,
+                                           ctypes.c_size_t]
+    prm = L.GemmParams(M=m, N=n, K=k, Lda=k, Ldb=n, Flags=0x0A, StrideA=m * k, StrideB=stride_b, StrideC=m * n)
+    name = ctypes.create_string_buffer(64)
+    assert L.og_int8_gemm_kernel_name(ctypes.byref(prm), batch, name, 64) == 0
+    assert name.value.decode() == "mfma-i8-rows16-xcd", name.value
+    say(f"noalloc refusal, {label}: {batch} x {m}x{n}x{k}")
+    ba = d.CreateBuffer(np.zeros(batch * m * k, np.uint8))
     bb = d.CreateBufferOf(og.ElementType.Int8, k * n)
-    bc = d.CreateBufferOf(og.ElementType.Int32, m * n)
-    prm = L.GemmParams(M=m, N=n, K=k, Lda=k, Ldb=n, Flags=0x02, StrideC=m * n)
+    bc = d.CreateBufferOf(og.ElementType.Int32, batch * m * n)
+    bz = d.CreateBuffer(np.full(4, 128, np.uint8))
     none = L.Buf(None, 0)
-    st = L.og_int8_gemm_noalloc(d.Context, ctypes.byref(prm), 1, binding(ba), binding(bb), binding(bc), none, none,
-                                none, none, none)
+    st = L.og_int8_gemm_noalloc(d.Context, ctypes.byref(prm), batch, binding(ba), binding(bb), binding(bc),
+                                binding(bz), none, none, none, none)
     assert st == UNSUPPORTED
     assert L.og_last_error_argument(d.Context).decode() == "scratch"
     d.WaitIdle()
