@@ -328,58 +328,101 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
         // Ping-pong: waves 0-3 (group 0, rows 0-127 of the tile) and 4-7 (group 1, rows 128-255) put one wave of each
         // group on every SIMD, and the two groups take turns: while one group's waves issue a stage's 16 MFMAs (512
         // cycles of the SIMD's matrix core), the other group's read their fragments of the stage they multiply next,
-        // move them to the signed domain, form their byte sums and issue their half of a later stage's DMA. A barrier
+        // move them to the signed domain, form their byte sums and issue their share of later stages' DMA. A barrier
         // ends each such phase, two a stage, so the matrix core of every SIMD always has one wave feeding it.
-        //   phase 2t:     group 0 multiplies stage t;  group 1 issues A of stage t + 4 and reads stage t;
+        //   phase 2t:     group 0 multiplies stage t;  group 1 issues half of an A pair and reads stage t;
         //   phase 2t + 1: group 1 multiplies stage t;  group 0 issues B of stage t + 4 and reads stage t + 1.
-        // Stage t + 4 goes into the buffer of stage t - 1, which both groups finished reading by phase 2t - 2. Stage
-        // t + 1 must have landed before phase 2t + 1, where group 0 reads it: at the end of phase 2t, group 1 (A of
-        // stages t + 1 .. t + 4 outstanding) and group 0 (B of t + 1 .. t + 3) each wait for their loads of stage
-        // t + 1, before the barrier that lets group 0 read it.
-        static_assert(BT == 256 && WAVES == 8 && FM == 2 && FN == 4 && WGN == 2, "the ping-pong layout");
-        constexpr int PD = NS - 1;   // stages in flight beyond the one being read
-        constexpr int GL = 4;        // DMA loads of a group's thread a stage: one operand (16 KB) over 256 threads
-        static_assert(A_STAGE / 16 / 256 == GL && B_STAGE / 16 / 256 == GL, "half a stage a group");
+        // LDS: A in 3 pair slots of 256 rows x 128 bytes (two stages: each row a whole 128-byte line, where a 64-byte
+        // stage would fetch half lines), then B in 4 stage slots of 64 x 256 bytes. Pair q (stages 2q, 2q + 1) goes
+        // into slot q % 3 in halves of 128 rows, at phases 4q - 8 and 4q - 6, after both groups are done with pair
+        // q - 3 (read last in phase 4q - 10); B of stage t + 4 goes into slot t % 4 in phase 2t + 1, after group 1 read
+        // B of stage t in phase 2t. Stage t + 1 must have landed before phase 2t + 1, where group 0 reads it: at the
+        // end of phase 2t each group waits for its own loads of it, then meets the other.
+        // A pair slot: row r's 16-byte chunk c (k 16 c .. + 15 of the pair) at position c ^ ((r >> 1) & 7): the rows
+        // of one parity fill one 128-byte half of the 256 bytes LDS serves a cycle, so a fragment read (16 rows, one
+        // chunk) is conflict-free, and a DMA instruction writes 8 whole rows.
+        static_assert(BT == 256 && WAVES == 8 && FM == 2 && FN == 4 && WGN == 2 && NS * STAGE == 163840, "the layout");
+        constexpr int GL = 4;   // DMA loads of a group's thread a phase (16 KB over 256 threads)
+        constexpr int A_PAIR = 2 * A_STAGE, B_OFF = 3 * A_PAIR, B_SLOT = D::B_STAGE;
+        static_assert(B_OFF + 4 * B_SLOT == NS * STAGE && A_STAGE / 16 / 256 == GL && B_SLOT / 16 / 256 == GL, "slots");
         auto pp = [&](auto wm_tag, auto wn_tag) {
             constexpr int WM = decltype(wm_tag)::value, WN = decltype(wn_tag)::value, GRP = WM >> 1;
             // Byte sums: row block WN of this wave's rows, column block WM of its columns (one wave each).
             constexpr int SAR = SUM_A ? WN : -1, SBR = SUM_B ? WM : -1;
             const int lw = wave & 3;
             const uint32_t lds_l = lds_addr(smem) + (uint32_t)lw * 1024u;
-            // The group's operand: load i of local wave lw fills 1 KB at (4 i + lw) KB of its tile (group 1: A;
-            // group 0: B).
+            // This thread's global chunk offsets. Group 1, A: load i of local wave lw fills 1 KB at (4 i + lw) KB of
+            // a half pair (rows 8 (4 i + lw) + lane / 8, position lane % 8). Group 0, B: 1 KB at (4 i + lw) KB of a
+            // stage.
             uint32_t off_g[GL];
 #pragma unroll
             for (int i = 0; i < GL; i++) {
                 const int s = (i * 4 + lw) * 64 + lane;
-                if constexpr (GRP == 1 || TRANS_B) {
+                if constexpr (GRP == 1) {
+                    const int r = s >> 3, q = (s & 7) ^ ((r >> 1) & 7);
+                    off_g[i] = (uint32_t)r * (uint32_t)lda + 16u * (uint32_t)q;
+                } else if constexpr (TRANS_B) {
                     const int r = s >> 2, q = s & 3;
-                    off_g[i] = (uint32_t)r * (uint32_t)(GRP == 1 ? lda : ldb) + 16u * (uint32_t)a_pos(r, q);
+                    off_g[i] = (uint32_t)r * (uint32_t)ldb + 16u * (uint32_t)a_pos(r, q);
                 } else {
                     const int k = s / (DBN / 16), q = s % (DBN / 16);
                     off_g[i] = (uint32_t)k * (uint32_t)ldb + 16u * (uint32_t)b_pos<BT>(k, q);
                 }
             }
-            auto issue = [&](auto u_tag, int32_t st) {
-                constexpr int U = decltype(u_tag)::value;
-                const StageRsrc rr = stage_rsrc(st * DBK);
+            // Half h of A pair q (rows 128 h .. + 127, k 128 q .. + 127) into its slot; B of stage st into slot U.
+            auto issue_a = [&](int32_t q, auto h_tag) {
+                constexpr int H = decltype(h_tag)::value;
+                const int32_t k0 = min(128 * q, K), r0 = H * 128 * lda;
+                const u4w ra = drsrc(a_base + r0 + k0, a_valid - r0 - k0);
+                const uint32_t base = lds_l + (uint32_t)(q % 3) * (uint32_t)A_PAIR;
                 static_for<0, GL>([&](auto i_tag) {
                     constexpr int I = decltype(i_tag)::value;
-                    if constexpr (GRP == 1) dma16<U * STAGE + I * 4096>(rr.a, lds_l, off_g[I]);
-                    else dma16<U * STAGE + A_STAGE + I * 4096>(rr.b, lds_l, off_g[I]);
+                    dma16<H * A_STAGE + I * 4096>(ra, base, off_g[I]);
                 });
+            };
+            auto issue_b = [&](auto u_tag, int32_t st) {
+                constexpr int U = decltype(u_tag)::value;
+                const int32_t k0 = min(st * DBK, K);
+                const u4w rb = drsrc(b_base + k0 * b_step, b_valid - k0 * b_step);
+                static_for<0, GL>([&](auto i_tag) {
+                    constexpr int I = decltype(i_tag)::value;
+                    dma16<B_OFF + U * B_SLOT + I * 4096>(rb, lds_l, off_g[I]);
+                });
+            };
+            // Fragment reads of stage t: A from pair slot (t / 2) % 3, its half t % 2 (lane l: row 32 i + l % 32 of
+            // the wave's rows, chunk 4 (t % 2) + 2 ks + l / 32); B from slot t % 4 as before.
+            auto read_a_pp = [&](uint32_t slot, int half, int i, int ks) {
+                const int r = wm * WTM + 32 * i + i32, c = 4 * half + 2 * ks + h2;
+                return *reinterpret_cast<const v4i *>(smem + slot + r * 128 + 16 * (c ^ ((r >> 1) & 7)));
+            };
+            auto read_b_pp = [&](int u, int j, int ks) -> v4i {
+                const uint8_t *bs = smem + B_OFF + u * B_SLOT;
+                if constexpr (TRANS_B) {
+                    const int r = wn * WTN + 32 * j + i32;
+                    return *reinterpret_cast<const v4i *>(bs + r * 64 + 16 * a_pos(r, 2 * ks + h2));
+                } else {
+                    const int c = (wn * WTN + 32 * j + 16 * (g4 & 1)) >> 4;
+                    v2i h[2];
+#pragma unroll
+                    for (int hh = 0; hh < 2; hh++) {
+                        const int k = 32 * ks + 16 * (g4 >> 1) + 8 * hh + (i16 >> 1);
+                        h[hh] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(OG_LDS2(bs + k * DBN + 16 * b_pos<BT>(k, c) + 8 * (i16 & 1)));
+                    }
+                    return (v4i){h[0].x, h[0].y, h[1].x, h[1].y};
+                }
             };
             // The fragments of the next stage this wave multiplies, in the signed domain: [k half][block].
             v4i af[2][2], bf[2][FN];
-            auto fetch = [&](auto u_tag) {
-                constexpr int U = decltype(u_tag)::value;
+            auto fetch = [&](int32_t t, auto u_tag) {
+                constexpr int U = decltype(u_tag)::value, H = U & 1;
+                const uint32_t slot = (uint32_t)((t >> 1) % 3) * (uint32_t)A_PAIR;
                 v4i ar[2][2], br[2][FN];
 #pragma unroll
                 for (int ks = 0; ks < 2; ks++) {
 #pragma unroll
-                    for (int i = 0; i < 2; i++) ar[ks][i] = read_a(U, i, ks);
+                    for (int i = 0; i < 2; i++) ar[ks][i] = read_a_pp(slot, H, i, ks);
 #pragma unroll
-                    for (int j = 0; j < FN; j++) br[ks][j] = read_b(U, j, ks);
+                    for (int j = 0; j < FN; j++) br[ks][j] = read_b_pp(U, j, ks);
                 }
 #pragma unroll
                 for (int ks = 0; ks < 2; ks++) {
@@ -401,41 +444,52 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
 #pragma unroll
                         for (int j = 0; j < FN; j++) acc[i][j] = mfma32(af[ks][i], bf[ks][j], acc[i][j]);
             };
+            // Stage t (U = t % 4).
             auto stage = [&](auto u_tag, int32_t t) {
-                constexpr int U = decltype(u_tag)::value, DU = (U + PD) % NS, NU = (U + 1) % NS;
+                constexpr int U = decltype(u_tag)::value, H = U & 1;
                 // phase 2t
                 if constexpr (GRP == 0) {
                     multiply();
                     __builtin_amdgcn_sched_barrier(0);
-                    wait_vm_lgkm_barrier<GL * (PD - 2)>();   // this wave's B of stage t + 1 landed
+                    wait_vm_lgkm_barrier<2 * GL>();   // B of stage t + 1 landed (t + 2, t + 3 may be in flight)
                 } else {
-                    issue(std::integral_constant<int, DU>{}, t + PD);
-                    fetch(u_tag);
+                    issue_a((t >> 1) + 2, std::integral_constant<int, H>{});
+                    fetch(t, u_tag);
                     __builtin_amdgcn_sched_barrier(0);
-                    wait_vm_lgkm_barrier<GL * (PD - 1)>();   // this wave's A of stage t + 1 landed
+                    // A of stage t + 1 landed: pair (t + 1) / 2, whose halves were issued at stages t - 3, t - 2 (t odd)
+                    // or t - 4, t - 3 (t even).
+                    wait_vm_lgkm_barrier<(H ? 2 : 3) * GL>();
                 }
                 __builtin_amdgcn_sched_barrier(0);
                 // phase 2t + 1
                 if constexpr (GRP == 1) {
                     multiply();
                 } else {
-                    issue(std::integral_constant<int, DU>{}, t + PD);
-                    if (t + 1 < nk) fetch(std::integral_constant<int, NU>{});   // (past the last stage: nothing)
+                    issue_b(u_tag, t + 4);
+                    if (t + 1 < nk) fetch(t + 1, std::integral_constant<int, (U + 1) % 4>{});   // (past the last: nothing)
                 }
                 __builtin_amdgcn_sched_barrier(0);
                 wait_lgkm_barrier();
                 __builtin_amdgcn_sched_barrier(0);
             };
-            // Prologue: stages 0 .. PD - 1 in flight (each group its operand); stage 0 landed; group 0 reads it.
-            static_for<0, PD>([&](auto u_tag) { issue(u_tag, decltype(u_tag)::value); });
-            wait_vm_barrier<GL * (PD - 1)>();
-            if constexpr (GRP == 0) fetch(std::integral_constant<int, 0>{});
+            // Prologue: group 1 issues A pairs 0 and 1 (stages 0-3), group 0 B of stages 0-3; stage 0 landed (group 1:
+            // pair 0 of its 16 loads; group 0: B of stage 0 of its 16); group 0 reads it.
+            if constexpr (GRP == 1) {
+                issue_a(0, std::integral_constant<int, 0>{});
+                issue_a(0, std::integral_constant<int, 1>{});
+                issue_a(1, std::integral_constant<int, 0>{});
+                issue_a(1, std::integral_constant<int, 1>{});
+                wait_vm_barrier<2 * GL>();
+            } else {
+                static_for<0, 4>([&](auto u_tag) { issue_b(u_tag, decltype(u_tag)::value); });
+                wait_vm_barrier<3 * GL>();
+                if (nk > 0) fetch(0, std::integral_constant<int, 0>{});   // (K = 0: no stage, no byte sums)
+            }
             __builtin_amdgcn_sched_barrier(0);
             wait_lgkm_barrier();
             __builtin_amdgcn_sched_barrier(0);
-            static_assert(NS == 5, "the loop below is unrolled for 5 stages");
-            for (int32_t kt = 0; kt < nk; kt += NS) {
-                static_for<0, NS>([&](auto u_tag) {
+            for (int32_t kt = 0; kt < nk; kt += 4) {
+                static_for<0, 4>([&](auto u_tag) {
                     if (kt + decltype(u_tag)::value < nk) stage(u_tag, kt + decltype(u_tag)::value);
                 });
             }
@@ -765,13 +819,22 @@ constexpr int direct_waves()
     return (BT == 256 && SA && SB) ? 4 : WAVES;
 }
 
+// Whether a 256 tile on 8 waves runs its stages in ping-pong order: not when A's row sums are needed (B has a zero
+// point or is unsigned), whose ping-pong form spills registers.
+template <int BT, bool SA, bool SB, int WAVES>
+constexpr bool direct_pingpong()
+{
+    return BT == 256 && direct_waves<BT, SA, SB, WAVES>() == 8 && !SA;
+}
+
 // One instantiation per operand signedness and needed byte sums (an unsigned operand always needs the other's sums).
 template <int BT, bool T, bool FA, bool FB, int WAVES>
 inline void launch_direct_flips(const GemmArgs &g, hipStream_t s, dim3 grid, int32_t tn, int32_t tm, int32_t ks,
                                 int32_t kslice, bool sa, bool sb)
 {
 #define OG_D(SA, SB) \
-    hipLaunchKernelGGL((k_gemm_direct<BT, T, SA, SB, FA, FB, direct_waves<BT, SA, SB, WAVES>()>), grid, \
+    hipLaunchKernelGGL((k_gemm_direct<BT, T, SA, SB, FA, FB, direct_waves<BT, SA, SB, WAVES>(), \
+                                      direct_pingpong<BT, SA, SB, WAVES>()>), grid, \
                        dim3(64 * direct_waves<BT, SA, SB, WAVES>()), 0, s, g, tn, tm, ks, kslice)
     if constexpr (FA && FB) {
         OG_D(true, true);
