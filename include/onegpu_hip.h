@@ -224,6 +224,30 @@ typedef struct og_dq_params {
  * y = clamp(rne(x / scale) + zp, 0, 255), NaN to 0; an all-zero range gives (1, 0). Uses a fixed workspace inside ctx. */
 int og_dynamic_quantize(og_ctx *ctx, const og_dq_params *params, og_buffer X, og_buffer Y, og_buffer scale, og_buffer zero);
 
+/* ------------------------------------------------------------------ quantizing a product's output without a read pass
+ * (no counterpart in the reference: there, DynamicQuantizeLinear of a layer's float output starts with the DqMinMax
+ * dispatch, a read of the whole tensor, DynamicQuantize.hlsl:35-69). */
+
+/* (min, max) pairs a ranged product may write; its `ranges` buffer holds 2 * OG_RANGES_MAX float32. */
+#define OG_RANGES_MAX 1024u
+
+/* og_int8_gemm with OG_EPI_FLOAT (or, with act_scale given, og_int8_gemm_float_scaled) whose kernels also record the
+ * range of the float values they store: *groups (min, max) pairs at `ranges` (8-byte aligned, 2 * OG_RANGES_MAX
+ * float32) whose NaN-ignoring minimum and maximum are those of C. C is dense (StrideC = M * N when batch > 1) and holds
+ * at most 2^31 - 1 elements. The direct MFMA kernels, the split-k summing pass and the one-launch few-rows kernel write
+ * the pairs from their epilogue (one a workgroup, or a column slab); the other kernels are followed by a range pass
+ * over C. C is bit for bit what og_int8_gemm (og_int8_gemm_float_scaled) writes. */
+int og_int8_gemm_float_ranged(og_ctx *ctx, const og_int8_gemm_params *params, uint32_t batch, og_buffer A, og_buffer B,
+                              og_buffer C, og_buffer ZA, og_buffer ZB, og_buffer bias, og_buffer act_scale,
+                              uint32_t act_offset, og_buffer scale, og_buffer fbias, og_buffer ranges,
+                              uint32_t *groups);
+
+/* og_dynamic_quantize of x whose range a ranged product recorded (its ranges and groups): the quantize pass alone, one
+ * launch, no read pass. y, scale and zero point are bit for bit og_dynamic_quantize's when the pairs cover x (as
+ * og_int8_gemm_float_ranged's cover its C). */
+int og_dynamic_quantize_ranged(og_ctx *ctx, const og_dq_params *params, og_buffer X, og_buffer Y, og_buffer scale,
+                               og_buffer zero, og_buffer ranges, uint32_t groups);
+
 /* ------------------------------------------------------------------ DequantizeLinear / QuantizeLinear */
 
 /* DequantizeParams / QuantizeParams, 9 words (Dequantize.hlsl:9-20, Quantize.hlsl:10-21). The tensor is seen as

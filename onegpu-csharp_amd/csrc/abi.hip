@@ -593,12 +593,16 @@ static int scratch_for(og_ctx *ctx, ProductScratch &sc, uint64_t partial_bytes, 
     return st;
 }
 
+static int launch_product_kernel(og_ctx *ctx, const og::GemmArgs &g, og::GemmKernel k, int ks, ProductScratch &sc);
+
 // Chooses the kernel for a validated product and launches it (two launches for the split few-rows forms), on ctx's
 // stream with its device current. og_int8_gemm and the convolution's products come through here; `fixed` takes the
-// scratch from og_int8_gemm_noalloc's array.
-static int launch_product(og_ctx *ctx, const og::GemmArgs &g, bool fixed = false)
+// scratch from og_int8_gemm_noalloc's array. A ranged float product (g.ranges set, C dense) sets *range_groups to the
+// (min, max) pairs written at g.ranges: from the kernel's epilogue where it has one, else from a range pass over C.
+static int launch_product(og_ctx *ctx, const og::GemmArgs &g_in, bool fixed = false, uint32_t *range_groups = nullptr)
 {
     int st = OG_OK;
+    og::GemmArgs g = g_in;
     ProductScratch sc;
     if (fixed) {
         sc.fixed = true;
@@ -616,14 +620,52 @@ static int launch_product(og_ctx *ctx, const og::GemmArgs &g, bool fixed = false
                     og::gemv_xcd_ok(g)
                 ? og::GemmKernel::RowXcd
                 : og::GemmKernel::RowTiles;
+    // The split of a tiled product along K (the 128 x 128 direct kernel on grids under half the chip).
+    const int ks = k == og::GemmKernel::Tiled && og::tiled_fast_ok(g) && og::direct_ok(g) &&
+                           !og::tiled_uses_large(g.M, g.N, g.batch) && !(g.flags & OG_GEMM_LARGE_TILE)
+                       ? og::direct_split(g)
+                       : 1;
+    // A ranged product: the pairs the chosen kernel's epilogue writes (0: it has no range epilogue, or more pairs than
+    // the caller's buffer holds; the range pass over C runs after it instead).
+    uint32_t epi_groups = 0;
+    if (g.ranges) {
+        if (k == og::GemmKernel::Tiled && og::tiled_fast_ok(g) && og::direct_ok(g))
+            epi_groups = ks > 1 ? og::direct_split_range_groups(g)
+                                : og::direct_range_groups(g, (g.flags & OG_GEMM_LARGE_TILE) ||
+                                                                 og::tiled_uses_large(g.M, g.N, g.batch));
+        else if (k == og::GemmKernel::RowXcd)
+            epi_groups = og::gemv_xcd_range_groups(g);
+        if (epi_groups > (uint32_t)og::kRangesMax) epi_groups = 0;
+        if (epi_groups == 0) g.ranges = nullptr;
+    }
+    st = launch_product_kernel(ctx, g, k, ks, sc);
+    if (st != OG_OK || !range_groups) return st;
+    if (epi_groups) {
+        *range_groups = epi_groups;
+        return st;
+    }
+    // No range epilogue: a range pass over the dense float result.
+    uint32_t groups = 0;
+    const char *product = ctx->last_kernel;   // the product keeps its name
+    st = launch(ctx, "og_int8_gemm", [&](const char **n) {
+        return og::launch_range_pass(static_cast<const float *>(g.C), (uint32_t)((uint64_t)g.M * g.N * g.batch),
+                                     g_in.ranges, ctx->stream, n, &groups);
+    });
+    ctx->last_kernel = product;
+    *range_groups = groups;
+    return st;
+}
+
+// Launches product kind k (ks > 1: the direct kernel split along K) with the scratch of `sc`.
+static int launch_product_kernel(og_ctx *ctx, const og::GemmArgs &g, og::GemmKernel k, int ks, ProductScratch &sc)
+{
+    int st = OG_OK;
     switch (k) {
     case og::GemmKernel::Portable:
         st = launch(ctx, "og_int8_gemm", [&](const char **n) { return og::launch_gemm_portable(g, ctx->stream, n); });
         break;
     case og::GemmKernel::Tiled: {
         // A grid that fills under half the chip splits along K when it takes the 128 x 128 direct kernel.
-        const int ks = og::tiled_fast_ok(g) && og::direct_ok(g) && !og::tiled_uses_large(g.M, g.N, g.batch)
-                           ? og::direct_split(g) : 1;
         if (ks > 1) {
             st = scratch_for(ctx, sc, og::direct_split_workspace_bytes(g, ks), 0);
             if (st != OG_OK) return st;
@@ -678,6 +720,12 @@ struct RequantOut {
     bool is_signed;
 };
 
+// The range output of og_int8_gemm_float_ranged.
+struct RangeOut {
+    og_buffer ranges;
+    uint32_t *groups;
+};
+
 // The activation scale of og_int8_gemm_float_scaled.
 struct ActScale {
     og_buffer buf;
@@ -688,10 +736,21 @@ struct ActScale {
 // output Y (OffC and StrideC in bytes) and `scale` the multiplier.
 static int run_gemm(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_buffer A, og_buffer B, og_buffer C,
                     og_buffer ZA, og_buffer ZB, og_buffer bias, og_buffer scale, og_buffer fbias, const RequantOut *rq,
-                    const ActScale *act = nullptr, bool fixed_scratch = false)
+                    const ActScale *act = nullptr, bool fixed_scratch = false, const RangeOut *rout = nullptr)
 {
     int st = check_gemm_params(ctx, p, batch, rq != nullptr);
     if (st != OG_OK) return st;
+    if (rout) {
+        if (!(p->Epi & OG_EPI_FLOAT) || rq) return fail(ctx, OG_ERR_INVALID_ARG, "Epi", "a ranged product needs the float result bit");
+        if (!rout->groups) return fail(ctx, OG_ERR_INVALID_ARG, "groups", "null pointer");
+        if (!rout->ranges.ptr || ((uintptr_t)rout->ranges.ptr & 7) || rout->ranges.bytes < 8ull * og::kRangesMax)
+            return fail(ctx, OG_ERR_INVALID_ARG, "ranges", "the ranges need %d (min, max) pairs of float32, 8-byte aligned", og::kRangesMax);
+        if (batch > 1 && p->StrideC != (uint64_t)p->M * p->N)
+            return fail(ctx, OG_ERR_INVALID_ARG, "StrideC", "a ranged product's C is dense: StrideC must be M * N");
+        if ((uint64_t)p->M * p->N * batch > 0x7FFFFFFFull)
+            return fail(ctx, OG_ERR_INVALID_ARG, "c", "a ranged product's C holds more than 2147483647 elements");
+        *rout->groups = 0;
+    }
     if (act) {
         if (!(p->Epi & OG_EPI_FLOAT)) return fail(ctx, OG_ERR_INVALID_ARG, "Epi", "a scaled product needs the float result bit");
         if (!act->buf.ptr || ((uintptr_t)act->buf.ptr & 3)) return fail(ctx, OG_ERR_INVALID_ARG, "activationScale", "the activation scale is missing or misaligned");
@@ -778,9 +837,10 @@ static int run_gemm(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, o
             (act ? og::EPI_SCALE_PRODUCT : 0u);
     g.act_scale = act ? static_cast<const float *>(act->buf.ptr) + act->offset : nullptr;
     g.zp_y = rq ? rq->zero_point : 0;
+    g.ranges = rout ? static_cast<float *>(rout->ranges.ptr) : nullptr;
 
     (void)hipSetDevice(ctx->device);
-    st = launch_product(ctx, g, fixed_scratch);
+    st = launch_product(ctx, g, fixed_scratch, rout ? rout->groups : nullptr);
     return st == OG_OK ? ok(ctx) : st;
 }
 
@@ -804,6 +864,18 @@ int og_int8_gemm_float_scaled(og_ctx *ctx, const og_int8_gemm_params *p, uint32_
 {
     const ActScale act{act_scale, act_offset};
     return run_gemm(ctx, p, batch, A, B, C, ZA, ZB, bias, scale, fbias, nullptr, &act);
+}
+
+// og_int8_gemm's float product (or og_int8_gemm_float_scaled's, with act_scale given) that also records the range of
+// what it stores, for og_dynamic_quantize_ranged (no counterpart in the reference).
+int og_int8_gemm_float_ranged(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_buffer A, og_buffer B,
+                              og_buffer C, og_buffer ZA, og_buffer ZB, og_buffer bias, og_buffer act_scale,
+                              uint32_t act_offset, og_buffer scale, og_buffer fbias, og_buffer ranges, uint32_t *groups)
+{
+    const ActScale act{act_scale, act_offset};
+    const RangeOut rout{ranges, groups};
+    return run_gemm(ctx, p, batch, A, B, C, ZA, ZB, bias, scale, fbias, nullptr, act_scale.ptr ? &act : nullptr,
+                    false, &rout);
 }
 
 int og_int8_gemm_requantized(og_ctx *ctx, const og_int8_gemm_params *p, uint32_t batch, og_buffer A, og_buffer B,
@@ -1144,6 +1216,33 @@ int og_dynamic_quantize(og_ctx *ctx, const og_dq_params *p, og_buffer X, og_buff
     (void)hipSetDevice(ctx->device);
     int st = launch(ctx, "og_dynamic_quantize", [&](const char **k) { return og::launch_dynamic_quantize(d, ctx->ws, ctx->stream, k, 0); });
     if (st == OG_OK) st = launch(ctx, "og_dynamic_quantize", [&](const char **k) { return og::launch_dynamic_quantize(d, ctx->ws, ctx->stream, k, 1); });
+    return st == OG_OK ? ok(ctx) : st;
+}
+
+// DynamicQuantizeLinear's quantize pass alone, over the ranges a ranged product recorded for x (no counterpart in the
+// reference).
+int og_dynamic_quantize_ranged(og_ctx *ctx, const og_dq_params *p, og_buffer X, og_buffer Y, og_buffer scale,
+                               og_buffer zero, og_buffer ranges, uint32_t groups)
+{
+    if (!p) return fail(ctx, OG_ERR_INVALID_ARG, "params", "null parameter block");
+    if (p->Count < 1 || p->Count > 0x7FFFFFFFu) return fail(ctx, OG_ERR_INVALID_ARG, "count", "count %d must be at least 1", (int32_t)p->Count);
+    if (!X.ptr || ((uintptr_t)X.ptr & 3) || !fits((uint64_t)p->OffX * 4, (uint64_t)p->Count * 4, X)) return fail(ctx, OG_ERR_INVALID_ARG, "x", "elements %u..%llu reach past the buffer", p->OffX, (unsigned long long)p->OffX + p->Count);
+    if (!Y.ptr || !fits(p->OffY, p->Count, Y)) return fail(ctx, OG_ERR_INVALID_ARG, "y", "elements %u..%llu reach past the buffer", p->OffY, (unsigned long long)p->OffY + p->Count);
+    if (!scale.ptr || ((uintptr_t)scale.ptr & 3) || !fits((uint64_t)p->OffScale * 4, 4, scale)) return fail(ctx, OG_ERR_INVALID_ARG, "scale", "element %u reaches past the buffer", p->OffScale);
+    if (!zero.ptr || !fits(p->OffZero, 1, zero)) return fail(ctx, OG_ERR_INVALID_ARG, "zeroPoint", "element %u reaches past the buffer", p->OffZero);
+    if (!ranges.ptr || ((uintptr_t)ranges.ptr & 7) || ranges.bytes < 8ull * og::kRangesMax) return fail(ctx, OG_ERR_INVALID_ARG, "ranges", "the ranges need %d (min, max) pairs of float32, 8-byte aligned", og::kRangesMax);
+    if (groups < 1 || groups > (uint32_t)og::kRangesMax) return fail(ctx, OG_ERR_INVALID_ARG, "groups", "%u pairs: between 1 and %d", groups, og::kRangesMax);
+    if (!ctx) return fail(ctx, OG_ERR_NO_DEVICE, "ctx", "no context: the arguments are valid but there is no device to run on");
+    og::DqArgs d{};
+    d.x = static_cast<const float *>(X.ptr) + p->OffX;
+    d.y = static_cast<uint8_t *>(Y.ptr) + p->OffY;
+    d.scale = static_cast<float *>(scale.ptr) + p->OffScale;
+    d.zero = static_cast<uint8_t *>(zero.ptr) + p->OffZero;
+    d.count = p->Count;
+    (void)hipSetDevice(ctx->device);
+    int st = launch(ctx, "og_dynamic_quantize_ranged", [&](const char **k) {
+        return og::launch_dynamic_quantize_ranged(d, static_cast<const float *>(ranges.ptr), groups, ctx->stream, k);
+    });
     return st == OG_OK ? ok(ctx) : st;
 }
 

@@ -21,6 +21,12 @@ bool direct_ok(const GemmArgs &g)
     return b_dwords_ok(g);
 }
 
+uint32_t direct_range_groups(const GemmArgs &g, bool large)
+{
+    if (large) return 0;   // the 256 tile has no range epilogue
+    return (uint32_t)std::min<int64_t>(((g.N + 127) / 128) * ((g.M + 127) / 128) * g.batch, int64_t(1) << 30);
+}
+
 hipError_t launch_gemm_direct(const GemmArgs &g, hipStream_t s, const char **kernel, bool large)
 {
     const int32_t bt = large ? 256 : 128;
@@ -72,6 +78,20 @@ namespace {
 template <bool V4>
 __global__ __launch_bounds__(256) void k_splitk_sum(GemmArgs g, int32_t ks, const int32_t *parts)
 {
+    __shared__ float red[2 * 256 / 64];
+    // A ranged float product: the NaN-ignoring range of the values this thread stores.
+    const bool ranged = g.ranges != nullptr;
+    float rmn = __int_as_float(0x7F800000), rmx = __int_as_float(0xFF800000);
+    auto put = [&](int64_t ci, int32_t col, uint32_t sum) {
+        if (ranged) {
+            const float f = sum_to_float(g, col, sum);
+            static_cast<float *>(g.C)[ci] = f;
+            rmn = fminf(rmn, f);
+            rmx = fmaxf(rmx, f);
+        } else {
+            store_value(g, ci, col, sum);
+        }
+    };
     const int64_t mn = (int64_t)g.M * g.N, per = V4 ? mn / 4 : mn, total = per * g.batch;
     for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += (int64_t)gridDim.x * 256) {
         const int64_t b = t / per, r = (t - b * per) * (V4 ? 4 : 1);
@@ -101,10 +121,10 @@ __global__ __launch_bounds__(256) void k_splitk_sum(GemmArgs g, int32_t ks, cons
                 sum.w += v.w;
             }
             const int64_t c = b * g.strideC + r;
-            store_value(g, c, n, sum.x);
-            store_value(g, c + 1, n + 1, sum.y);
-            store_value(g, c + 2, n + 2, sum.z);
-            store_value(g, c + 3, n + 3, sum.w);
+            put(c, n, sum.x);
+            put(c + 1, n + 1, sum.y);
+            put(c + 2, n + 2, sum.z);
+            put(c + 3, n + 3, sum.w);
         } else {
             uint32_t sum = 0;
             int32_t kc = 0;
@@ -115,12 +135,23 @@ __global__ __launch_bounds__(256) void k_splitk_sum(GemmArgs g, int32_t ks, cons
                 sum += v[0] + v[1] + v[2] + v[3];
             }
             for (; kc < ks; kc++) sum += (uint32_t)p[kc * mn];
-            store_value(g, b * g.strideC + r, n, sum);
+            put(b * g.strideC + r, n, sum);
         }
     }
+    if (ranged) store_workgroup_range<256>(rmn, rmx, red, g.ranges, blockIdx.x);
 }
 
 }  // namespace
+
+// The summing pass's grid: one workgroup a 256 four-column groups (or columns), at most 2^20 workgroups.
+static int64_t splitk_sum_groups(const GemmArgs &g)
+{
+    const bool v4 = g.N % 4 == 0;   // the partials start 256-byte aligned, so each row of 4-column groups is aligned
+    const int64_t total = (int64_t)g.M * g.N * g.batch / (v4 ? 4 : 1);
+    return std::min<int64_t>((total + 255) / 256, int64_t(1) << 20);
+}
+
+uint32_t direct_split_range_groups(const GemmArgs &g) { return (uint32_t)splitk_sum_groups(g); }
 
 hipError_t launch_gemm_direct_split(const GemmArgs &g, const Workspace &ws, hipStream_t s, const char **kernel, int ks,
                                     int step)
@@ -134,6 +165,7 @@ hipError_t launch_gemm_direct_split(const GemmArgs &g, const Workspace &ws, hipS
         gs.strideC = (int64_t)g.M * g.N;
         gs.batch = g.batch * ks;
         gs.epi = 0;
+        gs.ranges = nullptr;   // the summing pass records the ranges
         const int64_t stages = g.K / DBK;
         const int32_t kslice = (int32_t)((stages + ks - 1) / ks) * DBK;
         const int64_t blocks = (int64_t)tn * tm * gs.batch;
@@ -141,9 +173,8 @@ hipError_t launch_gemm_direct_split(const GemmArgs &g, const Workspace &ws, hipS
         return hipGetLastError();
     }
     *kernel = "splitk-sum";
-    const bool v4 = g.N % 4 == 0;   // the partials start 256-byte aligned, so each row of 4-column groups is aligned
-    const int64_t total = (int64_t)g.M * g.N * g.batch / (v4 ? 4 : 1);
-    const int64_t wgs = std::min<int64_t>((total + 255) / 256, int64_t(1) << 20);
+    const bool v4 = g.N % 4 == 0;
+    const int64_t wgs = splitk_sum_groups(g);
     if (v4) hipLaunchKernelGGL(k_splitk_sum<true>, dim3((uint32_t)wgs), dim3(256), 0, s, g, (int32_t)ks, ws.partials);
     else hipLaunchKernelGGL(k_splitk_sum<false>, dim3((uint32_t)wgs), dim3(256), 0, s, g, (int32_t)ks, ws.partials);
     return hipGetLastError();

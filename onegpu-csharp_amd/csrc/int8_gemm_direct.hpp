@@ -685,6 +685,8 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
     uint8_t *const Yb = static_cast<uint8_t *>(g.C) + bsplit * g.strideC;
     const int32_t ncol0 = n0 + wn * WTN + i32;
     const int32_t M = g.M, N = g.N, zp_y = g.zp_y;
+    // The NaN-ignoring range of the float values this thread stores (for a ranged float product; 128 tile).
+    float rmn = __int_as_float(0x7F800000), rmx = __int_as_float(0xFF800000);
     // MODE 0: int32 (+ bias); 1: float32, `opt` = float bias present; 2: requantized bytes, `opt` = uint8 output.
     auto store_all = [&](auto mode_tag, bool opt) {
         constexpr int MODE = decltype(mode_tag)::value;
@@ -740,6 +742,8 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
                         for (int e = 0; e < 4; e++) {
                             f[e] = __fmul_rn((float)(int32_t)v[e], sc4[e]);
                             if (opt) f[e] = __fadd_rn(f[e], fb4[e]);
+                            rmn = fminf(rmn, f[e]);   // (the 128 tile only: this path)
+                            rmx = fmaxf(rmx, f[e]);
                         }
                         *reinterpret_cast<v4i *>(Cb + at) =
                             (v4i){__float_as_int(f[0]), __float_as_int(f[1]), __float_as_int(f[2]), __float_as_int(f[3])};
@@ -782,6 +786,10 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
                                 float f = __fmul_rn((float)(int32_t)v, sc[j]);
                                 if (opt) f = __fadd_rn(f, fb[j]);
                                 row[32 * j] = __float_as_int(f);
+                                if constexpr (BT == 128) {
+                                    rmn = fminf(rmn, f);
+                                    rmx = fmaxf(rmx, f);
+                                }
                             } else if constexpr (MODE == 2) {
                                 yrow[32 * j] = (uint8_t)requantize_byte(v, sc[j], zp_y, opt);
                             } else {
@@ -806,6 +814,12 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
     } else if (epi & OG_EPI_FLOAT) {
         if (epi & OG_EPI_FLOAT_BIAS) store_all(std::integral_constant<int, 1>{}, true);
         else store_all(std::integral_constant<int, 1>{}, false);
+        if (BT == 128 && g.ranges) {
+            // A ranged float product: the workgroup's range of what it stored, in its slot (its workgroup id). (The 256
+            // tile has no range epilogue: with it, its registers spill; its ranged products take a range pass.)
+            __syncthreads();   // every thread done reading the epilogue's arrays in LDS
+            store_workgroup_range<THREADS>(rmn, rmx, reinterpret_cast<float *>(smem), g.ranges, blockIdx.x);
+        }
     } else {
         store_all(std::integral_constant<int, 0>{}, false);
     }

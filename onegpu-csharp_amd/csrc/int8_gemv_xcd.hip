@@ -354,18 +354,34 @@ __global__ __launch_bounds__(GX_THREADS) void k_gemv_xcd(GemmArgs g, int32_t sla
     }
     __syncthreads();
 
-    if (en >= N) return;
-    const uint32_t cs = SUM_B ? (uint32_t)smem[M * GX_COLS + ecol] : 0u;
+    // A ranged float product: the NaN-ignoring range of the values this thread stores, then the slab's in slot q.
+    float rmn = __int_as_float(0x7F800000), rmx = __int_as_float(0xFF800000);
+    if (en < N) {
+        const uint32_t cs = SUM_B ? (uint32_t)smem[M * GX_COLS + ecol] : 0u;
 #pragma unroll
-    for (int j = 0; j < 16 / GX_EROWS; j++) {
-        const int m = erow0 + GX_EROWS * j;
-        if (m >= M) break;
-        const uint32_t v = (uint32_t)smem[m * GX_COLS + ecol];
-        const uint32_t rs = SUM_A ? (uint32_t)smem[R * GX_COLS + m] : 0u;
-        const uint32_t res = v - wz * rs - zz[j] * (cs - (uint32_t)K * wz) + ib;
-        const int64_t ci = (int64_t)b * g.strideC + (int64_t)m * N + en;
-        if (epi & EPI_REQUANT) store_requantized_col(g, ci, res, esc, 0.0f);
-        else store_sum_col(g, ci, res, esc, efb);
+        for (int j = 0; j < 16 / GX_EROWS; j++) {
+            const int m = erow0 + GX_EROWS * j;
+            if (m >= M) break;
+            const uint32_t v = (uint32_t)smem[m * GX_COLS + ecol];
+            const uint32_t rs = SUM_A ? (uint32_t)smem[R * GX_COLS + m] : 0u;
+            const uint32_t res = v - wz * rs - zz[j] * (cs - (uint32_t)K * wz) + ib;
+            const int64_t ci = (int64_t)b * g.strideC + (int64_t)m * N + en;
+            if (epi & EPI_REQUANT) {
+                store_requantized_col(g, ci, res, esc, 0.0f);
+            } else if (g.ranges) {
+                float f = __fmul_rn((float)(int32_t)res, esc);
+                if (epi & OG_EPI_FLOAT_BIAS) f = __fadd_rn(f, efb);
+                static_cast<float *>(g.C)[ci] = f;
+                rmn = fminf(rmn, f);
+                rmx = fmaxf(rmx, f);
+            } else {
+                store_sum_col(g, ci, res, esc, efb);
+            }
+        }
+    }
+    if (g.ranges) {
+        __syncthreads();   // every thread done reading the sums in LDS
+        store_workgroup_range<GX_THREADS>(rmn, rmx, reinterpret_cast<float *>(smem), g.ranges, (uint32_t)q);
     }
 }
 
@@ -397,6 +413,11 @@ uint64_t gemv_xcd_workspace_bytes(const GemmArgs &g)
 {
     const int64_t q = (int64_t)g.batch * ((g.N + GX_COLS - 1) / GX_COLS), nkc = (g.K + GX_KT - 1) / GX_KT;
     return (uint64_t)(q * nkc * gemv_xcd_part(g.M) * 4);
+}
+
+uint32_t gemv_xcd_range_groups(const GemmArgs &g)
+{
+    return (uint32_t)((int64_t)g.batch * ((g.N + GX_COLS - 1) / GX_COLS));   // one a column slab (its finishing tile)
 }
 
 uint64_t gemv_xcd_words(const GemmArgs &g)

@@ -31,7 +31,14 @@ struct GemmArgs {
     uint32_t flags;  // OG_GEMM_*
     uint32_t epi;    // OG_EPI_*, plus EPI_REQUANT / EPI_REQUANT_U8 below
     int32_t zp_y;    // the output zero point of a requantized product
+    // A float product's range output (og_int8_gemm_float_ranged), or nullptr: each workgroup that stores C writes the
+    // NaN-ignoring minimum and maximum of the values it stored to ranges[2 slot], ranges[2 slot + 1], its slot a number
+    // below the kernel's range_groups (product_range_groups).
+    float *ranges;
 };
+
+// Pairs a ranged product may write: its caller's buffer holds 2 * kRangesMax floats (OG_RANGES_MAX).
+constexpr int kRangesMax = 1024;
 
 // Library-internal epilogue bits (above the public OG_EPI_* ones): C is 8-bit and each sum is requantized with the
 // multiplier at `scale` and the zero point zp_y; uint8 output when EPI_REQUANT_U8, else int8.
@@ -58,6 +65,13 @@ hipError_t noalloc_scratch_setup(int device, hipStream_t s, void **out);
 
 // Kernel choice for a product, as og_int8_gemm_kernel_name reports it.
 enum class GemmKernel { Portable, Tiled, Skinny, SkinnyDirect, RowTiles, RowXcd };
+
+// The (min, max) pairs a float product writes from its epilogue when GemmArgs::ranges is set: the direct kernels one a
+// workgroup, the split-k summing pass one a workgroup, the one-launch few-rows kernel one a column slab; 0 for the
+// kernels without a range epilogue (the caller then runs a range pass over C).
+uint32_t direct_range_groups(const GemmArgs &g, bool large);
+uint32_t direct_split_range_groups(const GemmArgs &g);
+uint32_t gemv_xcd_range_groups(const GemmArgs &g);
 GemmKernel choose_gemm_kernel(int32_t M, int32_t N, int32_t K, int32_t batch, uint32_t flags);
 const char *gemm_kernel_name(GemmKernel k);
 
@@ -132,6 +146,13 @@ struct DqArgs {
     uint32_t count;
 };
 hipError_t launch_dynamic_quantize(const DqArgs &d, const Workspace &ws, hipStream_t s, const char **kernel, int step);
+// DynamicQuantizeLinear's quantize pass alone, over `groups` (min, max) pairs at `ranges` (at most kRangesMax; the
+// buffer holds 2 * kRangesMax floats) that cover x: a ranged product's, or launch_range_pass's.
+hipError_t launch_dynamic_quantize_ranged(const DqArgs &d, const float *ranges, uint32_t groups, hipStream_t s,
+                                          const char **kernel);
+// DynamicQuantizeLinear's range pass alone over count floats at x, into `ranges`; *groups = the pairs written.
+hipError_t launch_range_pass(const float *x, uint32_t count, float *ranges, hipStream_t s, const char **kernel,
+                             uint32_t *groups);
 
 struct DequantArgs {
     const void *x;
@@ -226,6 +247,34 @@ __device__ __forceinline__ void transpose4x4(uint32_t r0, uint32_t r1, uint32_t 
 
 __device__ __forceinline__ int32_t sext8(uint32_t b) { return (int32_t)(int8_t)(uint8_t)b; }
 
+// A workgroup of THREADS threads combines its threads' (mn, mx) (fminf / fmaxf: a NaN never wins, and the kernels' float
+// results are never signalling NaNs) and thread 0 stores them to ranges[2 slot], [2 slot + 1]. `lds` holds 2 * THREADS
+// / 64 floats nobody else uses until the call returns; every thread of the workgroup calls it.
+template <int THREADS>
+__device__ __forceinline__ void store_workgroup_range(float mn, float mx, float *lds, float *ranges, uint32_t slot)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        mn = fminf(mn, __shfl_xor(mn, o));
+        mx = fmaxf(mx, __shfl_xor(mx, o));
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        lds[2 * wave] = mn;
+        lds[2 * wave + 1] = mx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int w = 1; w < THREADS / 64; w++) {
+            mn = fminf(mn, lds[2 * w]);
+            mx = fmaxf(mx, lds[2 * w + 1]);
+        }
+        ranges[2 * slot] = mn;
+        ranges[2 * slot + 1] = mx;
+    }
+}
+
 // The column scale of a float result: scale[n or 0], or its product with the activation scale.
 __device__ __forceinline__ float column_scale(const GemmArgs &g, int32_t col)
 {
@@ -242,6 +291,16 @@ __device__ __forceinline__ uint32_t requantize_byte(uint32_t sum, float mult, in
     if ((__float_as_uint(v) & 0x7FFFFFFFu) > 0x7F800000u) return (uint32_t)lo & 0xFFu;   // NaN
     const float r = fminf(fmaxf(rintf(v), (float)(lo - zp)), (float)(hi - zp));
     return (uint32_t)((int32_t)r + zp) & 0xFFu;
+}
+
+// The float result of a sum (Int8GemmEpilogue.hlsli:17-42): fl(fl(float(sum + bias)) * scale), then + float bias as a
+// separate rounding.
+__device__ __forceinline__ float sum_to_float(const GemmArgs &g, int32_t col, uint32_t sum)
+{
+    if (g.epi & OG_EPI_INT_BIAS) sum += (uint32_t)g.bias[col];
+    float f = __fmul_rn((float)(int32_t)sum, column_scale(g, col));
+    if (g.epi & OG_EPI_FLOAT_BIAS) f = __fadd_rn(f, g.fbias[col]);
+    return f;
 }
 
 // The int32 sum as the reference's StoreValue leaves it (Int8GemmEpilogue.hlsli:17-42): the raw sum; + int bias;

@@ -109,26 +109,27 @@ __device__ __forceinline__ uint32_t dq_one(float x, float scale, float zp)
 }
 
 // Pass 2's scale and zero point, in every workgroup: pass 1's ranges combined (the kernel boundary orders them; min and
-// max are order-free, so every workgroup derives the same values). Each thread loads kDqMaxGroups / DQ_THREADS of the
-// (min, max) pairs before the caller's block of x, unconditionally (the workspace always holds kDqMaxGroups pairs, so
-// no load waits on a branch), and ignores the pairs from `groups` on; workgroup 0 also writes the scale and zero point
-// out (the zero point one byte, its neighbours untouched).
+// max are order-free, so every workgroup derives the same values). Each thread loads P of the (min, max) pairs before
+// the caller's block of x, unconditionally (the buffer always holds P * DQ_THREADS pairs, so no load waits on a
+// branch), and ignores the pairs from `groups` on; workgroup 0 also writes the scale and zero point out (the zero point
+// one byte, its neighbours untouched). P = 1 over the quantizer's own 256 ranges; up to 4 over a ranged product's.
 typedef float f2 __attribute__((ext_vector_type(2)));
-constexpr int DQ_PAIRS = kDqMaxGroups / DQ_THREADS;
-static_assert(kDqMaxGroups % DQ_THREADS == 0, "the ranges split evenly over the threads");
+static_assert(kDqMaxGroups == DQ_THREADS && kRangesMax == 4 * DQ_THREADS, "the ranges split evenly over the threads");
 
-__device__ __forceinline__ void dq_load_ranges(const float *ranges, f2 (&r)[DQ_PAIRS])
+template <int P>
+__device__ __forceinline__ void dq_load_ranges(const float *ranges, f2 (&r)[P])
 {
 #pragma unroll
-    for (int q = 0; q < DQ_PAIRS; q++) r[q] = reinterpret_cast<const f2 *>(ranges)[threadIdx.x + q * DQ_THREADS];
+    for (int q = 0; q < P; q++) r[q] = reinterpret_cast<const f2 *>(ranges)[threadIdx.x + q * DQ_THREADS];
 }
 
-__device__ __forceinline__ void dq_combine(const f2 (&r)[DQ_PAIRS], uint32_t groups, float *smin, float *smax,
+template <int P>
+__device__ __forceinline__ void dq_combine(const f2 (&r)[P], uint32_t groups, float *smin, float *smax,
                                            float *sparam, float *scale_out, uint8_t *zero_out, float &scale, float &zpf)
 {
     float mn = __int_as_float(0x7F800000), mx = __int_as_float(0xFF800000);
 #pragma unroll
-    for (int q = 0; q < DQ_PAIRS; q++) {
+    for (int q = 0; q < P; q++) {
         if (threadIdx.x + q * DQ_THREADS < groups) {
             mn = (r[q].x < mn) ? r[q].x : mn;
             mx = (r[q].y > mx) ? r[q].y : mx;
@@ -155,13 +156,14 @@ __device__ __forceinline__ void dq_combine(const f2 (&r)[DQ_PAIRS], uint32_t gro
 // combines the ranges while x is still on its way from HBM. In a whole block with x and y 16-byte aligned, lane l of
 // wave w takes elements 1024 w + 256 c + 4 l .. + 3 (c = 0..3) with one 16-byte load and one 4-byte store each, so
 // every instruction covers one contiguous span across the wave; otherwise lane t takes elements t, t + 256, ...
+template <int P>
 __global__ __launch_bounds__(DQ_THREADS) void k_dq_quantize(const float *x, uint8_t *y, uint32_t count,
                                                             const float *ranges, uint32_t groups, float *scale_out,
                                                             uint8_t *zero_out)
 {
     __shared__ float smin[DQ_THREADS / 64], smax[DQ_THREADS / 64], sparam[2];
-    f2 r[DQ_PAIRS];
-    dq_load_ranges(ranges, r);
+    f2 r[P];
+    dq_load_ranges<P>(ranges, r);
     const uint64_t blk = (uint64_t)blockIdx.x * 4096;
     float scale, zp;
     if ((((uintptr_t)x | (uintptr_t)y) & 15) == 0 && blk + 4096 <= count) {
@@ -198,9 +200,32 @@ hipError_t launch_dynamic_quantize(const DqArgs &d, const Workspace &ws, hipStre
         *kernel = "dq-quantize";
         // One block of 4096 elements a workgroup (at most 2^20 workgroups for a 32-bit count).
         const uint32_t wgs = d.count == 0 ? 1u : (uint32_t)(((uint64_t)d.count + 4095) / 4096);
-        hipLaunchKernelGGL(k_dq_quantize, dim3(wgs), dim3(DQ_THREADS), 0, s, d.x, d.y, d.count,
+        hipLaunchKernelGGL(k_dq_quantize<1>, dim3(wgs), dim3(DQ_THREADS), 0, s, d.x, d.y, d.count,
                            (const float *)ws.dq_ranges, groups, d.scale, d.zero);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_dynamic_quantize_ranged(const DqArgs &d, const float *ranges, uint32_t groups, hipStream_t s,
+                                          const char **kernel)
+{
+    *kernel = "dq-quantize";
+    const uint32_t wgs = d.count == 0 ? 1u : (uint32_t)(((uint64_t)d.count + 4095) / 4096);
+#define OG_DQR(P) hipLaunchKernelGGL(k_dq_quantize<P>, dim3(wgs), dim3(DQ_THREADS), 0, s, d.x, d.y, d.count, ranges, \
+                                     groups, d.scale, d.zero)
+    if (groups <= (uint32_t)DQ_THREADS) OG_DQR(1);
+    else if (groups <= 2u * DQ_THREADS) OG_DQR(2);
+    else OG_DQR(4);
+#undef OG_DQR
+    return hipGetLastError();
+}
+
+hipError_t launch_range_pass(const float *x, uint32_t count, float *ranges, hipStream_t s, const char **kernel,
+                             uint32_t *groups)
+{
+    *kernel = "dq-minmax";
+    *groups = dq_groups(count);
+    hipLaunchKernelGGL(k_dq_minmax, dim3(*groups), dim3(DQ1_THREADS), 0, s, x, count, ranges);
     return hipGetLastError();
 }
 

@@ -545,12 +545,28 @@ void Int8Gemm::EncodeFloatScaled(GpuCommandEncoder &encoder, const Int8GemmProbl
     FloatProduct(encoder, problem, a, b, c, &activationScale, weightScale, zeroPointA, zeroPointB, floatBias, intBias);
 }
 
+void Int8Gemm::EncodeFloatRanged(GpuCommandEncoder &encoder, const Int8GemmProblem &problem, const GpuBuffer &a,
+                                 const GpuBuffer &b, const GpuBuffer &c, const Int8Operand &scale,
+                                 const Int8Ranges &ranges, const std::optional<Int8Operand> &zeroPointA,
+                                 const std::optional<Int8Operand> &zeroPointB,
+                                 const std::optional<Int8Operand> &floatBias, const std::optional<Int8Operand> &intBias,
+                                 const std::optional<Int8Operand> &activationScale)
+{
+    if (!ranges.Buffer.Valid()) throw GpuKernelShapeException(kGemm, "ranges", "buffer is null");
+    RequireType(kGemm, ranges.Buffer, ElementType::Float32, "ranges");
+    Check::Range(kGemm, "ranges", ranges.Buffer.Length(), 0, 2 * (int64_t)OG_RANGES_MAX);
+    if ((int64_t)problem.Batch * problem.M * problem.N > 0x7FFFFFFF)
+        throw GpuKernelShapeException(kGemm, "c", "a ranged product's output holds more than 2147483647 elements");
+    FloatProduct(encoder, problem, a, b, c, activationScale ? &*activationScale : nullptr, scale, zeroPointA, zeroPointB,
+                 floatBias, intBias, &ranges);
+}
+
 // EncodeFloat's checks and recording (Int8Gemm.cs:270-314), with the activation scale when there is one.
 void Int8Gemm::FloatProduct(GpuCommandEncoder &encoder, const Int8GemmProblem &problem, const GpuBuffer &a,
                             const GpuBuffer &b, const GpuBuffer &c, const Int8Operand *activationScale,
                             const Int8Operand &scale, const std::optional<Int8Operand> &zeroPointA,
                             const std::optional<Int8Operand> &zeroPointB, const std::optional<Int8Operand> &floatBias,
-                            const std::optional<Int8Operand> &intBias)
+                            const std::optional<Int8Operand> &intBias, const Int8Ranges *ranges)
 {
     if (!c.Valid()) throw GpuKernelShapeException(kGemm, "c", "buffer is null");
     auto prep = Prepare(problem, a, b, zeroPointA, zeroPointB);
@@ -592,6 +608,7 @@ void Int8Gemm::FloatProduct(GpuCommandEncoder &encoder, const Int8GemmProblem &p
         epi.ActScale = activationScale->Buffer;
         epi.OffActScale = (uint32_t)activationScale->Offset;
     }
+    epi.Ranges = ranges;
     Multiply(encoder, problem, a, a.Type() == ElementType::Int8, b, b.Type() == ElementType::Int8, c, problem.OffsetC,
              zeroPointA, zeroPointB, epi);
 }
@@ -767,6 +784,18 @@ void Int8Gemm::Multiply(GpuCommandEncoder &encoder, const Int8GemmProblem &p, co
             keep_of({&A, &B, &C, &zaBuf, &zbBuf, &ib, &sc}));
         return;
     }
+    if (epi.Ranges) {
+        GpuBuffer as = epi.ActScale, rg = epi.Ranges->Buffer;
+        const uint32_t aoff = epi.OffActScale;
+        std::shared_ptr<uint32_t> groups = epi.Ranges->Groups;
+        blocks_.Note(4, {&A, &B, &C, &zaBuf, &zbBuf, &ib, &as, &sc, &fb, &rg});
+        encoder.Record(
+            [w, batch, A, B, C, zaBuf, zbBuf, ib, as, aoff, sc, fb, rg, groups](og_ctx *ctx) {
+                ThrowIfFailed(ctx, og_int8_gemm_float_ranged(ctx, &w, batch, bind(A), bind(B), bind(C), bind(zaBuf), bind(zbBuf), bind(ib), bind(as), aoff, bind(sc), bind(fb), bind(rg), groups.get()), kGemm);
+            },
+            keep_of({&A, &B, &C, &zaBuf, &zbBuf, &ib, &as, &sc, &fb, &rg}));
+        return;
+    }
     if (epi.ActScale.Valid()) {
         GpuBuffer as = epi.ActScale;
         const uint32_t aoff = epi.OffActScale;
@@ -785,6 +814,8 @@ void Int8Gemm::Multiply(GpuCommandEncoder &encoder, const Int8GemmProblem &p, co
         },
         keep_of({&A, &B, &C, &zaBuf, &zbBuf, &ib, &sc, &fb}));
 }
+
+Int8Ranges::Int8Ranges(GpuBuffer buffer) : Buffer(std::move(buffer)) {}
 
 // ------------------------------------------------------------------ DynamicQuantizeKernels
 
@@ -827,6 +858,45 @@ void DynamicQuantizeKernels::Encode(GpuCommandEncoder &encoder, const GpuBuffer 
             ThrowIfFailed(ctx, og_dynamic_quantize(ctx, &w, bind(X), bind(Y), bind(S), bind(Z)), "DynamicQuantizeLinear");
         },
         keep_of({&X, &Y, &S, &Z}));
+}
+
+void DynamicQuantizeKernels::EncodeRanged(GpuCommandEncoder &encoder, const GpuBuffer &x, int offsetX, int count,
+                                          const GpuBuffer &y, int offsetY, const GpuBuffer &scale, int offsetScale,
+                                          const GpuBuffer &zeroPoint, int offsetZeroPoint, const Int8Ranges &ranges)
+{
+    const std::string Name = "DynamicQuantizeLinear";
+    if (!x.Valid()) throw GpuKernelShapeException(Name, "x", "buffer is null");
+    if (!y.Valid()) throw GpuKernelShapeException(Name, "y", "buffer is null");
+    if (!scale.Valid()) throw GpuKernelShapeException(Name, "scale", "buffer is null");
+    if (!zeroPoint.Valid()) throw GpuKernelShapeException(Name, "zeroPoint", "buffer is null");
+    if (!ranges.Buffer.Valid()) throw GpuKernelShapeException(Name, "ranges", "buffer is null");
+    RequireType(Name, x, ElementType::Float32, "x");
+    RequireType(Name, y, ElementType::UInt8, "y");
+    RequireType(Name, scale, ElementType::Float32, "scale");
+    RequireType(Name, zeroPoint, ElementType::UInt8, "zeroPoint");
+    RequireType(Name, ranges.Buffer, ElementType::Float32, "ranges");
+    if (count < 1) throw GpuKernelShapeException(Name, "count", "count " + std::to_string(count) + " must be at least 1");
+    Check::Range(Name, "x", x.Length(), offsetX, count);
+    Check::Range(Name, "y", y.Length(), offsetY, count);
+    Check::Range(Name, "scale", scale.Length(), offsetScale, 1);
+    Check::Range(Name, "zeroPoint", zeroPoint.Length(), offsetZeroPoint, 1);
+    Check::Range(Name, "ranges", ranges.Buffer.Length(), 0, 2 * (int64_t)OG_RANGES_MAX);
+    og_dq_params w{};
+    w.Count = (uint32_t)count;
+    w.OffX = (uint32_t)offsetX;
+    w.OffY = (uint32_t)offsetY;
+    w.OffScale = (uint32_t)offsetScale;
+    w.OffZero = (uint32_t)offsetZeroPoint;
+    GpuBuffer X = x, Y = y, S = scale, Z = zeroPoint, R = ranges.Buffer;
+    std::shared_ptr<uint32_t> groups = ranges.Groups;
+    blocks_.Note(3, {&X, &Y, &S, &Z, &R});   // the quantize pass over the recorded ranges
+    encoder.Record(
+        [w, X, Y, S, Z, R, groups](og_ctx *ctx) {
+            // The ranged product recorded before this pass has run by now (Submit runs the recorded work in order).
+            ThrowIfFailed(ctx, og_dynamic_quantize_ranged(ctx, &w, bind(X), bind(Y), bind(S), bind(Z), bind(R), *groups),
+                          "DynamicQuantizeLinear");
+        },
+        keep_of({&X, &Y, &S, &Z, &R}));
 }
 
 // ------------------------------------------------------------------ DequantizeKernels

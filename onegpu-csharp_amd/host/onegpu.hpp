@@ -220,6 +220,17 @@ struct Int8Scratch {
     int Offset = 0;
 };
 
+// This library's own: where a ranged float product (Int8Gemm::EncodeFloatRanged) records the range of what it stores,
+// for DynamicQuantizeKernels::EncodeRanged to quantize that output with no read pass. Buffer: 2 * OG_RANGES_MAX float32
+// (a GpuBuffer of that length, or one the instance creates); Groups: the (min, max) pairs the last ranged product
+// recorded into it wrote, known once that product has run (Submit), read by the quantize pass when it runs.
+struct Int8Ranges {
+    Int8Ranges() = default;
+    explicit Int8Ranges(GpuBuffer buffer);
+    GpuBuffer Buffer;
+    std::shared_ptr<uint32_t> Groups = std::make_shared<uint32_t>(0);
+};
+
 // What a kernel family's bind groups (Int8Gemm.cs:365-375; BindingCacheTests.cs:141-197) become on HIP. Nothing is
 // bound: a dispatch's arguments travel by value in its launch packet. A family instead remembers the argument blocks it
 // has recorded, one per dispatch kind and set of buffers (offsets and sizes are launch arguments, as they are uniforms
@@ -275,6 +286,16 @@ public:
                            const std::optional<Int8Operand> &zeroPointB = std::nullopt,
                            const std::optional<Int8Operand> &floatBias = std::nullopt,
                            const std::optional<Int8Operand> &intBias = std::nullopt);
+    // This library's own: EncodeFloat (or EncodeFloatScaled, with activationScale) that also records the range of the
+    // values it stores in `ranges`, so DynamicQuantizeKernels::EncodeRanged can quantize c without a read pass. The same
+    // bits in c; c is dense (Int8GemmProblem's C always is) and holds at most 2^31 - 1 elements.
+    void EncodeFloatRanged(GpuCommandEncoder &encoder, const Int8GemmProblem &problem, const GpuBuffer &a,
+                           const GpuBuffer &b, const GpuBuffer &c, const Int8Operand &scale, const Int8Ranges &ranges,
+                           const std::optional<Int8Operand> &zeroPointA = std::nullopt,
+                           const std::optional<Int8Operand> &zeroPointB = std::nullopt,
+                           const std::optional<Int8Operand> &floatBias = std::nullopt,
+                           const std::optional<Int8Operand> &intBias = std::nullopt,
+                           const std::optional<Int8Operand> &activationScale = std::nullopt);
     // Int8Gemm.cs:316-363: QLinearMatMul, the sums in scratch, then the requantizing pass.
     void EncodeRequantized(GpuCommandEncoder &encoder, const Int8GemmProblem &problem, const GpuBuffer &a,
                            const GpuBuffer &b, const GpuBuffer &y, const Int8Operand &multiplier, int zeroPointY,
@@ -300,6 +321,7 @@ private:
         bool Requantized = false;   // C is the 8-bit output; Scale holds the multiplier (og_int8_gemm_requantized)
         GpuBuffer ActScale;         // when valid: the column scale is fl(ActScale[OffActScale] * Scale[..])
         uint32_t OffActScale = 0;
+        const Int8Ranges *Ranges = nullptr;   // a ranged float product (og_int8_gemm_float_ranged)
         int ZeroPointY = 0;
         bool SignedY = false;
         GpuBuffer IntBias;
@@ -316,7 +338,7 @@ private:
                       const GpuBuffer &b, const GpuBuffer &c, const Int8Operand *activationScale,
                       const Int8Operand &scale, const std::optional<Int8Operand> &zeroPointA,
                       const std::optional<Int8Operand> &zeroPointB, const std::optional<Int8Operand> &floatBias,
-                      const std::optional<Int8Operand> &intBias);
+                      const std::optional<Int8Operand> &intBias, const Int8Ranges *ranges = nullptr);
     void Multiply(GpuCommandEncoder &encoder, const Int8GemmProblem &p, const GpuBuffer &a, bool aSigned,
                   const GpuBuffer &b, bool bSigned, const GpuBuffer &c, int offsetC,
                   const std::optional<Int8Operand> &za, const std::optional<Int8Operand> &zb, const Epilogue &epi);
@@ -337,6 +359,11 @@ public:
     // DynamicQuantizeKernels.cs:47-90.
     void Encode(GpuCommandEncoder &encoder, const GpuBuffer &x, int offsetX, int count, const GpuBuffer &y, int offsetY,
                 const GpuBuffer &scale, int offsetScale, const GpuBuffer &zeroPoint, int offsetZeroPoint);
+    // This library's own: Encode of x, the output a ranged product (Int8Gemm::EncodeFloatRanged) recorded the range of
+    // in `ranges`: the quantize pass alone, one dispatch. The same y, scale and zero point.
+    void EncodeRanged(GpuCommandEncoder &encoder, const GpuBuffer &x, int offsetX, int count, const GpuBuffer &y,
+                      int offsetY, const GpuBuffer &scale, int offsetScale, const GpuBuffer &zeroPoint,
+                      int offsetZeroPoint, const Int8Ranges &ranges);
     int BindGroupsCreated() const { return blocks_.Created(); }
     void ReleaseBindings() { blocks_.Release(); }
     void Dispose() {}

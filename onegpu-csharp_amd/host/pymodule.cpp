@@ -196,6 +196,12 @@ PYBIND11_MODULE(_onegpu_host, m)
         .def_readwrite("Offset", &Int8Operand::Offset)
         .def_readwrite("IsVector", &Int8Operand::IsVector);
 
+    py::class_<Int8Ranges>(m, "Int8Ranges")
+        .def(py::init([](GpuBuffer b) { return Int8Ranges(std::move(b)); }), py::arg("Buffer"))
+        .def_readwrite("Buffer", &Int8Ranges::Buffer)
+        .def_property_readonly("Groups", [](const Int8Ranges &r) { return *r.Groups; });
+    m.attr("OG_RANGES_MAX") = (int)OG_RANGES_MAX;
+
     py::class_<Int8Scratch>(m, "Int8Scratch")
         .def(py::init([](GpuBuffer b, int off) { return Int8Scratch{b, off}; }), py::arg("Buffer"), py::arg("Offset") = 0)
         .def_readwrite("Buffer", &Int8Scratch::Buffer)
@@ -227,6 +233,10 @@ PYBIND11_MODULE(_onegpu_host, m)
         .def("EncodeFloat", &Int8Gemm::EncodeFloat, py::arg("encoder"), py::arg("problem"), py::arg("a"), py::arg("b"),
              py::arg("c"), py::arg("scale"), py::arg("zeroPointA") = py::none(), py::arg("zeroPointB") = py::none(),
              py::arg("floatBias") = py::none(), py::arg("intBias") = py::none())
+        .def("EncodeFloatRanged", &Int8Gemm::EncodeFloatRanged, py::arg("encoder"), py::arg("problem"), py::arg("a"),
+             py::arg("b"), py::arg("c"), py::arg("scale"), py::arg("ranges"), py::arg("zeroPointA") = py::none(),
+             py::arg("zeroPointB") = py::none(), py::arg("floatBias") = py::none(), py::arg("intBias") = py::none(),
+             py::arg("activationScale") = py::none())
         .def("EncodeFloatScaled", &Int8Gemm::EncodeFloatScaled, py::arg("encoder"), py::arg("problem"), py::arg("a"),
              py::arg("b"), py::arg("c"), py::arg("activationScale"), py::arg("weightScale"),
              py::arg("zeroPointA") = py::none(), py::arg("zeroPointB") = py::none(), py::arg("floatBias") = py::none(),
@@ -248,6 +258,9 @@ PYBIND11_MODULE(_onegpu_host, m)
         .def("Encode", &DynamicQuantizeKernels::Encode, py::arg("encoder"), py::arg("x"), py::arg("offsetX"),
              py::arg("count"), py::arg("y"), py::arg("offsetY"), py::arg("scale"), py::arg("offsetScale"),
              py::arg("zeroPoint"), py::arg("offsetZeroPoint"))
+        .def("EncodeRanged", &DynamicQuantizeKernels::EncodeRanged, py::arg("encoder"), py::arg("x"),
+             py::arg("offsetX"), py::arg("count"), py::arg("y"), py::arg("offsetY"), py::arg("scale"),
+             py::arg("offsetScale"), py::arg("zeroPoint"), py::arg("offsetZeroPoint"), py::arg("ranges"))
         .def_property_readonly("BindGroupsCreated", &DynamicQuantizeKernels::BindGroupsCreated)
         .def("ReleaseBindings", &DynamicQuantizeKernels::ReleaseBindings)
         .def("Dispose", &DynamicQuantizeKernels::Dispose)

@@ -12,7 +12,8 @@ try:
     from ._onegpu_host import (ConvIntegerKernels, ConvProblem, DequantizeKernels, DynamicQuantizeKernels, ElementType,
                                GatherKernels, GpuBuffer,
                                GpuCommandEncoder, GpuComputeCapabilities, GpuDevice, GpuIndexStatus, Int8Gemm,
-                               Int8GemmOptions, Int8GemmProblem, Int8Operand, Int8Scratch, version)
+                               Int8GemmOptions, Int8GemmProblem, Int8Operand, Int8Ranges, Int8Scratch,
+                               OG_RANGES_MAX, version)
 except ImportError as e:  # pragma: no cover - a build problem, reported as such
     raise ImportError("onegpu_hip: the native extension is not built; run python onegpu-csharp_amd/build.py "
                       f"(or __graft_entry__.build()) first: {e}") from e
@@ -37,6 +38,6 @@ def padded_half_length(count: int) -> int:
 __all__ = ["ConvIntegerKernels", "ConvProblem", "DequantizeKernels", "DynamicQuantizeKernels", "ElementType", "GatherKernels", "GpuIndexStatus",
            "GpuKernelIndexException", "GpuBuffer", "GpuCommandEncoder",
            "GpuComputeCapabilities", "GpuDevice", "Int8Gemm", "Int8GemmOptions", "Int8GemmProblem", "Int8Operand",
-           "Int8Scratch", "GpuException", "GpuKernelShapeException", "GpuUnsupportedException", "GpuOutOfMemoryException",
+           "Int8Ranges", "OG_RANGES_MAX", "Int8Scratch", "GpuException", "GpuKernelShapeException", "GpuUnsupportedException", "GpuOutOfMemoryException",
            "GpuDeviceLostException", "GpuCommandFailedException", "padded_bool_length", "padded_half_length", "LIB_PATH",
            "version"]

@@ -554,3 +554,56 @@ def test_kernel_choice_is_reported():
     assert name(M=2048, N=3072, K=768) == "mfma-i8-direct128x128x64"          # 384 tiles: two workgroups a CU
     assert name(M=256, N=256, K=448) == "mfma-i8-direct128x128x64"            # 7 stages: too short to split
     assert name(M=1, N=11008, K=4096, Flags=0x400) == "portable-tile64x64x16"
+
+
+class DqParams(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in ("Count", "OffX", "OffY", "GridX", "Groups", "OffScale", "OffZero")]
+
+
+def test_ranged_entry_points_validate_before_touching_a_device():
+    # og_int8_gemm_float_ranged and og_dynamic_quantize_ranged (the quantize pass over a ranged product's output):
+    # the float result bit, a ranges buffer of OG_RANGES_MAX pairs, a dense C, a groups count in range. With no context
+    # a valid call reports that there is no device. Host addresses stand in for device ones: nothing is dereferenced.
+    lib = ctypes.CDLL(og.LIB_PATH)
+    lib.og_int8_gemm_float_ranged.argtypes = ([ctypes.c_void_p, ctypes.POINTER(GemmParams), ctypes.c_uint32] +
+                                              [Buf] * 7 + [ctypes.c_uint32, Buf, Buf, Buf,
+                                                           ctypes.POINTER(ctypes.c_uint32)])
+    lib.og_dynamic_quantize_ranged.argtypes = [ctypes.c_void_p, ctypes.POINTER(DqParams)] + [Buf] * 5 + [ctypes.c_uint32]
+    lib.og_last_error_argument.restype = ctypes.c_char_p
+    lib.og_last_error_argument.argtypes = [ctypes.c_void_p]
+    host = (ctypes.c_uint8 * 65536)()
+    addr = ctypes.addressof(host)
+    none = Buf(None, 0)
+    assert og.OG_RANGES_MAX == 1024
+    ranges_ok = Buf(addr + 32768, 8 * og.OG_RANGES_MAX)
+    groups = ctypes.c_uint32(7)
+
+    def gemm(epi=0x1 | 0x4, batch=1, stride_c=0, ranges=ranges_ok, act=none, g=ctypes.byref(groups)):
+        # 4 x 8 x 16 product, A u8, B i8, float result with a per-column scale
+        p = GemmParams(M=4, N=8, K=16, Flags=0x2, Epi=epi, StrideA=64, StrideB=128, StrideC=stride_c)
+        st = lib.og_int8_gemm_float_ranged(None, ctypes.byref(p), batch, Buf(addr, 256), Buf(addr, 512),
+                                           Buf(addr + 1024, 512), none, none, none, act, 0, Buf(addr + 2048, 64),
+                                           none, ranges, g)
+        return st, lib.og_last_error_argument(None).decode()
+
+    assert gemm() == (6, "ctx")
+    assert gemm(epi=0) == (1, "Epi")                                  # an int32 product has no range
+    assert gemm(ranges=Buf(addr + 32768, 8 * og.OG_RANGES_MAX - 8)) == (1, "ranges")
+    assert gemm(ranges=Buf(addr + 32772, 8 * og.OG_RANGES_MAX)) == (1, "ranges")   # not 8-byte aligned
+    assert gemm(batch=2, stride_c=40) == (1, "StrideC")               # C must be dense
+    assert gemm(batch=2, stride_c=32) == (6, "ctx")
+    assert gemm(g=None) == (1, "groups")
+    assert gemm(act=Buf(addr + 3072, 4)) == (6, "ctx")                # with the activation scale (scaled form)
+
+    def quant(count=64, groups_=5, ranges=ranges_ok):
+        p = DqParams(Count=count)
+        st = lib.og_dynamic_quantize_ranged(None, ctypes.byref(p), Buf(addr, 4 * count), Buf(addr + 8192, count),
+                                            Buf(addr + 12288, 4), Buf(addr + 12292, 4), ranges, groups_)
+        return st, lib.og_last_error_argument(None).decode()
+
+    assert quant() == (6, "ctx")
+    assert quant(groups_=0) == (1, "groups")
+    assert quant(groups_=og.OG_RANGES_MAX + 1) == (1, "groups")
+    assert quant(groups_=og.OG_RANGES_MAX) == (6, "ctx")
+    assert quant(ranges=Buf(addr + 32768, 64)) == (1, "ranges")
+    assert quant(count=0) == (1, "count")
