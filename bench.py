@@ -266,6 +266,64 @@ def c2_bert_ffn(d, steps, warmup, check=True, fused_scale=True):
     return res
 
 
+def c2_two_layer(d, steps, warmup, ranged=True, check=True):
+    """Configuration 2 as the BERT FFN's two layers: DQ(x [1024 x 768]) -> MatMulIntegerToFloat with W1 [768 x 3072]
+    -> h [1024 x 3072] -> DQ(h) -> MatMulIntegerToFloat with W2 [3072 x 768] (both per-column symmetric, scales made in
+    the epilogue). ranged=True: layer 1 records the range of h as it stores it (EncodeFloatRanged), so DQ(h) is its
+    quantize pass alone (EncodeRanged); ranged=False: DQ(h) runs both passes, as the reference chains it
+    (Int8Tests.cs:705-751 per layer)."""
+    M, K, N = 1024, 768, 3072
+    x = synth(d, og.ElementType.Float32, M * K, 2, 30, 0.0, 1.0, 2)
+    w1, s1 = sym_weights(d, K, N, 2, 31)
+    w2, s2 = sym_weights(d, N, K, 2, 32)
+    ya, yh = d.CreateBufferOf(og.ElementType.UInt8, M * K), d.CreateBufferOf(og.ElementType.UInt8, M * N)
+    sa, sh = d.CreateBufferOf(og.ElementType.Float32, 1), d.CreateBufferOf(og.ElementType.Float32, 1)
+    za, zh = d.CreateBufferOf(og.ElementType.UInt8, 4), d.CreateBufferOf(og.ElementType.UInt8, 4)
+    h = d.CreateBufferOf(og.ElementType.Float32, M * N)
+    out = d.CreateBufferOf(og.ElementType.Float32, M * K)
+    ranges = og.Int8Ranges(d.CreateBufferOf(og.ElementType.Float32, 2 * og.OG_RANGES_MAX))
+    dq, gemm = og.DynamicQuantizeKernels(d), og.Int8Gemm(d)
+    p1, p2 = og.Int8GemmProblem(M, N, K), og.Int8GemmProblem(M, K, N)
+
+    def step(e, i):
+        dq.Encode(e, x, 0, M * K, ya, 0, sa, 0, za, 0)
+        if ranged:
+            gemm.EncodeFloatRanged(e, p1, ya, w1, h, og.Int8Operand(s1, 0, True), ranges, og.Int8Operand(za, 0),
+                                   activationScale=og.Int8Operand(sa, 0))
+            dq.EncodeRanged(e, h, 0, M * N, yh, 0, sh, 0, zh, 0, ranges)
+        else:
+            gemm.EncodeFloatScaled(e, p1, ya, w1, h, og.Int8Operand(sa, 0), og.Int8Operand(s1, 0, True),
+                                   og.Int8Operand(za, 0))
+            dq.Encode(e, h, 0, M * N, yh, 0, sh, 0, zh, 0)
+        gemm.EncodeFloatScaled(e, p2, yh, w2, out, og.Int8Operand(sh, 0), og.Int8Operand(s2, 0, True),
+                               og.Int8Operand(zh, 0))
+
+    wall, region, times = timed(d, step, steps, warmup)
+    # Per dispatch of a step, in order (the step launches the same kernel names more than once).
+    nd = len(times) // steps
+    per = {}
+    for j in range(nd):
+        ms = [times[i * nd + j][0] * 1e3 for i in range(steps)]
+        per[f"{j}: {times[j][1]}"] = {"mean_us": statistics.mean(ms), "median_us": statistics.median(ms)}
+    res = {"ops": 2.0 * 2 * M * N * K, "wall_s": wall, "chain_mean_ms": region / steps * 1e3, "per_kernel": per,
+           "dispatches": nd, "range_groups": ranges.Groups if ranged else None}
+    if check:
+        import oracle
+        H = h.Read()
+        wy, ws_, wz = oracle.dynamic_quantize(H)
+        ok = np.array_equal(yh.Read()[:M * N], wy) and int(zh.Read()[0]) == wz and \
+            np.float32(sh.Read()[0]).view(np.uint32) == np.float32(ws_).view(np.uint32)
+        rows = np.array([0, 5, 511, 1023])
+        W2, S2 = w2.Read(), s2.Read()
+        sums = oracle.int8_gemm_rows(oracle.Gemm(M, K, N), wy, False, W2.view(np.uint8), True, rows,
+                                     (np.array([wz], np.uint8), False, 0))
+        want = oracle.float_epilogue(sums.ravel(), K, (np.float32(ws_) * S2.astype(np.float32)).astype(np.float32),
+                                     True).reshape(len(rows), K)
+        ok = ok and np.array_equal(out.Read().reshape(M, K)[rows].view(np.uint32), want.view(np.uint32))
+        res["check"] = "bit-exact (DQ of h on every element, layer 2 on sampled rows)" if ok else "MISMATCH"
+    return res
+
+
 class C5:
     """Configuration 5's operands, resident on the device: x [32 x 512 x 4096] float32 N(0,1); 32 distinct int8 weight
     matrices [4096 x 4096] (each N(0, 0.02) quantized symmetric per column) with their 32 x 4096 column scales."""
@@ -685,6 +743,8 @@ def only(d, name, steps, warmup):
         r = c3_gemv(d, int(name[4:] or 1), steps, warmup, check=False)
     elif name == "c2":
         r = c2_bert_ffn(d, steps, warmup, check=False)
+    elif name in ("c2ffn", "c2ffn2"):
+        r = c2_two_layer(d, steps, warmup, ranged=name == "c2ffn", check=False)
     elif name == "c5":
         r = c5_batched(d, steps, warmup, check=False)[0]
     elif name == "c5chain":
@@ -716,7 +776,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline configuration only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["c4", "c4const", "c4nt", "c4plain", "c4plainnt", "gemv1", "gemv4", "gemv16", "c2", "c2q", "c2q2", "c5", "c5chain", "dequant", "quant", "dq", "gather4096", "gather65536", "resnet50", "whisper", "depthwise", "copy", "vendor"],
+    ap.add_argument("--only", choices=["c4", "c4const", "c4nt", "c4plain", "c4plainnt", "gemv1", "gemv4", "gemv16", "c2", "c2ffn", "c2ffn2", "c2q", "c2q2", "c5", "c5chain", "dequant", "quant", "dq", "gather4096", "gather65536", "resnet50", "whisper", "depthwise", "copy", "vendor"],
                     help="run one workload alone and print its summary (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -771,6 +831,13 @@ def main():
         configs["c2_bert_ffn_separate_scale"] = {"chain_mean_us": r["chain_mean_ms"] * 1e3,
                                                  "per_kernel": r["per_kernel"], "check": r["check"]}
         log(json.dumps(configs["c2_bert_ffn_separate_scale"]))
+        for ranged, key in ((True, "c2_ffn_two_layers_ranged"), (False, "c2_ffn_two_layers_two_pass_dq")):
+            log(f"config 2 as two FFN layers, DQ of the hidden layer {'from its recorded range' if ranged else 'in two passes'}")
+            r = c2_two_layer(d, args.steps, args.warmup, ranged)
+            configs[key] = {"chain_mean_us": r["chain_mean_ms"] * 1e3, "dispatches": r["dispatches"],
+                            "tops": r["ops"] / (r["chain_mean_ms"] * 1e-3) / 1e12, "per_kernel": r["per_kernel"],
+                            "range_groups": r["range_groups"], "check": r["check"]}
+            log(json.dumps(configs[key]))
         for fused, key in ((True, "qlinear_c2_one_launch"), (False, "qlinear_c2_two_passes")):
             log(f"QLinearMatMul on configuration 2's product, {'one launch' if fused else 'two passes'}")
             r = qlinear_c2(d, args.steps, args.warmup, fused)
