@@ -1198,7 +1198,9 @@ int og_gather(og_ctx *ctx, uint32_t elem_bytes, const og_gather_params *p, og_bu
 
 // ------------------------------------------------------------------ DynamicQuantizeLinear
 
-int og_dynamic_quantize(og_ctx *ctx, const og_dq_params *p, og_buffer X, og_buffer Y, og_buffer scale, og_buffer zero)
+// DynamicQuantizeLinear's argument checks (DynamicQuantizeKernels.cs:59-90) and its resolved arguments.
+static int dq_args(og_ctx *ctx, const og_dq_params *p, og_buffer X, og_buffer Y, og_buffer scale, og_buffer zero,
+                   og::DqArgs *d)
 {
     if (!p) return fail(ctx, OG_ERR_INVALID_ARG, "params", "null parameter block");
     if (p->Count < 1 || p->Count > 0x7FFFFFFFu) return fail(ctx, OG_ERR_INVALID_ARG, "count", "count %d must be at least 1", (int32_t)p->Count);
@@ -1206,13 +1208,21 @@ int og_dynamic_quantize(og_ctx *ctx, const og_dq_params *p, og_buffer X, og_buff
     if (!Y.ptr || !fits(p->OffY, p->Count, Y)) return fail(ctx, OG_ERR_INVALID_ARG, "y", "elements %u..%llu reach past the buffer", p->OffY, (unsigned long long)p->OffY + p->Count);
     if (!scale.ptr || ((uintptr_t)scale.ptr & 3) || !fits((uint64_t)p->OffScale * 4, 4, scale)) return fail(ctx, OG_ERR_INVALID_ARG, "scale", "element %u reaches past the buffer", p->OffScale);
     if (!zero.ptr || !fits(p->OffZero, 1, zero)) return fail(ctx, OG_ERR_INVALID_ARG, "zeroPoint", "element %u reaches past the buffer", p->OffZero);
-    if (!ctx) return fail(ctx, OG_ERR_NO_DEVICE, "ctx", "no context: the arguments are valid but there is no device to run on");
+    *d = og::DqArgs{};
+    d->x = static_cast<const float *>(X.ptr) + p->OffX;
+    d->y = static_cast<uint8_t *>(Y.ptr) + p->OffY;
+    d->scale = static_cast<float *>(scale.ptr) + p->OffScale;
+    d->zero = static_cast<uint8_t *>(zero.ptr) + p->OffZero;
+    d->count = p->Count;
+    return OG_OK;
+}
+
+int og_dynamic_quantize(og_ctx *ctx, const og_dq_params *p, og_buffer X, og_buffer Y, og_buffer scale, og_buffer zero)
+{
     og::DqArgs d{};
-    d.x = static_cast<const float *>(X.ptr) + p->OffX;
-    d.y = static_cast<uint8_t *>(Y.ptr) + p->OffY;
-    d.scale = static_cast<float *>(scale.ptr) + p->OffScale;
-    d.zero = static_cast<uint8_t *>(zero.ptr) + p->OffZero;
-    d.count = p->Count;
+    int st0 = dq_args(ctx, p, X, Y, scale, zero, &d);
+    if (st0 != OG_OK) return st0;
+    if (!ctx) return fail(ctx, OG_ERR_NO_DEVICE, "ctx", "no context: the arguments are valid but there is no device to run on");
     (void)hipSetDevice(ctx->device);
     int st = launch(ctx, "og_dynamic_quantize", [&](const char **k) { return og::launch_dynamic_quantize(d, ctx->ws, ctx->stream, k, 0); });
     if (st == OG_OK) st = launch(ctx, "og_dynamic_quantize", [&](const char **k) { return og::launch_dynamic_quantize(d, ctx->ws, ctx->stream, k, 1); });
@@ -1224,21 +1234,12 @@ int og_dynamic_quantize(og_ctx *ctx, const og_dq_params *p, og_buffer X, og_buff
 int og_dynamic_quantize_ranged(og_ctx *ctx, const og_dq_params *p, og_buffer X, og_buffer Y, og_buffer scale,
                                og_buffer zero, og_buffer ranges, uint32_t groups)
 {
-    if (!p) return fail(ctx, OG_ERR_INVALID_ARG, "params", "null parameter block");
-    if (p->Count < 1 || p->Count > 0x7FFFFFFFu) return fail(ctx, OG_ERR_INVALID_ARG, "count", "count %d must be at least 1", (int32_t)p->Count);
-    if (!X.ptr || ((uintptr_t)X.ptr & 3) || !fits((uint64_t)p->OffX * 4, (uint64_t)p->Count * 4, X)) return fail(ctx, OG_ERR_INVALID_ARG, "x", "elements %u..%llu reach past the buffer", p->OffX, (unsigned long long)p->OffX + p->Count);
-    if (!Y.ptr || !fits(p->OffY, p->Count, Y)) return fail(ctx, OG_ERR_INVALID_ARG, "y", "elements %u..%llu reach past the buffer", p->OffY, (unsigned long long)p->OffY + p->Count);
-    if (!scale.ptr || ((uintptr_t)scale.ptr & 3) || !fits((uint64_t)p->OffScale * 4, 4, scale)) return fail(ctx, OG_ERR_INVALID_ARG, "scale", "element %u reaches past the buffer", p->OffScale);
-    if (!zero.ptr || !fits(p->OffZero, 1, zero)) return fail(ctx, OG_ERR_INVALID_ARG, "zeroPoint", "element %u reaches past the buffer", p->OffZero);
+    og::DqArgs d{};
+    int st0 = dq_args(ctx, p, X, Y, scale, zero, &d);
+    if (st0 != OG_OK) return st0;
     if (!ranges.ptr || ((uintptr_t)ranges.ptr & 7) || ranges.bytes < 8ull * og::kRangesMax) return fail(ctx, OG_ERR_INVALID_ARG, "ranges", "the ranges need %d (min, max) pairs of float32, 8-byte aligned", og::kRangesMax);
     if (groups < 1 || groups > (uint32_t)og::kRangesMax) return fail(ctx, OG_ERR_INVALID_ARG, "groups", "%u pairs: between 1 and %d", groups, og::kRangesMax);
     if (!ctx) return fail(ctx, OG_ERR_NO_DEVICE, "ctx", "no context: the arguments are valid but there is no device to run on");
-    og::DqArgs d{};
-    d.x = static_cast<const float *>(X.ptr) + p->OffX;
-    d.y = static_cast<uint8_t *>(Y.ptr) + p->OffY;
-    d.scale = static_cast<float *>(scale.ptr) + p->OffScale;
-    d.zero = static_cast<uint8_t *>(zero.ptr) + p->OffZero;
-    d.count = p->Count;
     (void)hipSetDevice(ctx->device);
     int st = launch(ctx, "og_dynamic_quantize_ranged", [&](const char **k) {
         return og::launch_dynamic_quantize_ranged(d, static_cast<const float *>(ranges.ptr), groups, ctx->stream, k);
