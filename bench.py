@@ -572,6 +572,39 @@ def clock_of(kernel, workload):
         return None
 
 
+def c3_stream_floor(d, steps, warmup, copies=9):
+    """The floor configuration 3 is measured against, in one launch: og_util_stream_tiles reads B int8 [4096 x 11008]
+    (45 MB) in the one-launch few-rows kernel's own tiles, workgroups and loads and does nothing else; and a
+    device-to-device copy of the same 45 MB (read and write). `copies` matrices rotate, 405 MB in all, past the 256 MiB
+    Infinity Cache, as in configuration 3's leg."""
+    K, N = 4096, 11008
+    L = _abi()
+    L.og_util_stream_tiles.argtypes = [ctypes.c_void_p, _Buf, ctypes.c_uint32, ctypes.c_uint32, _Buf]
+    L.og_memcpy_d2d.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64]
+    bs = [synth(d, og.ElementType.Int8, K * N, 3, 20 + i, -127, 127, 0) for i in range(copies)]
+    sink = d.CreateBufferOf(og.ElementType.UInt32, 1)
+    dsts = [d.CreateBufferOf(og.ElementType.UInt8, K * N) for _ in range(2)]
+
+    def region(fn):
+        for i in range(warmup):
+            fn(i)
+        d.WaitIdle()
+        ms = ctypes.c_float(0.0)
+        _ok(L.og_timing_region_begin(d.Context), d)
+        for i in range(steps):
+            fn(warmup + i)
+        _ok(L.og_timing_region_end(d.Context, ctypes.byref(ms)), d)
+        d.WaitIdle()
+        return ms.value * 1e3 / steps
+
+    stream_us = region(lambda i: _ok(L.og_util_stream_tiles(d.Context, _b(bs[i % copies]), K, N, _b(sink)), d))
+    copy_us = region(lambda i: _ok(L.og_memcpy_d2d(d.Context, dsts[i % 2].DevicePointer, bs[i % copies].DevicePointer,
+                                                   K * N), d))
+    return {"bytes": K * N, "stream_tiles_us": stream_us, "stream_tiles_gbs": K * N / (stream_us * 1e-6) / 1e9,
+            "stream_tiles_frac": K * N / (stream_us * 1e-6) / 1e9 / PEAK_HBM_GBS, "copy_us": copy_us,
+            "copy_gbs_read_plus_write": 2 * K * N / (copy_us * 1e-6) / 1e9}
+
+
 def copy_workload(d, steps, warmup, mib=256):
     """A device-to-device copy of a known size (the counters' calibration for the traffic figures)."""
     n = mib << 20
@@ -759,6 +792,8 @@ def only(d, name, steps, warmup):
         r = embedding_gather(d, steps, warmup, int(name[6:] or 4096), check=False)
     elif name == "copy":
         r = copy_workload(d, steps, warmup)
+    elif name == "stream":
+        r = c3_stream_floor(d, steps, warmup)
     elif name in ("c4const", "c4nt", "c4plain", "c4plainnt"):
         r = c4_square(d, steps, warmup, check=False, constant=name == "c4const", trans_b=name.endswith("nt"),
                       plain=name.startswith("c4plain"))
@@ -776,7 +811,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline configuration only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["c4", "c4const", "c4nt", "c4plain", "c4plainnt", "gemv1", "gemv4", "gemv16", "c2", "c2ffn", "c2ffn2", "c2q", "c2q2", "c5", "c5chain", "dequant", "quant", "dq", "gather4096", "gather65536", "resnet50", "whisper", "depthwise", "copy", "vendor"],
+    ap.add_argument("--only", choices=["c4", "c4const", "c4nt", "c4plain", "c4plainnt", "gemv1", "gemv4", "gemv16", "c2", "c2ffn", "c2ffn2", "c2q", "c2q2", "c5", "c5chain", "dequant", "quant", "dq", "gather4096", "gather65536", "resnet50", "whisper", "depthwise", "copy", "stream", "vendor"],
                     help="run one workload alone and print its summary (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -817,6 +852,9 @@ def main():
                    "check": r["check"]}
         configs[f"c3_gemv_m{m}"] = gemv[m]
         log(json.dumps(gemv[m]))
+    log("config 3's floor: B read once in the one-launch kernel's tiles, and a 45 MB copy")
+    configs["c3_stream_floor"] = c3_stream_floor(d, args.steps, args.warmup)
+    log(json.dumps(configs["c3_stream_floor"]))
     if not args.quick:
         log("config 2: BERT FFN chain")
         r = c2_bert_ffn(d, args.steps, args.warmup)
@@ -915,7 +953,8 @@ def main():
             "metric": "GB/s at M=1 K=4096 N=11008 (MatMulIntegerToFloat, 9 rotating weight copies)",
             "value": round(g1["gbs"], 1), "unit": "GB/s",
             "roofline": {"bound": "hbm", "achieved": g1["gbs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": g1["frac"], "traffic": traffic_of(g1["kernels"][0], "gemv1")}},
+                         "frac": g1["frac"], "traffic": traffic_of(g1["kernels"][0], "gemv1")},
+            "floor": configs.get("c3_stream_floor")},
         "cpu_baseline": cpu,
         "configs": configs,
     }

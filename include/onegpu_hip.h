@@ -355,6 +355,10 @@ int og_util_synth(og_ctx *ctx, int kind, uint64_t seed, uint32_t tensor, og_buff
 int og_util_col_absmax_scale(og_ctx *ctx, og_buffer W, uint32_t rows, uint32_t cols, float divisor, og_buffer scale);
 /* out[i] = fl(a[0] * b[i]) for i < n (the on-device scale product of the dynamic int8 chain). */
 int og_util_scale_product(og_ctx *ctx, og_buffer a, og_buffer b, uint32_t n, og_buffer out);
+/* Reads B [K x N] (dense int8 rows, N a multiple of 16, K * N < 2^31) once, in the tiles, workgroups and loads of
+ * the one-launch few-rows product ("mfma-i8-rows16-xcd"), and does nothing else: the streaming floor that product is
+ * measured against (kernel name "stream-tiles"). `sink` (4 bytes) is written only on an unlikely checksum. */
+int og_util_stream_tiles(og_ctx *ctx, og_buffer B, uint32_t K, uint32_t N, og_buffer sink);
 
 /* ------------------------------------------------------------------ test hooks
  * (no counterpart in the reference: they let a test drive the failure path of the one-launch few-rows product,

@@ -1400,6 +1400,17 @@ int og_util_scale_product(og_ctx *ctx, og_buffer a, og_buffer b, uint32_t n, og_
     return st == OG_OK ? ok(ctx) : st;
 }
 
+int og_util_stream_tiles(og_ctx *ctx, og_buffer B, uint32_t K, uint32_t N, og_buffer sink)
+{
+    if (K < 1 || N < 16 || N % 16 || (uint64_t)K * N > 0x7FFFFFFFull) return fail(ctx, OG_ERR_INVALID_ARG, "K", "K >= 1, N >= 16 a multiple of 16, K * N < 2^31");
+    if (!B.ptr || ((uintptr_t)B.ptr & 15) || !fits(0, (uint64_t)K * N, B)) return fail(ctx, OG_ERR_INVALID_ARG, "B", "B reaches past the buffer or is not 16-byte aligned");
+    if (!sink.ptr || ((uintptr_t)sink.ptr & 3) || !fits(0, 4, sink)) return fail(ctx, OG_ERR_INVALID_ARG, "sink", "the sink needs 4 aligned bytes");
+    if (!ctx) return fail(ctx, OG_ERR_NO_DEVICE, "ctx", "no context");
+    (void)hipSetDevice(ctx->device);
+    int st = launch(ctx, "og_util_stream_tiles", [&](const char **k) { *k = "stream-tiles"; return og::launch_stream_tiles(static_cast<const uint8_t *>(B.ptr), (int32_t)K, (int32_t)N, static_cast<uint32_t *>(sink.ptr), ctx->stream); });
+    return st == OG_OK ? ok(ctx) : st;
+}
+
 // ------------------------------------------------------------------ test hooks
 
 int og_test_set_spin_limit(og_ctx *ctx, uint32_t polls)

@@ -397,6 +397,40 @@ hipError_t launch_xcc_probe(uint32_t *out, uint32_t groups, hipStream_t s)
     return hipGetLastError();
 }
 
+// The streaming floor of k_gemv_xcd's shapes (a benchmark utility): the same grid, tile mapping and loads of B (all
+// 16 issued at once, nontemporal), with nothing done with the bytes but a checksum that is stored only if it equals
+// an unlikely constant (so the loads stay live and nothing else touches memory).
+__global__ __launch_bounds__(GX_THREADS) void k_stream_tiles(const uint8_t *B, int32_t K, int32_t N, int32_t slabs,
+                                                             int32_t nkc, uint32_t *sink)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int32_t x8 = (int32_t)(blockIdx.x & 7u), jx = (int32_t)(blockIdx.x >> 3);
+    const int32_t q0 = (int32_t)((int64_t)x8 * slabs / 8), q1 = (int32_t)((int64_t)(x8 + 1) * slabs / 8);
+    const int32_t nq = q1 - q0;
+    if (jx >= nq * nkc) return;
+    const int32_t slab = q0 + jx % nq, kc = jx / nq;
+    const int32_t n0 = slab * GX_COLS, k0 = kc * GX_KT, rows = min(GX_KT, K - k0);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(B + (int64_t)k0 * N + n0), (short)0, (rows - 1) * N + min(GX_COLS, N - n0), 0x00020000);
+    const uint32_t r0 = (uint32_t)(8 * wave + (lane >> 3)) * (uint32_t)N + 16u * (uint32_t)(lane & 7);
+    v4i bv[GX_LOADS];
+#pragma unroll
+    for (int i = 0; i < GX_LOADS; i++) bv[i] = gx_load(rb, r0 + (uint32_t)(GX_ROWS_PER_LOAD * i) * (uint32_t)N);
+    v4i x = bv[0];
+#pragma unroll
+    for (int i = 1; i < GX_LOADS; i++) x ^= bv[i];
+    const uint32_t c = (uint32_t)(x.x ^ x.y ^ x.z ^ x.w);
+    if (c == 0x9E3779B9u) sink[0] = c;
+}
+
+hipError_t launch_stream_tiles(const uint8_t *B, int32_t K, int32_t N, uint32_t *sink, hipStream_t s)
+{
+    const int32_t slabs = (N + GX_COLS - 1) / GX_COLS, nkc = (K + GX_KT - 1) / GX_KT;
+    hipLaunchKernelGGL(k_stream_tiles, dim3((uint32_t)(8 * ((slabs + 7) / 8) * nkc)), dim3(GX_THREADS), 0, s, B, K, N,
+                       slabs, nkc, sink);
+    return hipGetLastError();
+}
+
 // The one-launch few-rows kernel's conditions: those of the two-launch tile kernel (B stored K x N; 16-byte aligned
 // rows; K and N multiples of 16), at least 16 column slabs (two an XCD) and at most 127 row bands (a 7-bit field of
 // the slab's word counts them).

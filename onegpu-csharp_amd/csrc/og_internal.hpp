@@ -215,6 +215,9 @@ hipError_t launch_synth(int kind, uint64_t seed, uint32_t tensor, void *out, uin
 hipError_t launch_col_absmax_scale(const float *w, uint32_t rows, uint32_t cols, float divisor, float *scale,
                                    hipStream_t s);
 hipError_t launch_scale_product(const float *a, const float *b, uint32_t n, float *out, hipStream_t s);
+// Reads B [K x N] (dense rows, N a multiple of 16) once in the few-rows one-launch kernel's tiles and loads, and does
+// nothing else (int8_gemv_xcd.hip): that kernel's streaming floor.
+hipError_t launch_stream_tiles(const uint8_t *B, int32_t K, int32_t N, uint32_t *sink, hipStream_t s);
 
 // ------------------------------------------------------------------ device helpers
 

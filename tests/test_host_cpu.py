@@ -607,3 +607,27 @@ def test_ranged_entry_points_validate_before_touching_a_device():
     assert quant(groups_=og.OG_RANGES_MAX) == (6, "ctx")
     assert quant(ranges=Buf(addr + 32768, 64)) == (1, "ranges")
     assert quant(count=0) == (1, "count")
+
+
+def test_stream_tiles_validates_before_touching_a_device():
+    # og_util_stream_tiles (the streaming floor of the one-launch few-rows product): N a multiple of 16, B 16-byte
+    # aligned and holding K x N bytes, a 4-byte sink. With no context a valid call reports that there is no device.
+    lib = ctypes.CDLL(og.LIB_PATH)
+    lib.og_util_stream_tiles.argtypes = [ctypes.c_void_p, Buf, ctypes.c_uint32, ctypes.c_uint32, Buf]
+    lib.og_last_error_argument.restype = ctypes.c_char_p
+    lib.og_last_error_argument.argtypes = [ctypes.c_void_p]
+    host = (ctypes.c_uint8 * 8192)()
+    addr = (ctypes.addressof(host) + 15) & ~15
+
+    def stream(k=64, n=64, b=None, sink=None):
+        b = Buf(addr, 4096) if b is None else b
+        sink = Buf(addr + 4096, 4) if sink is None else sink
+        st = lib.og_util_stream_tiles(None, b, k, n, sink)
+        return st, lib.og_last_error_argument(None).decode()
+
+    assert stream() == (6, "ctx")
+    assert stream(n=72) == (1, "K")                        # N not a multiple of 16
+    assert stream(k=0) == (1, "K")
+    assert stream(k=65) == (1, "B")                        # 65 x 64 bytes reach past the 4 KB buffer
+    assert stream(b=Buf(addr + 4, 4096)) == (1, "B")       # not 16-byte aligned
+    assert stream(sink=Buf(addr + 4096, 2)) == (1, "sink")

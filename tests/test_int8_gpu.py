@@ -786,3 +786,19 @@ def test_seeded_random_epilogues_are_bit_exact(config):
             kernels.add(d.LastKernel)
         assert bad == 0, f"{m}x{n}x{k}: {bad} wrong"
     say(f"ROW seeded random epilogues [{config}]: 24 shapes exact; kernels {sorted(kernels)}")
+
+
+def test_stream_tiles_reads_b_and_writes_nothing():
+    # og_util_stream_tiles, the streaming floor the few-rows product is measured against: it runs as "stream-tiles"
+    # over configuration 3's B and over a ragged shape, and leaves the sink alone (an all-zero B has checksum 0).
+    d = device()
+    L = abi()
+    L.og_util_stream_tiles.argtypes = [ctypes.c_void_p, L.Buf, ctypes.c_uint32, ctypes.c_uint32, L.Buf]
+    for k, n in ((4096, 11008), (1000, 144)):
+        say(f"stream-tiles {k} x {n}")
+        b = d.CreateBuffer(np.zeros(k * n, np.uint8))
+        sink = d.CreateBuffer(np.full(4, 0x5A, np.uint8))
+        check(L.og_util_stream_tiles(d.Context, binding(b), k, n, binding(sink)), d)
+        d.WaitIdle()
+        assert d.LastKernel == "stream-tiles"
+        assert np.array_equal(sink.Read()[:4], np.full(4, 0x5A, np.uint8))
