@@ -147,3 +147,50 @@ def test_ranged_pass_reports_a_missing_range():
         run(d, lambda e: og.DynamicQuantizeKernels(d).EncodeRanged(e, x, 0, 64, y, 0, s, 0, z, 0, ranges))
     assert ex.value.Argument == "groups"
     d.WaitIdle()
+
+
+def test_ranged_seeded_random_shapes():
+    # 24 seeded random shapes (aligned ones that take the range epilogues and ragged ones that take a range pass),
+    # batch 1 or 2, with and without biases: the float output, the recorded ranges and the quantize pass alone against
+    # the oracle's DynamicQuantizeLinear of that output, bit for bit.
+    d = device()
+    gemm = og.Int8Gemm(d)
+    dq = og.DynamicQuantizeKernels(d)
+    ranges = og.Int8Ranges(d.CreateBufferOf(og.ElementType.Float32, 2 * og.OG_RANGES_MAX))
+    rng = np.random.default_rng(2024)
+    kernels = set()
+    for i in range(24):
+        if i % 2 == 0:
+            m, n, k = int(rng.choice([1, 4, 16, 100, 256, 333])), 16 * int(rng.integers(1, 48)), 64 * int(rng.integers(1, 20))
+        else:
+            m, n, k = (int(rng.integers(1, 300)) for _ in range(3))
+        batch = int(rng.integers(1, 3))
+        biases = bool(rng.integers(0, 2))
+        say(f"ranged random {i}: {batch} x {m}x{n}x{k} biases {biases}")
+        bufs, want, _ = _layer(d, gemm, m, n, k, batch, 7000 + i, float(rng.random() * 0.05 + 1e-3), fbias=biases,
+                               ibias=biases)
+        run(d, lambda e: gemm.EncodeFloatRanged(e, og.Int8GemmProblem(m, n, k) if batch == 1 else _problem(m, n, k, batch),
+                                                bufs["a"], bufs["b"], bufs["c"], og.Int8Operand(bufs["ws"], 0, True), ranges,
+                                                og.Int8Operand(bufs["za"], 0), None,
+                                                og.Int8Operand(bufs["fb"], 0, True) if biases else None,
+                                                og.Int8Operand(bufs["ib"], 0, True) if biases else None,
+                                                og.Int8Operand(bufs["act"], 0)))
+        d.WaitIdle()
+        kernels.add(d.LastKernel)
+        c = bufs["c"].Read()
+        assert _same_bits(c, want) == 0, f"case {i}: the float output"
+        groups = ranges.Groups
+        assert 1 <= groups <= og.OG_RANGES_MAX
+        r = ranges.Buffer.Read()[:2 * groups].reshape(groups, 2)
+        finite = c[~np.isnan(c)]
+        assert r[:, 0].min() == finite.min() and r[:, 1].max() == finite.max(), f"case {i}: the ranges"
+        y = d.CreateBufferOf(og.ElementType.UInt8, c.size)
+        s = d.CreateBufferOf(og.ElementType.Float32, 1)
+        z = d.CreateBufferOf(og.ElementType.UInt8, 4)
+        run(d, lambda e: dq.EncodeRanged(e, bufs["c"], 0, c.size, y, 0, s, 0, z, 0, ranges))
+        d.WaitIdle()
+        wy, ws_, wz = oracle.dynamic_quantize(c)
+        got_y, got_s, got_z = y.Read()[:c.size], np.float32(s.Read()[0]), int(z.Read()[0])
+        assert np.array_equal(got_y, wy) and got_s.view(np.uint32) == np.float32(ws_).view(np.uint32) and got_z == wz, \
+            f"case {i}: DynamicQuantizeLinear from the ranges"
+    say(f"ROW ranged seeded random: 24 shapes exact; kernels {sorted(kernels)}")
