@@ -172,10 +172,11 @@ def c4_square(d, steps, warmup, check=True, constant=False, trans_b=False, plain
     return res
 
 
-def c3_gemv(d, m, steps, warmup, copies=9, check=True):
-    """Configuration 3: A = DynamicQuantizeLinear(N(0,1) [m x 4096]); B int8 [4096 x 11008] symmetric per column
-    (N(0, 0.02)); MatMulIntegerToFloat with scale = actScale * wScale[n]. `copies` weight matrices rotate."""
-    K, N = 4096, 11008
+def c3_gemv(d, m, steps, warmup, copies=9, check=True, n=11008):
+    """Configuration 3: A = DynamicQuantizeLinear(N(0,1) [m x 4096]); B int8 [4096 x n] symmetric per column
+    (N(0, 0.02)); MatMulIntegerToFloat with scale = actScale * wScale[n]. `copies` weight matrices rotate. n = 1376 is
+    one GPU's share of an 8-way column split of configuration 3's weights."""
+    K, N = 4096, n
     x = synth(d, og.ElementType.Float32, m * K, 3, 10, 0.0, 1.0, 2)
     ya = d.CreateBufferOf(og.ElementType.UInt8, m * K)
     s = d.CreateBufferOf(og.ElementType.Float32, 1)
@@ -772,6 +773,8 @@ def only(d, name, steps, warmup):
     if name == "c4":
         r = c4_square(d, steps, warmup, check=False)
         r.pop("host_operands", None)
+    elif name == "gemvshard":
+        r = c3_gemv(d, 1, steps, warmup, copies=48, check=False, n=1376)
     elif name.startswith("gemv"):
         r = c3_gemv(d, int(name[4:] or 1), steps, warmup, check=False)
     elif name == "c2":
@@ -811,7 +814,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline configuration only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["c4", "c4const", "c4nt", "c4plain", "c4plainnt", "gemv1", "gemv4", "gemv16", "c2", "c2ffn", "c2ffn2", "c2q", "c2q2", "c5", "c5chain", "dequant", "quant", "dq", "gather4096", "gather65536", "resnet50", "whisper", "depthwise", "copy", "stream", "vendor"],
+    ap.add_argument("--only", choices=["c4", "c4const", "c4nt", "c4plain", "c4plainnt", "gemv1", "gemv4", "gemv16", "gemvshard", "c2", "c2ffn", "c2ffn2", "c2q", "c2q2", "c5", "c5chain", "dequant", "quant", "dq", "gather4096", "gather65536", "resnet50", "whisper", "depthwise", "copy", "stream", "vendor"],
                     help="run one workload alone and print its summary (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -852,6 +855,15 @@ def main():
                    "check": r["check"]}
         configs[f"c3_gemv_m{m}"] = gemv[m]
         log(json.dumps(gemv[m]))
+    if not args.quick:
+        log("config 3 at one GPU's share of an 8-way column split: M=1, N=1376")
+        r = c3_gemv(d, 1, args.steps, args.warmup, copies=48, n=1376)
+        gbs = r["bytes"] / (r["step_mean_ms"] * 1e-3) / 1e9
+        configs["c3_gemv_m1_shard8"] = {"n": 1376, "weight_copies": 48, "gbs": gbs, "frac": gbs / PEAK_HBM_GBS,
+                                        "step_mean_us": r["step_mean_ms"] * 1e3, "kernels": r["kernels"],
+                                        "dispatch_mean_us": [t * 1e3 for t in r["dispatch_mean_ms"]],
+                                        "bytes": r["bytes"], "check": r["check"]}
+        log(json.dumps(configs["c3_gemv_m1_shard8"]))
     log("config 3's floor: B read once in the one-launch kernel's tiles, and a 45 MB copy")
     configs["c3_stream_floor"] = c3_stream_floor(d, args.steps, args.warmup)
     log(json.dumps(configs["c3_stream_floor"]))
