@@ -83,12 +83,18 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p)
 // assembly (an s_add there would change SCC behind the compiler's back) and moved into M0 with s_mov, which leaves
 // SCC alone. M0 is written without being saved: the compiler reserves M0 and these kernels give it nothing to hold
 // across a DMA (no indexed register access, s_sendmsg, GWS or LDS-DMA intrinsics; checked in the disassembly of
-// every kernel that includes this file: M0 is written only here).
+// every kernel that includes this file: M0 is written only here). The resource words are uniform; readfirstlane states
+// so, which keeps them in scalar registers where the compiler's uniformity analysis alone would not (the epilogue's
+// store loop, inlined into the 4-wave kernels, otherwise leaves it unsure).
 template <int OFF>
 __device__ __forceinline__ void dma16(u4w rsrc, uint32_t base, uint32_t voff)
 {
+    const u4w r = {(uint32_t)__builtin_amdgcn_readfirstlane((int)rsrc.x),
+                   (uint32_t)__builtin_amdgcn_readfirstlane((int)rsrc.y),
+                   (uint32_t)__builtin_amdgcn_readfirstlane((int)rsrc.z),
+                   (uint32_t)__builtin_amdgcn_readfirstlane((int)rsrc.w)};
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" : : "s"(base + (uint32_t)OFF),
-                 "v"(voff), "s"(rsrc) : "memory");
+                 "v"(voff), "s"(r) : "memory");
 }
 
 // LDS serves 256 bytes a cycle: a 16-byte fragment read takes 16 lanes at a time (rows r .. r + 15 of A: the
@@ -688,7 +694,8 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_direct(GemmArgs g, int32_t 
     // The NaN-ignoring range of the float values this thread stores (for a ranged float product; 128 tile).
     float rmn = __int_as_float(0x7F800000), rmx = __int_as_float(0xFF800000);
     // MODE 0: int32 (+ bias); 1: float32, `opt` = float bias present; 2: requantized bytes, `opt` = uint8 output.
-    auto store_all = [&](auto mode_tag, bool opt) {
+    // Inlined: as a call it would keep a 1,408-byte stack frame a lane in the 4-wave kernels.
+    auto store_all = [&](auto mode_tag, bool opt) __attribute__((always_inline)) {
         constexpr int MODE = decltype(mode_tag)::value;
         if constexpr (BT == 128) {
             // Staged through LDS: one store instruction per thread then writes four neighbouring columns (16 bytes, or
