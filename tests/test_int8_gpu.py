@@ -788,6 +788,73 @@ def test_seeded_random_epilogues_are_bit_exact(config):
     say(f"ROW seeded random epilogues [{config}]: 24 shapes exact; kernels {sorted(kernels)}")
 
 
+# K either side of 32768, where the direct kernels' zero-point corrections leave the full-rate 24-bit multiply for the
+# 32-bit one. A column sum less K times B's zero point, in the signed domain, reaches 255 K: past 2^23 from K = 32897
+# on, so a 24-bit multiply at K = 40960 would be wrong. The other kernels, whose corrections are 32-bit throughout,
+# run the same sizes. (name, m, n, k, a signed, b signed, zp modes of A and B, configuration, kernel prefix.)
+LARGE_K_CASES = [
+    ("256 tile, both zero points", 256, 256, 40960, False, False, 2, 2, "large tile", "mfma-i8-direct256x256x64"),
+    ("256 tile, both zero points, below the switch", 256, 256, 32704, False, False, 1, 2, "large tile",
+     "mfma-i8-direct256x256x64"),
+    ("256 tile ping-pong, A's zero point per row", 256, 256, 40960, False, True, 2, 0, "large tile",
+     "mfma-i8-direct256x256x64"),
+    ("128 tile split along K", 128, 128, 40960, False, False, 1, 2, "default", "mfma-i8-direct128x128x64"),
+    ("128 tile whole, C misaligned for the staged store", 1152, 1920, 40960, False, False, 2, 2, "default",
+     "mfma-i8-direct128x128x64"),
+    ("register-staged tile, K not a multiple of 64", 64, 64, 40976, False, False, 2, 1, "tiled only",
+     "mfma-i8-tile128x128x128"),
+    ("generic kernel, unaligned rows", 64, 64, 40961, False, False, 1, 2, "tiled only", "mfma-i8-generic128x128x64"),
+    ("few rows, one launch", 4, 2048, 40960, False, False, 1, 2, "default", "mfma-i8-rows16-xcd"),
+]
+
+
+def _large_k_data(c, adversarial: bool, seed: int) -> dict:
+    """Random bytes, or the fill that makes every correction term extreme: A = 0 under a zero point of 255 (u8),
+    B = 255 under a zero point of 0 (u8; int8 B without a zero point takes -128)."""
+    data = cases.case_data(c, seed)
+    if adversarial:
+        data["a"][:] = 0x00
+        data["b"][:] = 0xFF if not c.b_signed else 0x80
+        if data["za"] is not None:
+            data["za"][:] = 0xFF
+        if data["zb"] is not None:
+            data["zb"][:] = 0x00
+    return data
+
+
+@pytest.mark.parametrize("case", LARGE_K_CASES, ids=[c[0] for c in LARGE_K_CASES])
+def test_large_k_corrections_are_bit_exact(case):
+    name, m, n, k, a_s, b_s, za_mode, zb_mode, config, prefix = case
+    d = device()
+    gemm = og.Int8Gemm(d, og.Int8GemmOptions(**CONFIG_OPTIONS[config]))
+    off_c = 1 if "misaligned" in name else 0
+    c = cases.Case(name, cases.problem(m, n, k, off_c=off_c), a_s, b_s, za_mode, zb_mode)
+    for adversarial in (False, True):
+        say(f"large K [{config}] {name} {m}x{n}x{k} adversarial {adversarial}")
+        data = _large_k_data(c, adversarial, 900 + k % 97 + m)
+        want = cases.reference_sums(c, data)
+        if adversarial:
+            # Every product term is (0 - 255)(255 - 0), or (0 - 255)(-128) for int8 B: K of them, modulo 2^32.
+            term = -255 * (-128 if b_s else 255)
+            closed = np.int64(term) * np.int64(k)
+            assert np.all(want == np.int32(np.uint32(closed & 0xFFFFFFFF).view(np.int32)))
+        out = np.full(off_c + m * n + 2, 0x5A5A5A5A, np.int32)
+        bc = d.CreateBuffer(out)
+        ba = d.CreateBuffer(as_u8(data["a"]))
+        bb = d.CreateBuffer(as_i8(data["b"]) if b_s else as_u8(data["b"]))
+        za = og.Int8Operand(d.CreateBuffer(as_u8(data["za"])), 0, za_mode == 2) if data["za"] is not None else None
+        zb = og.Int8Operand(d.CreateBuffer(as_u8(data["zb"])), 0, zb_mode == 2) if data["zb"] is not None else None
+        run(d, lambda e: gemm.EncodeInt32(e, to_problem(c.p), ba, bb, bc, za, zb))
+        d.WaitIdle()   # reports a one-launch product whose parts never arrived
+        got = bc.Read()
+        kernel = d.LastKernel
+        bad = int(np.count_nonzero(got[off_c:off_c + m * n] != want))
+        bad += int(np.count_nonzero(got[:off_c] != 0x5A5A5A5A)) + int(np.count_nonzero(got[off_c + m * n:] != 0x5A5A5A5A))
+        say(f"ROW large K | {name} | {kernel} | adversarial {adversarial} | mismatches {bad}")
+        assert kernel.startswith(prefix), kernel
+        assert bad == 0
+
+
 def test_stream_tiles_reads_b_and_writes_nothing():
     # og_util_stream_tiles, the streaming floor the few-rows product is measured against: it runs as "stream-tiles"
     # over configuration 3's B and over a ragged shape, and leaves the sink alone (an all-zero B has checksum 0).

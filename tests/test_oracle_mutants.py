@@ -228,3 +228,42 @@ def test_gather_pin_catches_unwrapped_negative_indices():
 
 def test_conv_pin_catches_zero_padding():
     assert not pin_conv(_conv_pad_zero)
+
+
+# ------------------------------------------------------------------ the large-K GPU case has teeth
+
+def _identity_one(k, a_byte, za, b_byte, zb, mul) -> int:
+    """One output of the product kernels' signed-domain identity for constant uint8 operands and zero points,
+    C = acc - w' s - z' (t - K w') modulo 2^32 (s, t the byte sums, z', w' the zero points, all moved by -128), with
+    the two correction products formed by `mul`."""
+    s, t = k * (a_byte - 128), k * (b_byte - 128)
+    zp, wp = za - 128, zb - 128
+    acc = k * (a_byte - 128) * (b_byte - 128)
+    v = (acc - mul(wp, s) - mul(zp, t - k * wp)) & 0xFFFFFFFF
+    return v - (1 << 32) if v & 0x80000000 else v
+
+
+def _mul32(a, b) -> int:
+    return (a * b) & 0xFFFFFFFF
+
+
+def _mul24(a, b) -> int:
+    """The 24-bit multiply: each operand's low 24 bits as a signed number, the product's low 32 bits."""
+    def sx(x):
+        x &= 0xFFFFFF
+        return x - (1 << 24) if x & 0x800000 else x
+    return (sx(a) * sx(b)) & 0xFFFFFFFF
+
+
+def test_large_k_case_catches_a_24_bit_correction_multiply():
+    # The adversarial fill of test_large_k_corrections_are_bit_exact (A = 0 under zero point 255, B = 255 under zero
+    # point 0): the identity with 32-bit products gives the definition's sums at both sizes; with the 24-bit multiply
+    # it still does at K = 32704, below the kernels' switch, and no longer at K = 40960.
+    import test_int8_gpu
+    sizes = {c[3] for c in test_int8_gpu.LARGE_K_CASES}
+    assert {32704, 40960} <= sizes
+    for k in (32704, 40960):
+        want = int(np.int64(-255 * 255 * k).astype(np.int64) & 0xFFFFFFFF)
+        want = want - (1 << 32) if want & 0x80000000 else want
+        assert _identity_one(k, 0x00, 0xFF, 0xFF, 0x00, _mul32) == want
+        assert (_identity_one(k, 0x00, 0xFF, 0xFF, 0x00, _mul24) == want) == (k < 32768)
