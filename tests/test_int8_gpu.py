@@ -805,6 +805,9 @@ LARGE_K_CASES = [
      "mfma-i8-tile128x128x128"),
     ("generic kernel, unaligned rows", 64, 64, 40961, False, False, 1, 2, "tiled only", "mfma-i8-generic128x128x64"),
     ("few rows, one launch", 4, 2048, 40960, False, False, 1, 2, "default", "mfma-i8-rows16-xcd"),
+    # 127 k-slices a column slab, the most its 7-bit count fields take; 128 go to the two-launch kernel.
+    ("few rows, one launch, 127 k-slices", 3, 2048, 127 * 512, False, True, 2, 0, "default", "mfma-i8-rows16-xcd"),
+    ("few rows, 128 k-slices", 3, 2048, 128 * 512, False, True, 2, 0, "default", "mfma-i8-rows16-tiles"),
 ]
 
 
