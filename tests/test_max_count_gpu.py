@@ -91,3 +91,30 @@ def test_quantize_at_the_largest_count(x_max):
     bad = _same(got, want)
     say(f"ROW quantize at count {MAX4} | {kernel} | mismatching bytes {bad}")
     assert bad == 0
+
+
+def test_product_at_the_largest_output():
+    # C of 32768 x 65520 int32 (2,146,959,360 elements, 8 GiB), just under the boundary's limit of 2^31 elements, so
+    # output indices reach the top of the range. A[m][k] = m % 251 (uint8) under a zero point of 7, B[k][n] = n % 13 - 6
+    # (int8): C[m][n] = K (m % 251 - 7)(n % 13 - 6), a closed form checked for every element in chunks of rows.
+    d = device()
+    m, n, k = 32768, 65520, 64
+    gemm = og.Int8Gemm(d)
+    say(f"product at the largest output {m}x{n}x{k}")
+    a = np.repeat((np.arange(m) % 251).astype(np.uint8), k)
+    b = np.tile(((np.arange(n) % 13) - 6).astype(np.int8), k)
+    ba, bb = d.CreateBuffer(a), d.CreateBuffer(b)
+    bz = d.CreateBuffer(np.array([7, 0, 0, 0], np.uint8))
+    bc = d.CreateBufferOf(og.ElementType.Int32, m * n)
+    run(d, lambda e: gemm.EncodeInt32(e, og.Int8GemmProblem(m, n, k), ba, bb, bc, og.Int8Operand(bz, 0), None))
+    kernel = d.LastKernel
+    got = bc.Read()
+    del bc
+    col = (np.arange(n) % 13 - 6).astype(np.int64)
+    bad = 0
+    for r0 in range(0, m, 1024):
+        row = (np.arange(r0, r0 + 1024) % 251 - 7).astype(np.int64)
+        want = (k * row[:, None] * col[None, :]).astype(np.int32)
+        bad += int(np.count_nonzero(got[r0 * n:(r0 + 1024) * n].reshape(1024, n) != want))
+    say(f"ROW product at the largest output | {kernel} | mismatching elements {bad}")
+    assert bad == 0
