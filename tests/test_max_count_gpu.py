@@ -2,7 +2,8 @@
 float32 tensor of 8 GiB, whose last block of 4096 elements holds 4095), DequantizeLinear (uint8 to float32) and
 QuantizeLinear (float32 to uint8) at 2^31 - 4 (a byte tensor's buffer holds whole 32-bit words, as the reference's
 GpuKernelBuffers.PaddedBoolLength requires, and at most 2^31 - 1 elements; its last block holds 4092), each checked
-against the oracle over every element. The inputs repeat a short pattern whose period (4099) does not divide the
+against the oracle over every element; and a product and a gather whose output or table reaches the boundary's
+element limit, against closed forms. The inputs repeat a short pattern whose period (4099) does not divide the
 block, so they are cheap to make; the extreme values of x sit at its first and last elements, in the first and the
 last workgroup."""
 from __future__ import annotations
@@ -117,4 +118,29 @@ def test_product_at_the_largest_output():
         want = (k * row[:, None] * col[None, :]).astype(np.int32)
         bad += int(np.count_nonzero(got[r0 * n:(r0 + 1024) * n].reshape(1024, n) != want))
     say(f"ROW product at the largest output | {kernel} | mismatching elements {bad}")
+    assert bad == 0
+
+
+def test_gather_from_a_table_past_4_gib():
+    # An int32 table of 524287 rows x 4096 (8 GiB, just under 2^31 elements): its last rows start past 2^32 bytes.
+    # Element j of row r holds r * 4096 + j, so each gathered row names the row it came from; negative indices count
+    # from the end.
+    d = device()
+    k = og.GatherKernels(d)
+    rows, inner = 524287, 4096
+    say(f"gather from a table of {rows} x {inner} int32")
+    data = np.arange(rows * inner, dtype=np.int32)
+    idx = np.array([rows - 1, -1, 0, 262144, rows - 2, -rows, 524000, 7], np.int64)
+    bd, bi = d.CreateBuffer(data), d.CreateBuffer(idx)
+    del data
+    bo = d.CreateBuffer(np.full(idx.size * inner, -999, np.int32))
+    status = og.GpuIndexStatus(d)
+    run(d, lambda e: k.EncodeGather(e, bd, 0, [rows, inner], 0, bi, 0, int(idx.size), bo, 0, status))
+    status.ThrowIfFailed()
+    kernel = d.LastKernel
+    got = bo.Read().reshape(idx.size, inner)
+    row = np.where(idx < 0, idx + rows, idx)
+    want = (row[:, None] * inner + np.arange(inner)[None, :]).astype(np.int32)
+    bad = int(np.count_nonzero(got != want))
+    say(f"ROW gather past 4 GiB | {kernel} | mismatching elements {bad}")
     assert bad == 0
