@@ -112,6 +112,19 @@ void GpuCommandEncoder::Record(Command c, std::vector<std::shared_ptr<GpuBuffer:
     commands_.push_back(Entry{std::move(c), std::move(keep), nullptr});
 }
 
+void GpuCommandEncoder::RecordHost(Command c)
+{
+    if (submitted_) throw GpuException("GpuCommandEncoder: already submitted");
+    commands_.push_back(Entry{std::move(c), {}, nullptr, true});
+}
+
+int GpuCommandEncoder::DispatchCount() const
+{
+    int n = 0;
+    for (const Entry &e : commands_) n += e.host ? 0 : 1;
+    return n;
+}
+
 void GpuCommandEncoder::RecordDequant(DequantCommand c, std::vector<std::shared_ptr<GpuBuffer::Impl>> keep)
 {
     if (submitted_) throw GpuException("GpuCommandEncoder: already submitted");
@@ -249,7 +262,12 @@ void GpuDevice::Submit(GpuCommandEncoder &encoder)
     if (encoder.submitted_) throw GpuException("GpuDevice.Submit: encoder already submitted");
     encoder.submitted_ = true;
     if (encoder.commands_.empty()) return;
-    if (!ctx_) throw GpuUnsupportedException("GpuDevice.Submit: a host-only device cannot run work", "Device", "a HIP device", "none");
+    if (!ctx_) {
+        if (encoder.DispatchCount() > 0)
+            throw GpuUnsupportedException("GpuDevice.Submit: a host-only device cannot run work", "Device", "a HIP device", "none");
+        for (const auto &c : encoder.commands_) c.run(nullptr);   // host steps only
+        return;
+    }
     timed_ = 0;
     const int start = encoder.timing_start_, stop = encoder.timing_stop_, n = (int)encoder.commands_.size();
     const auto &cmds = encoder.commands_;
@@ -584,7 +602,12 @@ void Int8Gemm::FloatProduct(GpuCommandEncoder &encoder, const Int8GemmProblem &p
         if (floatBias->Buffer.Valid()) RequireType(kGemm, floatBias->Buffer, ElementType::Float32, "floatBias");
         CheckVector("floatBias", floatBias->Buffer, floatBias->Offset, true, problem.N);
     }
-    if (!prep.Ok) return;
+    if (!prep.Ok) {
+        // An empty ranged product stores nothing and records no pairs: from its place in the submission on, its count
+        // reads 0 (a host step, not a dispatch).
+        if (ranges) encoder.RecordHost([groups = ranges->Groups](og_ctx *) { *groups = 0; });
+        return;
+    }
     Epilogue epi;
     epi.Flags = OG_EPI_FLOAT | (scale.IsVector ? OG_EPI_SCALE_PER_COL : 0u);
     if (intBias) {

@@ -134,7 +134,9 @@ public:
     using Command = std::function<void(og_ctx *)>;
     void Record(Command c, std::vector<std::shared_ptr<GpuBuffer::Impl>> keep);
     void RecordDequant(DequantCommand c, std::vector<std::shared_ptr<GpuBuffer::Impl>> keep);
-    int DispatchCount() const { return (int)commands_.size(); }
+    // A host step that runs in its place at Submit: no dispatch, nothing launched (an empty ranged product's count).
+    void RecordHost(Command c);
+    int DispatchCount() const;
     // Per-dispatch timing of the commands recorded between the two calls (Resources.cs:216-222).
     void BeginPassTiming(int max_passes);
     int EndPassTiming();
@@ -145,6 +147,7 @@ private:
         Command run;
         std::vector<std::shared_ptr<GpuBuffer::Impl>> keep;
         std::shared_ptr<const DequantCommand> dq;   // set for a DequantizeLinear pass
+        bool host = false;                          // a host step (RecordHost)
     };
     std::vector<Entry> commands_;
     int timing_start_ = -1;  // first timed command

@@ -79,6 +79,14 @@ def test_int8_gemm_bad_arguments_are_rejected(d):
     assert enc.DispatchCount == 1
     with pytest.raises(og.GpuUnsupportedException):
         d.Submit(enc)
+    # An empty ranged product records a host step (its count reads 0 from there on), not a dispatch: a host-only
+    # device runs it.
+    ranges = og.Int8Ranges(buf(d, og.ElementType.Float32, 2 * og.OG_RANGES_MAX))
+    enc = d.BeginCommands()
+    gemm.EncodeFloatRanged(enc, P(0, 8, 2), a, b, f, og.Int8Operand(fl, 0), ranges)
+    assert enc.DispatchCount == 0
+    d.Submit(enc)
+    assert ranges.Groups == 0
 
 
 def test_scratch_that_is_too_small_is_refused(d):

@@ -858,6 +858,52 @@ def test_large_k_corrections_are_bit_exact(case):
         assert bad == 0
 
 
+@pytest.mark.parametrize("config", ["default", "portable", "large tile"])
+def test_empty_products_launch_nothing(config):
+    # M = 0 or N = 0 (K any): every product form records nothing that runs and leaves its output alone (the
+    # reference's Prepare returns Ok = false for these and records nothing); a ranged product counts no pairs from its
+    # place in the submission on, also after a full ranged product into the same ranges.
+    d = device()
+    gemm = og.Int8Gemm(d, og.Int8GemmOptions(**CONFIG_OPTIONS[config]))
+    fused = og.Int8Gemm(d, og.Int8GemmOptions(**CONFIG_OPTIONS[config], FusedRequantize=True))
+    ranges = og.Int8Ranges(d.CreateBufferOf(og.ElementType.Float32, 2 * og.OG_RANGES_MAX))
+    a = d.CreateBuffer(np.full(64 * 4096, 7, np.uint8))
+    b = d.CreateBuffer(np.full(4096 * 64, 3, np.int8))
+    scale = d.CreateBuffer(np.full(64, 0.5, np.float32))
+    zb = d.CreateBuffer(np.zeros(64, np.int8))
+    f64 = d.CreateBufferOf(og.ElementType.Float32, 64 * 64)
+    for m, n, k in ((0, 64, 64), (64, 0, 64), (0, 0, 0), (0, 64, 4096), (3, 0, 4096)):
+        say(f"empty [{config}] {m}x{n}x{k}")
+        run(d, lambda e: gemm.EncodeFloatRanged(e, og.Int8GemmProblem(64, 64, 64), a, b, f64, og.Int8Operand(scale, 0, True),
+                                                ranges))
+        assert ranges.Groups >= 1
+        c = d.CreateBuffer(np.full(16, 0x5A5A5A5A, np.int32))
+        f = d.CreateBuffer(np.full(16, -77.0, np.float32))
+        y = d.CreateBuffer(np.full(16, 0xA7, np.uint8))
+        p = og.Int8GemmProblem(m, n, k)
+        e = d.BeginCommands()
+        e.BeginPassTiming(8)
+        gemm.EncodeInt32(e, p, a, b, c, None, og.Int8Operand(zb, 0, True))
+        gemm.EncodeFloat(e, p, a, b, f, og.Int8Operand(scale, 0, True))
+        gemm.EncodeFloatRanged(e, p, a, b, f, og.Int8Operand(scale, 0, True), ranges)
+        for g in (gemm, fused):
+            g.EncodeRequantized(e, p, a, b, y, og.Int8Operand(scale, 0, True), 3)
+        e.EndPassTiming()
+        d.Submit(e)
+        d.WaitIdle()
+        assert d.ReadPassTimes() == [], "an empty product launched a kernel"
+        assert ranges.Groups == 0, "an empty ranged product after a full one leaves no pairs counted"
+        # In the other order, in one submission, the full product's pairs are the ones counted.
+        e = d.BeginCommands()
+        gemm.EncodeFloatRanged(e, p, a, b, f, og.Int8Operand(scale, 0, True), ranges)
+        gemm.EncodeFloatRanged(e, og.Int8GemmProblem(64, 64, 64), a, b, f64, og.Int8Operand(scale, 0, True), ranges)
+        d.Submit(e)
+        d.WaitIdle()
+        assert ranges.Groups >= 1
+        assert c.Read().tolist() == [0x5A5A5A5A] * 16 and f.Read().tolist() == [-77.0] * 16
+        assert y.Read().tolist() == [0xA7] * 16
+
+
 def test_stream_tiles_reads_b_and_writes_nothing():
     # og_util_stream_tiles, the streaming floor the few-rows product is measured against: it runs as "stream-tiles"
     # over configuration 3's B and over a ragged shape, and leaves the sink alone (an all-zero B has checksum 0).
