@@ -1,6 +1,6 @@
 """The device lifecycle through the C ABI, after DeviceCycleTests.cs, ConcurrentDeviceTests.cs and MultiDeviceTests.cs
 on one GPU: contexts created, used and destroyed many times in a row, by eight threads at once, and two contexts of
-one thread used in turn. Every use allocates its own buffers, runs the closed-form product of MultiDeviceTests.cs:30-55
+one thread used in turn; and four contexts running the one-launch few-rows product at once. Every use allocates its own buffers, runs the closed-form product of MultiDeviceTests.cs:30-55
 ([[1, 2], [3, 4]] x [[1, -1, 2], [-2, 3, -3]] = [[-3, 5, -4], [-5, 9, -6]]) and a larger seeded one on the MFMA
 kernel, and checks both."""
 from __future__ import annotations
@@ -138,3 +138,67 @@ def test_two_contexts_of_one_thread_in_turn():
         if c1 is not None:
             L.og_destroy(c1)
         L.og_destroy(c2)
+
+
+def test_one_launch_few_row_products_on_four_contexts_at_once():
+    # Four threads, each with its own context (stream, workspace and count words), run the one-launch few-rows product
+    # (its column slabs' parts handed over inside one XCD) back to back while the others do the same: every product
+    # exact, every og_sync clean, so no context's hand-off sees another's parts or words.
+    L = _lib()
+    m, n, k = 4, 4096, 4096
+    L.og_last_kernel.restype = ctypes.c_char_p
+    rng = np.random.default_rng(77)
+    data = []
+    for t in range(4):
+        a = rng.integers(0, 256, m * k, dtype=np.uint8)
+        b = rng.integers(-128, 128, k * n, dtype=np.int8)
+        za = np.array([rng.integers(0, 256), 0, 0, 0], np.uint8)
+        data.append((a, b, za, oracle.int8_gemm(oracle.Gemm(m, n, k), a, False, b, True, (za[:1], False, 0))))
+    errors: list[str] = []
+    lock = threading.Lock()
+
+    def worker(t: int) -> None:
+        a, b, za, want = data[t]
+        ctx = ctypes.c_void_p()
+        if L.og_init(0, ctypes.byref(ctx)) != 0:
+            with lock:
+                errors.append(f"thread {t}: og_init failed")
+            return
+        ptrs = []
+        try:
+            host = [a, b, za, np.zeros(m * n, np.int32)]
+            for h in host:
+                p = ctypes.c_void_p()
+                assert L.og_alloc(ctx, h.nbytes, ctypes.byref(p)) == 0
+                ptrs.append(p)
+                assert L.og_memcpy_h2d(ctx, p, h.ctypes.data, h.nbytes) == 0
+            buf = [L.Buf(p.value, h.nbytes) for p, h in zip(ptrs, host)]
+            none = L.Buf(None, 0)
+            prm = L.GemmParams(M=m, N=n, K=k, Flags=0x002 | 0x008)   # B int8; A's zero point (scalar)
+            got = np.zeros(m * n, np.int32)
+            for i in range(25):
+                st = L.og_int8_gemm(ctx, ctypes.byref(prm), 1, buf[0], buf[1], buf[3], buf[2], none, none, none, none)
+                kernel = L.og_last_kernel(ctx).decode()
+                if st != 0 or kernel != "mfma-i8-rows16-xcd":
+                    raise RuntimeError(f"status {st}, kernel {kernel}")
+                if L.og_memcpy_d2h(ctx, got.ctypes.data, ptrs[3], got.nbytes) != 0 or L.og_sync(ctx) != 0:
+                    raise RuntimeError(f"sync: {L.og_last_error(ctx).decode()}")
+                bad = int(np.count_nonzero(got != want))
+                if bad:
+                    raise RuntimeError(f"iteration {i}: {bad} wrong sums")
+        except Exception as ex:   # noqa: BLE001 - reported below with the thread
+            with lock:
+                errors.append(f"thread {t}: {ex}")
+        finally:
+            for p in ptrs:
+                L.og_free(ctx, p)
+            L.og_destroy(ctx)
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(4)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=100)
+    assert not any(th.is_alive() for th in threads), "a thread did not finish"
+    assert errors == [], errors
+    say("ROW lifecycle: 4 contexts at once x 25 one-launch few-rows products, every product exact, every sync clean")
