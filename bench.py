@@ -172,10 +172,11 @@ def c4_square(d, steps, warmup, check=True, constant=False, trans_b=False, plain
     return res
 
 
-def c3_gemv(d, m, steps, warmup, copies=9, check=True, n=11008):
+def c3_gemv(d, m, steps, warmup, copies=9, check=True, n=11008, opts=None):
     """Configuration 3: A = DynamicQuantizeLinear(N(0,1) [m x 4096]); B int8 [4096 x n] symmetric per column
     (N(0, 0.02)); MatMulIntegerToFloat with scale = actScale * wScale[n]. `copies` weight matrices rotate. n = 1376 is
-    one GPU's share of an 8-way column split of configuration 3's weights."""
+    one GPU's share of an 8-way column split of configuration 3's weights. `opts`: Int8GemmOptions fields (the
+    two-launch few-rows form: FewRowsOneLaunch=False)."""
     K, N = 4096, n
     x = synth(d, og.ElementType.Float32, m * K, 3, 10, 0.0, 1.0, 2)
     ya = d.CreateBufferOf(og.ElementType.UInt8, m * K)
@@ -191,7 +192,7 @@ def c3_gemv(d, m, steps, warmup, copies=9, check=True, n=11008):
         _ok(_abi().og_util_scale_product(d.Context, _b(s), _b(wscale), N, _b(sc)), d)
         ws.append((q, sc))
     c = d.CreateBufferOf(og.ElementType.Float32, m * N)
-    gemm = og.Int8Gemm(d)
+    gemm = og.Int8Gemm(d, og.Int8GemmOptions(**(opts or {})))
     p = og.Int8GemmProblem(m, N, K)
     zpa = og.Int8Operand(z, 0)
     wall, region, times = timed(d, lambda e, i: gemm.EncodeFloat(e, p, ya, ws[i % copies][0], c,
@@ -775,6 +776,8 @@ def only(d, name, steps, warmup):
         r.pop("host_operands", None)
     elif name == "gemvshard":
         r = c3_gemv(d, 1, steps, warmup, copies=48, check=False, n=1376)
+    elif name.startswith("gemv") and name.endswith("tiles"):
+        r = c3_gemv(d, int(name[4:-5] or 1), steps, warmup, check=False, opts={"FewRowsOneLaunch": False})
     elif name.startswith("gemv"):
         r = c3_gemv(d, int(name[4:] or 1), steps, warmup, check=False)
     elif name == "c2":
@@ -814,7 +817,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline configuration only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["c4", "c4const", "c4nt", "c4plain", "c4plainnt", "gemv1", "gemv4", "gemv16", "gemvshard", "c2", "c2ffn", "c2ffn2", "c2q", "c2q2", "c5", "c5chain", "dequant", "quant", "dq", "gather4096", "gather65536", "resnet50", "whisper", "depthwise", "copy", "stream", "vendor"],
+    ap.add_argument("--only", choices=["c4", "c4const", "c4nt", "c4plain", "c4plainnt", "gemv1", "gemv4", "gemv16", "gemvshard", "gemv1tiles", "gemv16tiles", "c2", "c2ffn", "c2ffn2", "c2q", "c2q2", "c5", "c5chain", "dequant", "quant", "dq", "gather4096", "gather65536", "resnet50", "whisper", "depthwise", "copy", "stream", "vendor"],
                     help="run one workload alone and print its summary (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
